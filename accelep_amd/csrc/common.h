@@ -1,0 +1,129 @@
+// Internal declarations shared by the host files (compiled with g++) and the kernel
+// files (compiled with hipcc) of libaccel_hip.so. Not installed.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "accel_hip.h"
+
+namespace accel_hip {
+
+// Thrown inside the library, turned into a status code at the C-ABI edge.
+struct Error {
+  int code;
+  std::string message;
+};
+
+[[noreturn]] void Fail(int code, const std::string& message);
+void Check(hipError_t status, const char* what);
+
+struct Context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string arch;
+  int cu_count = 0;
+  // Scratch for split-K partial sums. Grown on demand (the stream is drained first).
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+};
+
+// Initialises GPU 0 and the stream on first use.
+Context& Ctx();
+// Ensures workspace >= bytes; returns the context.
+Context& Scratch(size_t bytes);
+// Library-owned device temporaries, one per purpose, grown on demand (the stream is
+// drained before a buffer is replaced). Distinct from the split-K workspace.
+enum TempSlot { kTempDequantA = 0, kTempDequantB = 1, kTempFlags = 2, kTempCount = 3 };
+void* Temp(TempSlot slot, size_t bytes);
+
+// Stats of include/accel/runtime.h (AcceleratorStats) and the packed-GEMM probes.
+void NoteKernelMatmul();
+void NotePackedCall(int64_t k);
+void NoteBytesToDevice(size_t bytes);
+void NoteBytesToHost(size_t bytes);
+
+// ---- operand descriptions handed to the kernel launchers ------------------------------
+
+// How the scale (and zero) index of element (row r, col c) of an int8 matrix view is found.
+enum ScaleMode : int32_t { kScaleConst = 0, kScalePerCol = 1, kScalePerRow = 2 };
+
+struct Q8View {
+  const int8_t* q = nullptr;  // element (0, 0) of this matrix (plane.q + plane.offset)
+  const float* scale = nullptr;
+  const int8_t* zero = nullptr;  // nullptr: zero point 0
+  int32_t mode = kScaleConst;
+  int64_t const_index = 0;        // scale/zero index in kScaleConst mode
+  const int8_t* tiled = nullptr;  // staged column-tiled copy of q (kGemvTileCols wide), or nullptr
+};
+
+// ---- weight staging (staging.cc) --------------------------------------------------------
+// Width of the column tiles of a staged int8 matrix: tile t holds columns [64t, 64t + 64)
+// of every row, k x 64 bytes contiguous (columns past n are zero).
+constexpr int64_t kGemvTileCols = 64;
+// The staged copy of the [k, n] int8 matrix at q, built on first use; nullptr when q is not
+// inside a live allocation of this library (then the raw layout is read).
+const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);
+// Every write into device memory through this library calls this for the written range;
+// staged copies of that allocation are dropped.
+void NoteDeviceWrite(const void* ptr, size_t bytes);
+// Heap hooks (context.cc): the allocation containing ptr; false if none.
+bool FindAllocation(const void* ptr, uint64_t* id, const char** base, size_t* bytes);
+void DropStagedForAllocation(uint64_t id);
+void LaunchTileColumns(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
+
+struct Epilogue {
+  float alpha = 1.f;
+  float beta = 1.f;
+  const float* bias = nullptr;
+  int32_t bias_rank = 0;
+  int64_t bias_shape[2] = {1, 1};
+  int32_t activation = ACCEL_HIP_ACT_NONE;
+  const float* residual = nullptr;
+  const float* rms_weight = nullptr;
+  float rms_eps = 0.f;
+  float* rms_out = nullptr;
+  // True when only alpha*acc with alpha == 1 and nothing else applies.
+  bool Identity() const {
+    return alpha == 1.f && bias == nullptr && activation == ACCEL_HIP_ACT_NONE && residual == nullptr &&
+           rms_weight == nullptr;
+  }
+};
+
+// ---- kernel launchers (defined in *.hip) ----------------------------------------------
+
+// C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV).
+void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
+                  hipStream_t stream);
+// C[m, n] = A[m, k] @ B[k, n]; B is fp32 (b) or int8 (bq.q != nullptr). fp32 MFMA.
+void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
+                   const Epilogue& epi, hipStream_t stream);
+// partials [splits][m][n] -> C: sum in split order, times the column scale of `mode`
+// (none when scale is null or mode is per-row), then the epilogue.
+void LaunchSplitReduce(const float* partials, int32_t splits, int64_t m, int64_t n, float* c, int32_t mode,
+                       const float* scale, int64_t const_index, const Epilogue& epi, hipStream_t stream);
+// Generic dequantization of `count` elements starting at plane.offset into out (fp32).
+void LaunchDequantize(const AccelHipQuantPlane& plane, int64_t count, float* out, hipStream_t stream);
+void LaunchFill(float* dst, float value, int64_t count, hipStream_t stream);
+void LaunchEpilogueInPlace(float* c, int64_t m, int64_t n, const Epilogue& epi, hipStream_t stream);
+void LaunchRmsNormRows(const float* x, const float* weight, float* y, int64_t rows, int64_t dim, float eps,
+                       hipStream_t stream);
+void LaunchTranspose(const float* src, float* dst, int64_t rows, int64_t cols, hipStream_t stream);
+void LaunchResidualAdd(float* dest, const float* extra, int64_t count, hipStream_t stream);
+void LaunchSiluMul(float* gate, const float* up, int64_t count, hipStream_t stream);
+// Writes 1 into *bad if any id is out of range (the output rows of good ids are written).
+void LaunchEmbedding(const int32_t* ids, const float* table, const int8_t* qtable, const float* row_scale, float* out,
+                     int64_t seq, int64_t hidden, int64_t vocab, int32_t* bad, hipStream_t stream);
+void LaunchRope(float* states, const float* cos_table, const float* sin_table, int64_t seq, int64_t heads,
+                int64_t head_dim, int64_t position, hipStream_t stream);
+void LaunchCopy(void* dst, const void* src, size_t bytes, hipStream_t stream);
+void LaunchAttention(const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position,
+                     int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream);
+// rng_inout is a device word holding the xorshift32 state.
+void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
+                       int32_t top_k, hipStream_t stream);
+
+}  // namespace accel_hip

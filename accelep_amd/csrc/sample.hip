@@ -1,0 +1,275 @@
+// SampleToken (SimSampleToken, src/sim_sample.cc:25-115) on one workgroup, logits in HBM.
+//
+//  * temperature <= 0 (or NaN): argmax, the earliest id wins a tie; a NaN at id 0 gives 0,
+//    later NaNs never win (the reference's strict > scan).
+//  * top_k in (0, vocab): the table holds the min(top_k, 64) largest logits, equal logits
+//    resolved toward smaller ids (what the reference's replace-the-worst scan keeps), in
+//    id order. The table is found by a radix select on an order-preserving key and an
+//    id-ordered compaction; the draw over it then runs on one lane in the reference's
+//    order (double exp, cumulative sum, first sum >= draw).
+//  * otherwise the whole vocabulary: max, double sum and the cumulative search are block
+//    reductions/scans over contiguous id ranges (same result up to double rounding).
+// The xorshift32 state is read from and written back to a device word; it advances only
+// when a draw happens (sum > 0), as in the reference.
+#include "device_common.h"
+
+namespace accel_hip {
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ uint32_t OrderKey(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint32_t XorShift32(uint32_t x) {
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  return x;
+}
+
+template <class T>
+__device__ T BlockSum(T v, T* scratch) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  T total = scratch[0];
+  for (int w = 1; w < kWaves; ++w) total += scratch[w];
+  return total;
+}
+
+// Exclusive prefix over threads of a per-thread value (thread order == id order).
+template <class T>
+__device__ T BlockExclusiveScan(T v, T* scratch, T* total_out) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  T inc = v;
+  for (int off = 1; off < 64; off <<= 1) {
+    const T other = __shfl_up(inc, off);
+    if (lane >= off) inc += other;
+  }
+  __syncthreads();
+  if (lane == 63) scratch[wave] = inc;
+  __syncthreads();
+  T base = 0;
+  for (int w = 0; w < wave; ++w) base += scratch[w];
+  T total = 0;
+  for (int w = 0; w < kWaves; ++w) total += scratch[w];
+  *total_out = total;
+  return base + inc - v;
+}
+
+struct Best {
+  float v;
+  int64_t i;  // -1: no candidate
+};
+
+__device__ __forceinline__ Best Better(Best a, Best b) {
+  if (a.i < 0) return b;
+  if (b.i < 0) return a;
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+__device__ Best BlockArgmax(Best b, float* sv, int64_t* si) {
+  for (int off = 32; off > 0; off >>= 1) {
+    Best o;
+    o.v = __shfl_xor(b.v, off);
+    o.i = __shfl_xor(b.i, off);
+    b = Better(b, o);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = b.v;
+    si[threadIdx.x >> 6] = b.i;
+  }
+  __syncthreads();
+  Best r{sv[0], si[0]};
+  for (int w = 1; w < kWaves; ++w) r = Better(r, Best{sv[w], si[w]});
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void SampleKernel(const float* logits, int32_t* chosen, int64_t vocab,
+                                                         float temperature, uint32_t* rng, int32_t top_k) {
+  __shared__ float sv[kWaves];
+  __shared__ int64_t si[kWaves];
+  __shared__ double sd[kWaves];
+  __shared__ uint32_t su[kWaves];
+  __shared__ int64_t table_id[64];
+  __shared__ float table_logit[64];
+  const int tid = threadIdx.x;
+
+  if (!(temperature > 0.f)) {
+    Best b{0.f, -1};
+    for (int64_t i = tid; i < vocab; i += kThreads) {
+      const float v = logits[i];
+      if (!isnan(v)) b = Better(b, Best{v, i});
+    }
+    const Best r = BlockArgmax(b, sv, si);
+    if (tid == 0) *chosen = (isnan(logits[0]) || r.i < 0) ? 0 : static_cast<int32_t>(r.i);
+    return;
+  }
+
+  const bool full = top_k <= 0 || static_cast<int64_t>(top_k) >= vocab;
+  const double inv_t = 1.0 / static_cast<double>(temperature);
+  // Contiguous id range of this thread.
+  const int64_t per = (vocab + kThreads - 1) / kThreads;
+  const int64_t lo = min(vocab, static_cast<int64_t>(tid) * per);
+  const int64_t hi = min(vocab, lo + per);
+
+  if (!full) {
+    const int cap = top_k > 64 ? 64 : top_k;
+    // Radix select: the largest key K with count(key >= K) >= cap.
+    uint32_t prefix = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = prefix | (1u << bit);
+      uint32_t cnt = 0;
+      for (int64_t i = lo; i < hi; ++i) {
+        const float v = logits[i];
+        if (!isnan(v) && OrderKey(v) >= cand) ++cnt;
+      }
+      if (BlockSum<uint32_t>(cnt, su) >= static_cast<uint32_t>(cap)) prefix = cand;
+    }
+    uint32_t gt = 0, eq = 0;
+    for (int64_t i = lo; i < hi; ++i) {
+      const float v = logits[i];
+      if (isnan(v)) continue;
+      const uint32_t key = OrderKey(v);
+      gt += key > prefix;
+      eq += key == prefix;
+    }
+    uint32_t gt_total = 0, eq_total = 0;
+    const uint32_t eq_before = BlockExclusiveScan<uint32_t>(eq, su, &eq_total);
+    uint32_t dummy = 0;
+    const uint32_t gt_all = BlockSum<uint32_t>(gt, su);
+    const uint32_t need = static_cast<uint32_t>(cap) - gt_all;
+    // Selected in this range: all keys > K, and keys == K whose rank among equals < need.
+    uint32_t sel = 0;
+    {
+      uint32_t rank = eq_before;
+      for (int64_t i = lo; i < hi; ++i) {
+        const float v = logits[i];
+        if (isnan(v)) continue;
+        const uint32_t key = OrderKey(v);
+        if (key > prefix) ++sel;
+        else if (key == prefix) {
+          if (rank < need) ++sel;
+          ++rank;
+        }
+      }
+    }
+    (void)gt_total;
+    (void)dummy;
+    uint32_t sel_total = 0;
+    uint32_t pos = BlockExclusiveScan<uint32_t>(sel, su, &sel_total);
+    {
+      uint32_t rank = eq_before;
+      for (int64_t i = lo; i < hi; ++i) {
+        const float v = logits[i];
+        if (isnan(v)) continue;
+        const uint32_t key = OrderKey(v);
+        bool take = key > prefix;
+        if (key == prefix) {
+          take = rank < need;
+          ++rank;
+        }
+        if (take && pos < 64) {
+          table_id[pos] = i;
+          table_logit[pos] = v;
+          ++pos;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int filled = static_cast<int>(sel_total < 64 ? sel_total : 64);
+      float top = table_logit[0];
+      for (int s = 1; s < filled; ++s)
+        if (table_logit[s] > top) top = table_logit[s];
+      double sum = 0.0;
+      for (int s = 0; s < filled; ++s)
+        sum += exp((static_cast<double>(table_logit[s]) - static_cast<double>(top)) * inv_t);
+      if (!(sum > 0.0)) {
+        *chosen = 0;
+        return;
+      }
+      const uint32_t state = XorShift32(*rng);
+      *rng = state;
+      const double draw = (static_cast<double>(state) + 0.5) / 4294967296.0 * sum;
+      double acc = 0.0;
+      for (int s = 0; s < filled; ++s) {
+        acc += exp((static_cast<double>(table_logit[s]) - static_cast<double>(top)) * inv_t);
+        if (acc >= draw) {
+          *chosen = static_cast<int32_t>(table_id[s]);
+          return;
+        }
+      }
+      *chosen = static_cast<int32_t>(table_id[filled - 1]);
+    }
+    return;
+  }
+
+  // Full vocabulary. Max as the reference's scan: start at logits[0], strict >.
+  float local = -INFINITY;
+  bool any = false;
+  for (int64_t i = lo; i < hi; ++i) {
+    const float v = logits[i];
+    if (!isnan(v) && (!any || v > local)) {
+      local = v;
+      any = true;
+    }
+  }
+  Best b{local, any ? 0 : -1};
+  const Best mx = BlockArgmax(b, sv, si);
+  const float top = isnan(logits[0]) ? logits[0] : mx.v;
+  double part = 0.0;
+  for (int64_t i = lo; i < hi; ++i) part += exp((static_cast<double>(logits[i]) - static_cast<double>(top)) * inv_t);
+  double sum = 0.0;
+  const double before = BlockExclusiveScan<double>(part, sd, &sum);
+  __shared__ int64_t pick;
+  __shared__ uint32_t draw_state;
+  __shared__ int drew;
+  if (tid == 0) {
+    pick = vocab - 1;
+    drew = sum > 0.0;
+    if (drew) {
+      draw_state = XorShift32(*rng);
+      *rng = draw_state;
+    }
+  }
+  __syncthreads();
+  if (!drew) {
+    if (tid == 0) *chosen = 0;
+    return;
+  }
+  const double draw = (static_cast<double>(draw_state) + 0.5) / 4294967296.0 * sum;
+  // The first id whose cumulative weight reaches the draw lies in the first range whose
+  // end does.
+  if (before + part >= draw && before < draw + 0.0) {
+    double acc = before;
+    for (int64_t i = lo; i < hi; ++i) {
+      acc += exp((static_cast<double>(logits[i]) - static_cast<double>(top)) * inv_t);
+      if (acc >= draw) {
+        atomicMin(reinterpret_cast<unsigned long long*>(&pick), static_cast<unsigned long long>(i));
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) *chosen = static_cast<int32_t>(pick);
+}
+
+}  // namespace
+
+void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
+                       int32_t top_k, hipStream_t stream) {
+  hipLaunchKernelGGL(SampleKernel, dim3(1), dim3(kThreads), 0, stream, logits, chosen, vocab, temperature, rng_inout,
+                     top_k);
+  Check(hipGetLastError(), "SampleKernel launch");
+}
+
+}  // namespace accel_hip

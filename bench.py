@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the AccelEP hot path on one MI355X: the claimed MatMul on a packed
+constant int8 weight (accel::MatMulQuantized) and its fp32-MFMA forms.
+
+Headline (`value`): the int8-weight decode GEMV, X fp32 [1, 4096] @ W int8 [4096, 14336]
+with a per-column fp32 scale, in algorithmic GB/s. Eight device copies of W (470 MB, more
+than the 256 MB Infinity Cache) are used round robin so every step streams W from HBM.
+A step is one accel_hip_matmul_quantized call; the K timed steps are replayed from a HIP
+graph between two HIP events on the library stream.
+
+Secondary lines (same JSON object, "secondary"): the GEMV at M = 4 and 16, the fp32 MLP
+(Gemm+bias+Gelu, Gemm+bias+residual, fused epilogues) in TFLOP/s, the int8 prefill GEMM
+M=2048 K=4096 N=14336 with fused RMSNormalization in TFLOP/s, and the cache-warm GEMV.
+
+cpu_baseline: the reference's own MatMulQuantized (AccelEP src/sim_device.cc, compiled by
+oracle/Makefile into oracle/_ref) on the same M = 1 workload, single thread on the host.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "int8-W GEMV HBM GB/s + GEMM fp32-MFMA TFLOP/s (% peak); decode tok/s"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+K_DIM, N_DIM = 4096, 14336
+COPIES = 8
+
+
+def gemv_bytes(m, k=K_DIM, n=N_DIM):
+    """Algorithmic HBM bytes of one GEMV: int8 W once, fp32 scale, X read, C written."""
+    return k * n + 4 * n + 4 * m * k + 4 * m * n
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Hip:
+    def __init__(self):
+        from accelep_amd.capi import Epilogue, QuantPlane, check, lib
+        from accelep_amd.device import DeviceArray, quant_plane
+
+        self.L = lib()
+        self.check = check
+        self.Epilogue = Epilogue
+        self.QuantPlane = QuantPlane
+        self.DeviceArray = DeviceArray
+        self.quant_plane = quant_plane
+        check(self.L.accel_hip_init())
+        self.arch = self.L.accel_hip_device_arch().decode()
+
+    def sync(self):
+        self.check(self.L.accel_hip_synchronize())
+
+    def graph(self, fn, count):
+        """Captures `count` calls of fn(i) into one executable graph."""
+        self.check(self.L.accel_hip_capture_begin())
+        try:
+            for i in range(count):
+                fn(i)
+        finally:
+            g = C.c_void_p()
+            self.check(self.L.accel_hip_capture_end(C.byref(g)))
+        return g
+
+    def time_graph(self, graphs_and_reps):
+        """Event-timed replay: list of (graph, reps); returns elapsed ms."""
+        self.sync()
+        self.check(self.L.accel_hip_event_record(0))
+        for g, reps in graphs_and_reps:
+            if reps:
+                self.check(self.L.accel_hip_graph_launch(g, reps))
+        self.check(self.L.accel_hip_event_record(1))
+        ms = self.L.accel_hip_event_elapsed_ms(0, 1)
+        if ms < 0:
+            raise RuntimeError(self.L.accel_hip_last_error().decode())
+        return ms
+
+
+def timed_steps(hip, step, period, steps, warmup):
+    """Warms up, captures `period` steps (and the remainder) into graphs, times exactly `steps`."""
+    # At least one call before capturing: first use may grow the split-K workspace,
+    # which synchronizes and therefore cannot happen inside a capture.
+    for i in range(max(warmup, 1)):
+        step(i)
+    hip.sync()
+    full = hip.graph(step, period)
+    rest = steps % period
+    tail = hip.graph(step, rest) if rest else None
+    plan = [(full, steps // period)] + ([(tail, 1)] if tail else [])
+    ms = hip.time_graph(plan)
+    for g, _ in plan:
+        hip.L.accel_hip_graph_destroy(g)
+    return ms
+
+
+def bench_gemv(hip, m, steps, warmup, copies, rng):
+    """Returns (ms_per_step, GB/s) for the int8 GEMV at this M over `copies` weight copies."""
+    q_host = rng.integers(-127, 128, size=K_DIM * N_DIM, dtype=np.int8)
+    scale = hip.DeviceArray.from_numpy(rng.uniform(1e-3, 1e-2, size=N_DIM).astype(np.float32))
+    weights = [hip.DeviceArray.from_numpy(q_host) for _ in range(copies)]
+    planes = [hip.quant_plane(w, scale, None, [K_DIM, N_DIM], 1) for w in weights]
+    x = hip.DeviceArray.from_numpy(rng.standard_normal((m, K_DIM)).astype(np.float32))
+    out = hip.DeviceArray((m, N_DIM))
+
+    def step(i):
+        hip.check(hip.L.accel_hip_matmul_quantized(x.ptr, None, None, C.byref(planes[i % copies]), out.ptr, m, K_DIM,
+                                                   N_DIM))
+
+    ms = timed_steps(hip, step, copies, steps, warmup)
+    per = ms / steps
+    return per, gemv_bytes(m) / (per * 1e-3) / 1e9
+
+
+def bench_mlp(hip, steps, warmup, rng):
+    """fp32 MLP X[256,1024] -> Gemm(1024x4096)+bias -> Gelu -> Gemm(4096x1024)+bias + X.
+
+    Two fused calls per step (bias+gelu, bias+residual epilogues in registers)."""
+    m, d, h = 256, 1024, 4096
+    x = hip.DeviceArray.from_numpy(rng.standard_normal((m, d)).astype(np.float32))
+    w1 = hip.DeviceArray.from_numpy((rng.standard_normal((d, h)) * 0.02).astype(np.float32))
+    b1 = hip.DeviceArray.from_numpy((rng.standard_normal(h) * 0.02).astype(np.float32))
+    w2 = hip.DeviceArray.from_numpy((rng.standard_normal((h, d)) * 0.02).astype(np.float32))
+    b2 = hip.DeviceArray.from_numpy((rng.standard_normal(d) * 0.02).astype(np.float32))
+    hid = hip.DeviceArray((m, h))
+    y = hip.DeviceArray((m, d))
+    e1 = hip.Epilogue(alpha=1.0, beta=1.0, bias=b1.ptr, bias_rank=1, activation=2)
+    e1.bias_shape[0] = h
+    e2 = hip.Epilogue(alpha=1.0, beta=1.0, bias=b2.ptr, bias_rank=1, activation=0, residual=x.ptr)
+    e2.bias_shape[0] = d
+
+    def step(i):
+        hip.check(hip.L.accel_hip_matmul_fused(x.ptr, w1.ptr, hid.ptr, m, d, h, C.byref(e1)))
+        hip.check(hip.L.accel_hip_matmul_fused(hid.ptr, w2.ptr, y.ptr, m, h, d, C.byref(e2)))
+
+    ms = timed_steps(hip, step, 1, steps, warmup)
+    per = ms / steps
+    flops = 2 * m * d * h * 2
+    return per, flops / (per * 1e-3) / 1e12
+
+
+def bench_prefill(hip, steps, warmup, rng):
+    """int8 prefill GEMM X[2048,4096] @ W int8[4096,14336] (per-column scale) + RMSNormalization
+    (eps 1e-5, gamma ~ N(1, 0.1)) of the output rows, written in place."""
+    m, k, n = 2048, K_DIM, N_DIM
+    q = hip.DeviceArray.from_numpy(rng.integers(-127, 128, size=k * n, dtype=np.int8))
+    scale = hip.DeviceArray.from_numpy(rng.uniform(1e-3, 1e-2, size=n).astype(np.float32))
+    plane = hip.quant_plane(q, scale, None, [k, n], 1)
+    x = hip.DeviceArray.from_numpy(rng.standard_normal((m, k)).astype(np.float32))
+    g = hip.DeviceArray.from_numpy((1 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+    out = hip.DeviceArray((m, n))
+    e = hip.Epilogue(alpha=1.0, beta=1.0, rms_weight=g.ptr, rms_eps=1e-5, rms_out=out.ptr)
+
+    def step(i):
+        hip.check(hip.L.accel_hip_matmul_quantized_fused(x.ptr, None, None, C.byref(plane), out.ptr, m, k, n,
+                                                         C.byref(e)))
+
+    ms = timed_steps(hip, step, 1, steps, warmup)
+    per = ms / steps
+    return per, 2 * m * k * n / (per * 1e-3) / 1e12
+
+
+def cpu_baseline(rng):
+    """The reference's MatMulQuantized (compiled AccelEP sources) on the M=1 headline workload."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ctypes import make_plane, oracle, reference
+
+    ref = reference()
+    kind = "reference" if ref is not None else "port"
+    impl = ref if ref is not None else oracle()
+    q = rng.integers(-127, 128, size=K_DIM * N_DIM, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, size=N_DIM).astype(np.float32)
+    a = rng.standard_normal((1, K_DIM)).astype(np.float32)
+    plane, keep = make_plane(q, s, None, [K_DIM, N_DIM], 1)
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        impl.matmul_quantized(a, None, None, plane, 1, K_DIM, N_DIM)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    return {
+        "value": round(gemv_bytes(1) / best / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"full M=1 workload X[1,4096] @ int8 W[4096,14336] per-column scale, "
+                   f"{'AccelEP MatMulQuantized (src/sim_device.cc:541-602) compiled -O2' if ref else 'oracle port'}, "
+                   f"single thread, best of 2 runs: {best:.2f} s/call; host has {os.cpu_count()} logical CPUs"),
+        "seconds_per_call": round(best, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-headline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the hot path runs on a single MI355X and there is no "
+              f"multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("steps must be >= 1 and warmup >= 0")
+
+    rng = np.random.default_rng(20251201)
+    hip = Hip()
+    log(f"device {hip.arch}")
+
+    per1, gbs1 = bench_gemv(hip, 1, args.steps, args.warmup, COPIES, rng)
+    log(f"gemv M=1 (HBM, {COPIES} copies): {per1 * 1e3:.2f} us/step, {gbs1:.1f} GB/s")
+    secondary = {}
+    if not args.only_headline:
+        for m in (4, 16):
+            per, gbs = bench_gemv(hip, m, args.steps, args.warmup, COPIES, rng)
+            flops = 2 * m * K_DIM * N_DIM
+            secondary[f"gemv_m{m}"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
+                                       "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                       "TFLOP/s": round(flops / (per * 1e-3) / 1e12, 2)}
+            log(f"gemv M={m}: {per * 1e3:.2f} us/step, {gbs:.1f} GB/s")
+        per, gbs = bench_gemv(hip, 1, args.steps, args.warmup, 1, rng)
+        secondary["gemv_m1_cache_warm"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
+                                           "note": "one weight copy, L2/MALL may serve it; not HBM-honest"}
+        steps2 = max(1, args.steps // 4)
+        per, tf = bench_mlp(hip, steps2, max(1, args.warmup // 4), rng)
+        secondary["mlp_fp32"] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
+                                 "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "steps": steps2,
+                                 "config": "X[256,1024] Gemm1024x4096+bias+gelu, Gemm4096x1024+bias+residual"}
+        log(f"mlp fp32: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
+        steps4 = max(1, args.steps // 20)
+        per, tf = bench_prefill(hip, steps4, max(1, args.warmup // 20), rng)
+        secondary["prefill_int8_rmsnorm"] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
+                                             "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "steps": steps4,
+                                             "config": "X[2048,4096] @ int8 W[4096,14336] + RMSNorm(eps 1e-5)"}
+        log(f"prefill int8+rms: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
+        secondary["decode_tok_s"] = None
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (reference MatMulQuantized, 1 thread) ...")
+        cpu = cpu_baseline(np.random.default_rng(7))
+        log(f"cpu baseline: {cpu['value']} GB/s ({cpu['seconds_per_call']} s/call)")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs1, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per1, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "int8-weight decode GEMV: X fp32[1,4096] @ W int8[4096,14336], per-column fp32 scale "
+                        "(accel::MatMulQuantized), 8 weight copies rotated to defeat the 256 MB MALL",
+            "weights": "int8 uniform [-127,127], scale uniform [1e-3,1e-2], X ~ N(0,1)",
+            "parallelism": "1 GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs1, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs1 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "GemvQ8Kernel<4,true,false>",
+            "algorithmic_bytes_per_launch": gemv_bytes(1),
+            "avg_launch_us_event_timed": round(per1 * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

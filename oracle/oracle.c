@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the AccelEP SimDevice hot path. TEST INFRASTRUCTURE ONLY:
- * loaded by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as
- * the checker, never by the product. Build: oracle/Makefile (gcc -O2
+ * loaded by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg to
+ * check results, never by the product. Build: oracle/Makefile (gcc -O2
  * -ffp-contract=off, so no product is ever fused into its add).
  *
  * Every function states the reference behaviour it follows (path:line in the

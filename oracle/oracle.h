@@ -2,7 +2,7 @@
  * CPU oracle for the AccelEP SimDevice hot path. TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
- * this library, and there only as the checker. The product path (accelep_amd/)
+ * this library, and there only to check results. The product path (accelep_amd/)
  * never links or calls it.
  *
  * Each function restates the reference algorithm in plain C, compiled with

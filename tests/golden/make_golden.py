@@ -4,7 +4,7 @@ The outputs come from oracle/_ref/libaccel_ref.so, i.e. AccelEP's own src/*.cc c
 by oracle/Makefile (run `make -C oracle` first, with the reference tree present). The
 fixtures are data only: seeded inputs plus what the reference computed on them. Tests
 check the oracle restatement and the HIP kernels against them where the reference tree
-is absent (the GPU box).
+is absent (a GPU host without the reference sources).
 
 Run: python tests/golden/make_golden.py
 """

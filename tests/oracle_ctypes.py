@@ -1,4 +1,4 @@
-"""ctypes bindings for the CPU checker: oracle/liboracle.so (the C restatement) and
+"""ctypes bindings for the CPU oracle: oracle/liboracle.so (the C restatement) and
 oracle/_ref/libaccel_ref.so (the reference's own sources, compiled; present only where
 the reference tree was available at build time).
 

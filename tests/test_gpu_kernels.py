@@ -1,0 +1,405 @@
+"""Parity of the HIP kernels (through the C-ABI) with the compiled reference's outputs
+(tests/golden/reference_outputs.npz) and the CPU oracle.
+
+Tolerances:
+  * integer/index work (ids, KV rows, gathers, greedy argmax, sampling): bit-exact;
+  * elementwise steps with no transcendental (relu/none epilogues, rope, add, copies):
+    bit-exact;
+  * fp32 matmuls: every element within 2*gamma_K*(|A|@|W|) of the float64 product (Higham's
+    inner-product bound, any summation order), and for K <= 1024 with N(0,1)-scale inputs
+    also numpy allclose(rtol=1e-5, atol=1e-5), the reference's plugin-test tolerance;
+  * erf/exp-based steps (gelu, silu, attention softmax): within a few ulp (stated per test).
+"""
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from golden_cases import (attention_cases, embed_cases, epilogue_cases, quant_cases, rmsnorm_cases, rope_cases,
+                          sample_cases, silu_add_cases)
+from hip_helpers import (Buffer, Epilogue, HipError, DeviceArray, assert_gamma_bound, check, dev, dequant_host, lib,
+                         matmul_quantized, quant_plane, same_bits, stats)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_outputs.npz"
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    check(lib().accel_hip_init())
+    assert lib().accel_hip_device_arch().decode().startswith("gfx950")
+    yield
+
+
+def oracle():
+    from oracle_ctypes import oracle as _o
+
+    return _o()
+
+
+# ---- heap and copies (src/sim_device.cc:133-183) -------------------------------------------
+
+def test_heap_semantics():
+    L = lib()
+    before = L.accel_hip_live_allocs()
+    a = Buffer()
+    check(L.accel_hip_allocate(128, C.byref(a)))
+    b = Buffer()
+    check(L.accel_hip_allocate(0, C.byref(b)))
+    assert a.data and b.data and b.bytes == 0 and b.id > a.id > 0
+    assert L.accel_hip_live_allocs() == before + 2
+    out = np.full(32, 7, np.float32)
+    check(L.accel_hip_copy_d2h(out.ctypes.data, a, 128))
+    assert not out.any()  # zero-filled
+    with pytest.raises(HipError) as e:
+        check(L.accel_hip_copy_d2h(out.ctypes.data, a, 256))
+    assert e.value.kind == "invalid_argument"
+    bogus = Buffer(a.data, a.bytes, a.id + 1000)
+    with pytest.raises(HipError) as e:
+        check(L.accel_hip_free(bogus))
+    assert e.value.kind == "logic_error"
+    check(L.accel_hip_free(Buffer(None, 0, 0)))  # null is a no-op
+    check(L.accel_hip_free(a))
+    check(L.accel_hip_free(b))
+    assert L.accel_hip_live_allocs() == before
+    c = Buffer()
+    check(L.accel_hip_allocate(128, C.byref(c)))
+    assert c.id > b.id  # ids are never reused
+    # A reused block is zero again.
+    check(L.accel_hip_copy_d2h(out.ctypes.data, c, 128))
+    assert not out.any()
+    check(L.accel_hip_free(c))
+
+
+def test_copies_are_counted_and_private():
+    L = lib()
+    L.accel_hip_reset_stats()
+    host = np.arange(4, dtype=np.float32)
+    d = dev(host)
+    host[0] = 99
+    back = d.numpy()
+    assert back.tolist() == [0, 1, 2, 3]
+    s = stats()
+    assert s.bytes_to_device == 16 and s.bytes_to_host == 16
+    d.peek()
+    assert stats().bytes_to_host == 16  # peek is not counted
+
+
+# ---- matmul (src/sim_device.cc:185-196, 387-402) -------------------------------------------
+
+def run_matmul(a, b):
+    m, k = a.shape
+    n = b.shape[1]
+    A, B = dev(a, np.float32), dev(b, np.float32)
+    Cd = dev(np.full((m, n), 5, np.float32))
+    check(lib().accel_hip_matmul(A.buffer, B.buffer, Cd.buffer, m, k, n))
+    return Cd.numpy()
+
+
+def test_matmul_known_answer():
+    assert run_matmul(np.array([[1, 2], [3, 4]]), np.array([[5, 6], [7, 8]])).tolist() == [[19, 22], [43, 50]]
+
+
+def test_matmul_reference_fixtures(gold):
+    for key in [k[:-2] for k in gold if k.startswith("matmul_") and k.endswith("_a")]:
+        a, b = gold[key + "_a"], gold[key + "_b"]
+        got = run_matmul(a, b)
+        assert_gamma_bound(got, a, b)
+        want = gold[key + "_device"]
+        scale = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))
+        assert np.all(np.abs(got - want) <= 1e-5 * np.maximum(scale, 1.0))
+
+
+def test_matmul_probes_and_zero_k():
+    L = lib()
+    L.accel_hip_reset_packed_probes()
+    L.accel_hip_reset_stats()
+    run_matmul(np.ones((3, 7)), np.ones((7, 5)))
+    assert L.accel_hip_packed_matmul_calls() == 1 and L.accel_hip_packed_k_trips() == 7
+    assert stats().kernel_matmuls == 1
+    A = dev(np.zeros(1, np.float32))
+    B = dev(np.zeros(1, np.float32))
+    Cd = dev(np.full((2, 3), 7, np.float32))
+    check(L.accel_hip_matmul(A.buffer, B.buffer, Cd.buffer, 2, 0, 3))
+    assert not Cd.numpy().any()  # k == 0 overwrites C with zeros
+    with pytest.raises(HipError) as e:
+        check(L.accel_hip_matmul(A.buffer, B.buffer, Cd.buffer, 2, 4, 3))
+    assert e.value.kind == "invalid_argument" and "MatMul A is out of range" in e.value.message
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 1024, 4096), (256, 4096, 1024), (77, 300, 129), (1, 576, 49)])
+def test_matmul_against_oracle(m, k, n):
+    r = np.random.default_rng(m * 7 + k)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    b = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
+    got = run_matmul(a, b)
+    assert_gamma_bound(got, a, b)
+    if k <= 1024:
+        np.testing.assert_allclose(got, oracle().reference_matmul(a, b), rtol=1e-5, atol=1e-5)
+
+
+# ---- MatMulQuantized (src/sim_device.cc:541-602) -------------------------------------------
+
+def test_quantized_reference_fixtures(gold):
+    for case in quant_cases():
+        got = matmul_quantized(case)
+        want = gold[f"quant_{case['name']}_out"]
+        if case["k"] == 0:
+            same_bits(got, want)
+            continue
+        if case.get("aq") is not None:
+            a = dequant_host(case["aq"], case["m"], case["k"])
+            w = case["b"]
+        else:
+            a = case["a"]
+            w = dequant_host(case["bq"], case["k"], case["n"])
+        assert_gamma_bound(got, a, w)
+        if case["name"] == "dq_kat":
+            assert got[0, 0] == np.float32(-48.5)
+        if case["name"].startswith("col_"):
+            np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def c3_case(m, k, n, seed, zero=False, axis=1):
+    r = np.random.default_rng(seed)
+    q = r.integers(-127, 128, size=k * n, dtype=np.int8)
+    cnt = n if axis == 1 else k
+    scale = r.uniform(1e-3, 1e-2, size=cnt).astype(np.float32)
+    z = r.integers(-3, 4, size=cnt, dtype=np.int8) if zero else None
+    a = r.standard_normal((m, k)).astype(np.float32)
+    return dict(name="c3", m=m, k=k, n=n, a=a, bq=dict(q=q, scale=scale, zero=z, shape=[k, n], axis=axis, offset=0))
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_gemv_c3_shape(m):
+    """int8 W[4096, 14336], per-column scale: the decode GEMV sweep at full size."""
+    case = c3_case(m, 4096, 14336, 1000 + m)
+    got = matmul_quantized(case)
+    w = dequant_host(case["bq"], 4096, 14336)
+    worst_abs, worst_ratio = assert_gamma_bound(got, case["a"], w)
+    assert worst_ratio < 1.0
+
+
+@pytest.mark.parametrize("m,k,n,zero,axis", [(3, 2048, 4096, True, 1), (5, 1000, 1000, True, 0), (2, 576, 1536, False, 0),
+                                             (9, 333, 77, True, 1)])
+def test_gemv_modes(m, k, n, zero, axis):
+    case = c3_case(m, k, n, 7 * m + k, zero=zero, axis=axis)
+    got = matmul_quantized(case)
+    assert_gamma_bound(got, case["a"], dequant_host(case["bq"], k, n))
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 576, 1536), (64, 4096, 1024), (100, 200, 300), (2048, 576, 192)])
+def test_gemm_int8_panels(m, k, n):
+    """m > 16: fp32 MFMA GEMM with the int8 panel dequantized in LDS."""
+    case = c3_case(m, k, n, 31 * m + n, zero=(m == 100))
+    got = matmul_quantized(case)
+    w = dequant_host(case["bq"], k, n)
+    assert_gamma_bound(got, case["a"], w)
+    if k <= 1024:
+        np.testing.assert_allclose(got, case["a"] @ w, rtol=1e-5, atol=1e-5)
+
+
+def test_staged_weight_follows_rewrites():
+    """The GEMV reads a staged column-tiled copy of W; rewriting W (host copy, or W used as a
+    kernel output) must be seen by the next call."""
+    r = np.random.default_rng(77)
+    m, k, n = 2, 256, 320
+    q1 = r.integers(-127, 128, size=k * n, dtype=np.int8)
+    q2 = r.integers(-127, 128, size=k * n, dtype=np.int8)
+    s = r.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    qd, sd, ad = dev(q1), dev(s), dev(a)
+    plane = quant_plane(qd, sd, None, [k, n], 1)
+    out = dev(np.zeros((m, n), np.float32))
+
+    def run():
+        check(lib().accel_hip_matmul_quantized(ad.ptr, None, None, C.byref(plane), out.ptr, m, k, n))
+        return out.numpy()
+
+    w1 = dequant_host(dict(q=q1, scale=s, zero=None, shape=[k, n], axis=1, offset=0), k, n)
+    w2 = dequant_host(dict(q=q2, scale=s, zero=None, shape=[k, n], axis=1, offset=0), k, n)
+    assert_gamma_bound(run(), a, w1)
+    assert_gamma_bound(run(), a, w1)  # second call reads the staged copy
+    qd.upload(q2)
+    assert_gamma_bound(run(), a, w2)
+    # W's allocation overwritten by a kernel output (residual add over its bytes as floats).
+    zeros = dev(np.zeros(k * n // 4, np.float32))
+    check(lib().accel_hip_residual_add(qd.buffer, zeros.buffer, k * n // 4))  # adds 0.0: bytes of q2 kept
+    qd.upload(q1)
+    assert_gamma_bound(run(), a, w1)
+
+
+def test_quantized_errors_and_counters():
+    L = lib()
+    L.accel_hip_reset_stats()
+    L.accel_hip_reset_packed_probes()
+    case = c3_case(2, 64, 32, 5)
+    matmul_quantized(case)
+    assert stats().kernel_matmuls == 1 and L.accel_hip_packed_k_trips() == 64
+    with pytest.raises(HipError) as e:
+        check(L.accel_hip_matmul_quantized(None, None, None, None, None, 2, 3, 4))
+    assert e.value.kind == "invalid_argument"
+
+
+# ---- fused epilogue -------------------------------------------------------------------------
+
+def test_fused_epilogue_matches_composed_oracle():
+    o = oracle()
+    r = np.random.default_rng(44)
+    m, k, n = 8, 512, 384
+    case = c3_case(m, k, n, 45)
+    bias = r.standard_normal(n).astype(np.float32)
+    resid = r.standard_normal((m, n)).astype(np.float32)
+    bias_d = dev(bias)
+    res_d = dev(resid)
+    for act in (0, 1, 2):
+        e = Epilogue(alpha=1.5, beta=0.5, bias=bias_d.ptr, bias_rank=1, activation=act, residual=res_d.ptr)
+        e.bias_shape[0] = n
+        got = matmul_quantized(case, e)
+        w = dequant_host(case["bq"], k, n)
+        base = o.reference_matmul(case["a"], w)
+        want = o.gemm_epilogue(base, 1.5, bias, [n], 0.5, act) + resid
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
+def test_fused_rmsnorm_epilogue():
+    r = np.random.default_rng(46)
+    m, k, n = 12, 256, 1000
+    case = c3_case(m, k, n, 47)
+    gamma_w = (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+    g_d = dev(gamma_w)
+    out = dev(np.zeros((m, n), np.float32))
+    e = Epilogue(alpha=1.0, beta=1.0, rms_weight=g_d.ptr, rms_eps=1e-5, rms_out=out.ptr)
+    c = matmul_quantized(case, e)
+    y = out.numpy()
+    want = oracle().rmsnorm(c, gamma_w, m, n, 1e-5)  # normalizes the stored C rows
+    np.testing.assert_allclose(y, want, rtol=1e-6, atol=1e-6)
+
+
+# ---- GemmEpilogue (src/sim_device.cc:211-245) ------------------------------------------------
+
+def test_epilogue_reference_fixtures(gold):
+    L = lib()
+    for case in epilogue_cases():
+        cd = dev(case["c"])
+        m, n = case["c"].shape
+        shape = (C.c_int64 * 2)(*(list(case["bias_shape"]) + [0, 0])[:2])
+        if case["bias"] is not None:
+            bd = dev(case["bias"])
+            check(L.accel_hip_gemm_epilogue(cd.buffer, m, n, case["alpha"], C.byref(bd.buffer), len(case["bias_shape"]),
+                                            shape, case["beta"], case["act"]))
+        else:
+            check(L.accel_hip_gemm_epilogue(cd.buffer, m, n, case["alpha"], None, 0, shape, case["beta"], case["act"]))
+        got = cd.numpy()
+        want = gold[f"epi_{case['name']}_out"]
+        if case["act"] == 2:
+            # Device erff vs glibc erff differ by a few ulp; 1 + erf(x) cancels for negative x,
+            # so the bound is relative to the gelu input scale: |d| <= 1e-6*|want| + 2e-7.
+            fin = np.isfinite(want)
+            assert np.array_equal(np.isnan(got), np.isnan(want))
+            assert np.array_equal(got[~fin & ~np.isnan(want)], want[~fin & ~np.isnan(want)])
+            np.testing.assert_allclose(got[fin], want[fin], rtol=1e-6, atol=2e-7)
+        else:
+            same_bits(got, want)
+
+
+def test_nonfinite_relu_bits():
+    # tests/test_runtime.cc:427-459: inf*0 -> NaN survives relu, -inf -> +0, -1*0 -> -0.
+    L = lib()
+    vals = np.array([np.nan, -np.inf, 0.0], np.float32)
+    cd = dev(vals[None, :])
+    check(L.accel_hip_gemm_epilogue(cd.buffer, 1, 3, -1.0, None, 0, (C.c_int64 * 2)(), 0.0, 1))
+    got = cd.numpy()[0]
+    assert np.isnan(got[0]) and got.view(np.uint32)[1] == 0x7F800000 and got.view(np.uint32)[2] == 0x80000000
+
+
+# ---- named decode kernels --------------------------------------------------------------------
+
+def test_rmsnorm_reference_fixtures(gold):
+    for c in rmsnorm_cases():
+        x = dev(c["x"])
+        w = dev(c["w"])
+        y = dev(np.full((c["rows"], c["dim"]), 42.0, np.float32))
+        check(lib().accel_hip_rms_norm(x.buffer, w.buffer, y.buffer, c["rows"], c["dim"], c["eps"], c["row_offset"]))
+        np.testing.assert_allclose(y.numpy(), gold[f"rms_{c['name']}_out"], rtol=2e-7, atol=1e-7)
+
+
+def test_embedding_reference_fixtures(gold):
+    for c in embed_cases():
+        ids = dev(c["ids"])
+        table = dev(c["table"])
+        out = dev(np.zeros((c["seq"], c["table"].shape[1]), np.float32))
+        rc = lib().accel_hip_embedding(ids.buffer, c["id_offset"], table.buffer, out.buffer, c["seq"],
+                                       c["table"].shape[1], c["table"].shape[0])
+        if int(gold[f"embed_{c['name']}_rc"]) != 0:
+            assert rc == 1 and "outside the vocabulary" in lib().accel_hip_last_error().decode()
+        else:
+            assert rc == 0
+            same_bits(out.numpy(), gold[f"embed_{c['name']}_out"])
+
+
+def test_rope_reference_fixtures(gold):
+    for c in rope_cases():
+        st = dev(c["states"])
+        cs = dev(c["cos"])
+        sn = dev(c["sin"])
+        check(lib().accel_hip_rope(st.buffer, cs.buffer, sn.buffer, c["seq"], c["heads"], c["head_dim"],
+                                   c["position"]))
+        same_bits(st.numpy(), gold[f"rope_{c['name']}_out"])
+
+
+def test_append_cache_exact():
+    src = np.arange(12, dtype=np.float32)
+    cache = dev(np.full(20, -5, np.float32))
+    s = dev(src)
+    check(lib().accel_hip_append_cache(s.buffer, cache.buffer, 2, 1, 2, 3))
+    want = np.full(20, -5, np.float32)
+    want[6:18] = src
+    same_bits(cache.numpy(), want)
+
+
+def test_attention_reference_fixtures(gold):
+    for c in attention_cases():
+        q, k, v = dev(c["q"]), dev(c["k"]), dev(c["v"])
+        total = c["seq"] + c["position"]
+        scores = dev(np.zeros(total, np.float32))
+        out = dev(np.zeros(c["q"].shape, np.float32))
+        check(lib().accel_hip_attention(q.buffer, k.buffer, v.buffer, scores.buffer, out.buffer, c["seq"],
+                                        c["position"], c["heads"], c["kv_heads"], c["head_dim"]))
+        np.testing.assert_allclose(out.numpy(), gold[f"attn_{c['name']}_out"], rtol=1e-5, atol=2e-6)
+
+
+def test_silu_add_reference_fixtures(gold):
+    for c in silu_add_cases():
+        g, u = dev(c["gate"]), dev(c["up"])
+        check(lib().accel_hip_silu_mul(g.buffer, u.buffer, c["gate"].size))
+        np.testing.assert_allclose(g.numpy(), gold[f"silu_{c['name']}_out"], rtol=1e-6, atol=1e-30)
+        d, e = dev(c["gate"]), dev(c["up"])
+        check(lib().accel_hip_residual_add(d.buffer, e.buffer, c["gate"].size))
+        same_bits(d.numpy(), gold[f"add_{c['name']}_out"])
+
+
+def test_sampling_reference_fixtures(gold):
+    ids = []
+    states = []
+    chosen = dev(np.full(3, -1, np.int32))
+    for c in sample_cases():
+        lg = dev(c["logits"])
+        st = C.c_uint32(c["rng"])
+        check(lib().accel_hip_sample_token(lg.buffer, chosen.buffer, 1, c["logits"].size, c["temperature"],
+                                           C.byref(st), c["top_k"]))
+        ids.append(int(chosen.numpy()[1]))
+        states.append(st.value)
+    want_ids = gold["sample_ids"]
+    want_states = gold["sample_rng_after"]
+    mism = [i for i in range(len(ids)) if ids[i] != want_ids[i] or states[i] != want_states[i]]
+    assert not mism, f"{len(mism)} sampling cases differ, first {mism[:5]}"
