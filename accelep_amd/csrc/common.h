@@ -61,9 +61,14 @@ struct Q8View {
 };
 
 // ---- weight staging (staging.cc) --------------------------------------------------------
-// Width of the column tiles of a staged int8 matrix: tile t holds columns [64t, 64t + 64)
-// of every row, k x 64 bytes contiguous (columns past n are zero).
-constexpr int64_t kGemvTileCols = 64;
+// Width of the column tiles of a staged int8 matrix: tile t holds columns [8t, 8t + 8) of
+// rows 0..kp-1 (kp = k rounded up to even), kp x 8 bytes contiguous; columns past n and the
+// pad row are zero.
+constexpr int64_t kGemvTileCols = 8;
+inline size_t StagedTileBytes(int64_t k, int64_t n) {
+  return static_cast<size_t>((n + kGemvTileCols - 1) / kGemvTileCols) * static_cast<size_t>(k + (k & 1)) *
+         static_cast<size_t>(kGemvTileCols);
+}
 // The staged copy of the [k, n] int8 matrix at q, built on first use; nullptr when q is not
 // inside a live allocation of this library (then the raw layout is read).
 const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);

@@ -3,23 +3,23 @@
 //
 // Bound: HBM. Algorithmic bytes per call = k*n (int8 W) + 4*n (scale) + 4*m*k (A) + 4*m*n (C).
 //
-// Both kernels stream W with 16-byte loads (16 int8 columns of one row per lane), convert
-// the bytes to fp32 exactly and let the matrix cores do the multiply-adds. Per-column (or
-// whole-tensor) scale multiplies each finished sum once; a per-row scale is folded into A;
-// zero points are subtracted from the exact integer before the product. Every sum runs in a
-// fixed order, so results are deterministic.
+// Both kernels stream W with 16-byte loads and convert the bytes to fp32 exactly. Per-column
+// (or whole-tensor) scale multiplies each finished sum once; a per-row scale is folded into
+// A; zero points are subtracted from the exact integer before the product. Every sum runs
+// in a fixed order, so results are deterministic.
 //
-// Narrow kernel (m <= 4), the decode path:
-//  * a workgroup (8 waves) owns a 64-column tile over its whole K range, so no workgroup
-//    waits for another; 4 lanes cover one 64-byte row segment and a wave loads 16 rows
-//    (1 KB) per instruction, 8 loads in flight per wave;
-//  * v_mfma_f32_4x4x1_16b_f32: block b of lane l = 4b+j holds row slot b and columns
-//    16j+t (t = byte of the load), A rows 0..3; the 16 row slots are summed with lane
-//    shuffles, the 8 waves through LDS;
-//  * tiles go to XCDs in contiguous runs (workgroup i runs on XCD i % 8), so the two tiles
-//    that share each 128-byte line of W are read through the same L2.
-// Wide kernel (4 < m <= 16): 256-column tiles, 16 lanes per 256-byte row segment, 4 rows per
-// wave load feed v_mfma_f32_16x16x4_f32 as its K = 4; A staged in LDS.
+// Narrow kernel (m <= 4), the decode path, reads a staged copy of W in 8-column tiles (each
+// tile k x 8 bytes, contiguous):
+//  * a workgroup owns one tile over its K range, so no workgroup waits for another; a
+//    4096 x 14336 matrix gives 1792 workgroups of 32 KB each, 7 per CU on 256 CUs;
+//  * lane l loads rows (2l, 2l + 1) of the tile as one 16-byte load, a wave 128 rows (1 KB)
+//    per instruction, and multiplies on the VALU (the product per byte is one conversion and
+//    m fused multiply-adds, below the HBM time for m <= 4);
+//  * the 8 column sums of the 64 lanes are reduce-scattered with lane shuffles, the waves'
+//    sums added through LDS;
+//  * tiles go to XCDs in contiguous runs (workgroup i runs on XCD i % 8).
+// Wide kernel (4 < m <= 16): W in place, 256-column tiles, 16 lanes per 256-byte row segment,
+// 4 rows per wave load feed v_mfma_f32_16x16x4_f32 as its K = 4; A staged in LDS.
 // Split-K (only where the tile count cannot fill the GPU): each split writes its partial
 // sums to the workspace and a second kernel adds them in split order (no inter-workgroup
 // synchronization inside a kernel).
@@ -47,8 +47,9 @@ struct GemvArgs {
   int32_t splits;
   int64_t rows_per_split;
   float* partials;  // [splits][m][n] when splits > 1
-  // Column-tiled copy of W (narrow kernel): 64-column tile t, row r at tiled + (t*k + r)*64,
-  // columns past n zero. nullptr: read W in its [k, n] layout.
+  // Column-tiled copy of W (narrow kernel): 8-column tile t, row r at tiled + (t*kp + r)*8
+  // (kp = k rounded up to even), columns past n and the pad row zero. nullptr: read W in
+  // its [k, n] layout.
   const int8_t* tiled;
   Epilogue epi;
 };
@@ -106,68 +107,151 @@ __device__ __forceinline__ void Emit(const GemvArgs& p, int split, int64_t mm, i
   }
 }
 
-// ---- narrow kernel: m <= 4, staged column tiles -----------------------------------------------
-constexpr int kNarrowWaves = 8;
-constexpr int kNarrowThreads = kNarrowWaves * 64;
-constexpr int kNarrowTile = 64;
-constexpr int kNarrowUnroll = 4;
+// ---- narrow kernel: m <= 4, staged 8-column tiles --------------------------------------------
+// Staged tile t holds columns [8t, 8t + 8) for rows 0..kp-1 (kp = k rounded up to even), byte
+// (r, c) at tiled[(t * kp + r) * 8 + c], zero past n and in the pad row. One workgroup owns
+// one tile (over its split's rows): its bytes are one contiguous run, so the tiles of all
+// workgroups stream W in order. Lane l of the workgroup loads rows (r, r + 1), r = 2l + step,
+// as one 16-byte load (row r in bytes 0..7, row r + 1 in bytes 8..15); A rows are multiplied
+// on the VALU (one conversion and m fused multiply-adds per byte).
+constexpr int kNarrowTile = 8;
 
-// One batch of kNarrowUnroll 16-row loads of one wave, as loaded: no value is inspected
-// until ComputeNarrowBatch, so issuing a batch never waits for memory.
-struct NarrowBatch {
-  uint4 w[kNarrowUnroll];
-  float a[kNarrowUnroll];
-  float s[kNarrowUnroll];   // per-row scale (kRowScale)
-  int8_t z[kNarrowUnroll];  // per-row zero (kZero && kRowScale)
+template <int M>
+struct NarrowShape {
+  static constexpr int kWaves = M == 1 ? 4 : 8;  // waves per workgroup
+  static constexpr int kUnroll = M == 1 ? 8 : 4;  // 16-byte loads per lane per batch
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int64_t kStepRows = kThreads * 2;           // rows one load of the workgroup covers
+  static constexpr int64_t kBatchRows = kStepRows * kUnroll;   // rows of one batch
 };
 
-// kRowScale: the plane's scale (and zero) runs along k; the scale is folded into A.
-// `tbase` is this lane's 16 bytes of row 0 in its tile of the staged copy.
-template <bool kZero, bool kRowScale>
-__device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, int64_t r0, int slot, int64_t ke,
-                                                const int8_t* tbase, int64_t a_row, NarrowBatch& b) {
-  constexpr int64_t kStep = kNarrowWaves * 16;
+// One batch of loads, as loaded: nothing is inspected until ComputeNarrowBatch, so issuing
+// a batch never waits for memory.
+template <int M, int U>
+struct NarrowBatch {
+  u32x4 w[U];
+  float a[U][M][2];
+  float s[U][2];   // per-row scale (kRowScale)
+  int8_t z[U][2];  // per-row zero (kZero && kRowScale)
+};
+
+// Rows past ke are clamped to valid addresses (the W pair to kw - 2, kw = ke rounded up to
+// even, which never passes the staged pad row; A, scale and zero to ke - 1) and are zeroed
+// through A at use, so the loads need no branches. Row indexes are 32-bit: the launcher
+// sends only k < 2^28 here.
+// kPairA: k even and A 8-byte aligned, so (a[r], a[r + 1]) is one aligned 8-byte load.
+// kClamp false: the caller has checked that every row of the batch lies below ke.
+template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
+__device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
+                                                int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
+  using S = NarrowShape<M>;
 #pragma unroll
-  for (int u = 0; u < kNarrowUnroll; ++u) {
-    const int64_t row = r0 + u * kStep + slot;
-    const int64_t rc = row < ke ? row : ke - 1;  // rows past ke re-read a valid row
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tbase + rc * kNarrowTile));
-    b.w[u] = make_uint4(v[0], v[1], v[2], v[3]);
-    b.a[u] = p.a[a_row * p.k + rc];
-    if (kRowScale) b.s[u] = p.scale[rc];
-    if (kZero && kRowScale) b.z[u] = p.zero[rc];
+  for (int u = 0; u < U; ++u) {
+    const int r = r0 + u * static_cast<int>(S::kStepRows);
+    const int rw = !kClamp || r < kw - 2 ? r : kw - 2;
+    b.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u));
+    const int r1 = !kClamp || r < ke - 1 ? r : ke - 1;
+    const int r2 = !kClamp || r + 1 < ke - 1 ? r + 1 : ke - 1;
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      // Offsets as 32-bit values from the uniform row base: one VGPR per address.
+      const char* abase = reinterpret_cast<const char*>(arow[mm]);
+      if (kPairA) {
+        // k is even here, so ke is even and the pair (rp, rp + 1) is whole.
+        const int rp = !kClamp || r < ke - 2 ? r : ke - 2;
+        const float2 v = *reinterpret_cast<const float2*>(abase + static_cast<uint32_t>(rp) * 4u);
+        b.a[u][mm][0] = v.x;
+        b.a[u][mm][1] = v.y;
+      } else {
+        b.a[u][mm][0] = *reinterpret_cast<const float*>(abase + static_cast<uint32_t>(r1) * 4u);
+        b.a[u][mm][1] = *reinterpret_cast<const float*>(abase + static_cast<uint32_t>(r2) * 4u);
+      }
+    }
+    if (kRowScale) {
+      b.s[u][0] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.scale) + static_cast<uint32_t>(r1) * 4u);
+      b.s[u][1] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.scale) + static_cast<uint32_t>(r2) * 4u);
+    }
+    if (kZero && kRowScale) {
+      b.z[u][0] = p.zero[static_cast<uint32_t>(r1)];
+      b.z[u][1] = p.zero[static_cast<uint32_t>(r2)];
+    }
   }
 }
 
-// kValu (m == 1): the product runs on the VALU (one fma per byte); otherwise
-// v_mfma_f32_4x4x1_16b_f32 multiplies A rows 0..3 at once.
-template <bool kZero, bool kRowScale, bool kValu>
-__device__ __forceinline__ void ComputeNarrowBatch(const NarrowBatch& b, int64_t r0, int slot, int64_t ke,
-                                                   bool a_live, const float (&zc)[16], v4f (&acc)[16],
-                                                   float (&accv)[16]) {
-  constexpr int64_t kStep = kNarrowWaves * 16;
+template <int M, int U, bool kZero, bool kRowScale, bool kClamp>
+__device__ __forceinline__ void ComputeNarrowBatch(const NarrowBatch<M, U>& b, int r0, int ke,
+                                                   const float (&zc)[kNarrowTile], float (&acc)[M][kNarrowTile]) {
+  using S = NarrowShape<M>;
 #pragma unroll
-  for (int u = 0; u < kNarrowUnroll; ++u) {
-    const bool valid = r0 + u * kStep + slot < ke;
-    float a = kRowScale ? __fmul_rn(b.a[u], b.s[u]) : b.a[u];
-    a = (valid && a_live) ? a : 0.f;
-    const float zr = (kZero && kRowScale) ? static_cast<float>(b.z[u]) : 0.f;
+  for (int u = 0; u < U; ++u) {
+    const int r = r0 + u * static_cast<int>(S::kStepRows);
+    const bool v0 = !kClamp || r < ke;
+    const bool v1 = !kClamp || r + 1 < ke;
+    float a0[M], a1[M];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      float x = ByteToFloat(Word(b.w[u], t >> 2), t & 3);
-      if (kZero) x = x - (zc[t] + zr);
-      if (kValu) {
-        accv[t] = __builtin_fmaf(a, x, accv[t]);
-      } else {
-        acc[t] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, x, acc[t], 0, 0, 0);
+    for (int mm = 0; mm < M; ++mm) {
+      const float x0 = kRowScale ? __fmul_rn(b.a[u][mm][0], b.s[u][0]) : b.a[u][mm][0];
+      const float x1 = kRowScale ? __fmul_rn(b.a[u][mm][1], b.s[u][1]) : b.a[u][mm][1];
+      a0[mm] = v0 ? x0 : 0.f;
+      a1[mm] = v1 ? x1 : 0.f;
+    }
+    const float z0 = (kZero && kRowScale) ? static_cast<float>(b.z[u][0]) : 0.f;
+    const float z1 = (kZero && kRowScale) ? static_cast<float>(b.z[u][1]) : 0.f;
+#pragma unroll
+    for (int c = 0; c < kNarrowTile; ++c) {
+      float w0 = ByteToFloat(b.w[u][c >> 2], c & 3);
+      float w1 = ByteToFloat(b.w[u][2 + (c >> 2)], c & 3);
+      if (kZero) {
+        w0 = w0 - (zc[c] + z0);
+        w1 = w1 - (zc[c] + z1);
+      }
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        acc[mm][c] = __builtin_fmaf(a0[mm], w0, acc[mm][c]);
+        acc[mm][c] = __builtin_fmaf(a1[mm], w1, acc[mm][c]);
       }
     }
   }
 }
 
-template <bool kZero, bool kRowScale, bool kValu>
-__global__ __launch_bounds__(kNarrowThreads) void GemvNarrowKernel(GemvArgs p) {
-  __shared__ float red[kNarrowWaves][4][kNarrowTile];
+// Sums one value per column over the 64 lanes of a wave: three halving exchanges leave lane l
+// with column (l >> 3) & 7 summed over its 8-lane group, three more finish the sum.
+__device__ __forceinline__ float WaveColumnSum8(const float (&v8)[kNarrowTile], int lane) {
+  const bool h1 = lane & 32, h2 = lane & 16, h3 = lane & 8;
+  float v4[4], v2[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float send = h1 ? v8[i] : v8[i + 4];
+    const float keep = h1 ? v8[i + 4] : v8[i];
+    v4[i] = keep + __shfl_xor(send, 32);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float send = h2 ? v4[i] : v4[i + 2];
+    const float keep = h2 ? v4[i + 2] : v4[i];
+    v2[i] = keep + __shfl_xor(send, 16);
+  }
+  float v = (h3 ? v2[1] : v2[0]) + __shfl_xor(h3 ? v2[0] : v2[1], 8);
+  v = v + __shfl_xor(v, 4);
+  v = v + __shfl_xor(v, 2);
+  v = v + __shfl_xor(v, 1);
+  return v;
+}
+
+// Waves per SIMD the register budget must allow. For m = 1 with a per-column or whole-tensor
+// scale, 7 (<= 72 VGPRs): the 1792 tiles of a 4096 x 14336 matrix put 7 workgroups of 4 waves
+// on each of 256 CUs, all resident at once. Other forms need more registers and take what
+// the compiler gives them (1: no bound).
+template <int M, bool kRowScale>
+constexpr int NarrowMinWaves() {
+  return (M == 1 && !kRowScale) ? 7 : 1;
+}
+
+template <int M, bool kZero, bool kRowScale, bool kPairA>
+__global__ __launch_bounds__(NarrowShape<M>::kThreads)
+__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNarrowKernel(GemvArgs p) {
+  using S = NarrowShape<M>;
+  __shared__ float red[S::kWaves][M][kNarrowTile];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -176,100 +260,84 @@ __global__ __launch_bounds__(kNarrowThreads) void GemvNarrowKernel(GemvArgs p) {
   const int split = blockIdx.y;
   const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
   const int64_t ke = min(p.k, kb + p.rows_per_split);
+  const int64_t kw = ke + (ke & 1);
+  const int64_t kp = p.k + (p.k & 1);
+  const int64_t col0 = static_cast<int64_t>(tile) * kNarrowTile;
 
-  const int slot = lane >> 2;  // row of a 16-row load (MFMA: the block index)
-  const int nj = lane & 3;     // 16-column chunk (MFMA: the block column)
-  const int64_t col = static_cast<int64_t>(tile) * kNarrowTile + nj * 16;
-  // A operand: the VALU form uses row 0 everywhere; the MFMA form feeds row l % 4 from lane l.
-  const bool a_live = kValu || nj < p.m;
-  const int64_t a_row = (kValu || !a_live) ? 0 : nj;
-  float zc[16];
-  ColumnZeros<kZero>(p, col, zc);
-
-  v4f acc[16];
-  float accv[16];
+  float zc[kNarrowTile];
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    accv[t] = 0.f;
-  }
-
-  // Batches of kNarrowUnroll 16-row loads, double buffered: the next batch is in flight
-  // while the current one is multiplied. Rows past ke are clamped to a valid address and
-  // contribute through a zero A operand, so the loads need no branches. The steady-state
-  // loop issues its loads unconditionally (a load inside a branch makes the compiler wait
-  // for every outstanding load where the paths merge); the last batches are peeled, and
-  // sched_barrier keeps the scheduler from sinking the next batch's loads into the current
-  // batch's arithmetic.
-  constexpr int64_t kStep = kNarrowWaves * 16;
-  constexpr int64_t kBatchRows = kStep * kNarrowUnroll;
-  const int8_t* tbase = p.tiled + static_cast<int64_t>(tile) * p.k * kNarrowTile + nj * 16;
-  NarrowBatch bx, by;
-  const int64_t first = kb + wave * 16;
-  const int64_t batches = first < ke ? (ke - first + kBatchRows - 1) / kBatchRows : 0;
-  int64_t r0 = first;
-  if (batches > 0) LoadNarrowBatch<kZero, kRowScale>(p, r0, slot, ke, tbase, a_row, bx);
-  int64_t i = 0;
-  for (; i + 2 < batches; i += 2) {
-    LoadNarrowBatch<kZero, kRowScale>(p, r0 + kBatchRows, slot, ke, tbase, a_row, by);
-    __builtin_amdgcn_sched_barrier(0);
-    ComputeNarrowBatch<kZero, kRowScale, kValu>(bx, r0, slot, ke, a_live, zc, acc, accv);
-    __builtin_amdgcn_sched_barrier(0);
-    LoadNarrowBatch<kZero, kRowScale>(p, r0 + 2 * kBatchRows, slot, ke, tbase, a_row, bx);
-    __builtin_amdgcn_sched_barrier(0);
-    ComputeNarrowBatch<kZero, kRowScale, kValu>(by, r0 + kBatchRows, slot, ke, a_live, zc, acc, accv);
-    __builtin_amdgcn_sched_barrier(0);
-    r0 += 2 * kBatchRows;
-  }
-  if (i + 2 == batches) {
-    LoadNarrowBatch<kZero, kRowScale>(p, r0 + kBatchRows, slot, ke, tbase, a_row, by);
-    ComputeNarrowBatch<kZero, kRowScale, kValu>(bx, r0, slot, ke, a_live, zc, acc, accv);
-    ComputeNarrowBatch<kZero, kRowScale, kValu>(by, r0 + kBatchRows, slot, ke, a_live, zc, acc, accv);
-  } else if (i + 1 == batches) {
-    ComputeNarrowBatch<kZero, kRowScale, kValu>(bx, r0, slot, ke, a_live, zc, acc, accv);
-  }
-
-  // Sum the 16 row slots (lanes 4b + j, b = 0..15) of each live A row; lanes 0..3 then hold
-  // columns 16*lane + t. MFMA block b's VGPR r is A row r.
-  if (kValu) {
+  for (int c = 0; c < kNarrowTile; ++c) zc[c] = 0.f;
+  if (kZero && !kRowScale) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      float v = accv[t];
-      v = v + __shfl_xor(v, 4);
-      v = v + __shfl_xor(v, 8);
-      v = v + __shfl_xor(v, 16);
-      v = v + __shfl_xor(v, 32);
-      acc[t][0] = v;
+    for (int c = 0; c < kNarrowTile; ++c) {
+      const int64_t col = col0 + c < p.n ? col0 + c : p.n - 1;
+      zc[c] = static_cast<float>(p.mode == kScalePerCol ? p.zero[col] : p.zero[p.const_index]);
     }
-  } else {
+  }
+  // The scale of the column this thread may store (c = tid % 8), loaded now so that storing
+  // the sums waits for no memory. Every thread loads (from a clamped, valid index); a per-row
+  // scale was folded into A and is not used here.
+  const int64_t scol = col0 + (tid & 7) < p.n ? col0 + (tid & 7) : p.n - 1;
+  const float col_scale = p.scale[p.mode == kScalePerCol ? scol : (p.mode == kScaleConst ? p.const_index : 0)];
+  float acc[M][kNarrowTile];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (r < p.m) {
+  for (int mm = 0; mm < M; ++mm)
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-          float v = acc[t][r];
-          v = v + __shfl_xor(v, 4);
-          v = v + __shfl_xor(v, 8);
-          v = v + __shfl_xor(v, 16);
-          v = v + __shfl_xor(v, 32);
-          acc[t][r] = v;
-        }
+    for (int c = 0; c < kNarrowTile; ++c) acc[mm][c] = 0.f;
+
+  // One batch in flight per wave: its loads are all issued before any of them is used. A
+  // workgroup holds few registers, so several run per CU and cover each other's waits (a
+  // second buffer would double the registers and halve the workgroups per CU).
+  const int8_t* tbase = p.tiled + static_cast<int64_t>(tile) * kp * kNarrowTile;
+  const float* arow[M];
+#pragma unroll
+  for (int mm = 0; mm < M; ++mm) arow[mm] = p.a + static_cast<int64_t>(mm < p.m ? mm : p.m - 1) * p.k;
+  const int ke32 = static_cast<int>(ke);
+  const int kw32 = static_cast<int>(kw);
+  // Whole batches (every row below ke, a workgroup-uniform test) issue all their loads at
+  // once and skip the clamps and selects. The last, partial batch goes two loads at a time,
+  // so its clamped form does not raise the register count of the kernel (which sets how many
+  // workgroups share a CU). sched_barrier keeps the scheduler from moving conversions between
+  // the loads, which would make each load wait for the one before it.
+  constexpr int kTailUnroll = 2;
+  static_assert(S::kUnroll % kTailUnroll == 0, "tail steps");
+  for (int r0 = static_cast<int>(kb) + 2 * tid; r0 - 2 * tid < ke32; r0 += static_cast<int>(S::kBatchRows)) {
+    if (r0 - 2 * tid + static_cast<int>(S::kBatchRows) <= ke32) {
+      NarrowBatch<M, S::kUnroll> bx;
+      LoadNarrowBatch<M, S::kUnroll, kZero, kRowScale, kPairA, false>(p, arow, r0, ke32, kw32, tbase, bx);
+      __builtin_amdgcn_sched_barrier(0);
+      ComputeNarrowBatch<M, S::kUnroll, kZero, kRowScale, false>(bx, r0, ke32, zc, acc);
+    } else {
+#pragma unroll 1
+      for (int u = 0; u < S::kUnroll; u += kTailUnroll) {
+        const int rt = r0 + u * static_cast<int>(S::kStepRows);
+        NarrowBatch<M, kTailUnroll> bt;
+        LoadNarrowBatch<M, kTailUnroll, kZero, kRowScale, kPairA, true>(p, arow, rt, ke32, kw32, tbase, bt);
+        __builtin_amdgcn_sched_barrier(0);
+        ComputeNarrowBatch<M, kTailUnroll, kZero, kRowScale, true>(bt, rt, ke32, zc, acc);
       }
     }
   }
-  if (lane < 4) {
-    for (int r = 0; r < 4; ++r)
-      for (int t = 0; t < 16; ++t) red[wave][r][lane * 16 + t] = acc[t][r];
+
+#pragma unroll
+  for (int mm = 0; mm < M; ++mm) {
+    const float v = WaveColumnSum8(acc[mm], lane);
+    if ((lane & 7) == 0) red[wave][mm][lane >> 3] = v;
   }
   __syncthreads();
-  if (tid < 4 * kNarrowTile) {
+  if (tid < M * kNarrowTile) {
     const int mm = tid / kNarrowTile;
     const int c = tid % kNarrowTile;
-    const int64_t out_col = static_cast<int64_t>(tile) * kNarrowTile + c;
-    if (mm < p.m && out_col < p.n) {
+    const int64_t col = col0 + c;
+    if (mm < p.m && col < p.n) {
       float s = red[0][mm][c];
-      for (int wv = 1; wv < kNarrowWaves; ++wv) s = s + red[wv][mm][c];
-      Emit(p, split, mm, out_col, s);
+      for (int wv = 1; wv < S::kWaves; ++wv) s = s + red[wv][mm][c];
+      if (p.splits > 1) {
+        p.partials[(static_cast<int64_t>(split) * p.m + mm) * p.n + col] = s;
+      } else {
+        const float cs = p.mode == kScalePerRow ? 1.f : col_scale;
+        p.c[mm * p.n + col] = ApplyEpilogue(__fmul_rn(s, cs), mm, col, p.n, p.epi);
+      }
     }
   }
 }
@@ -372,28 +440,34 @@ __global__ void SplitReduceKernel(const float* partials, int32_t splits, int64_t
   }
 }
 
-// dst[(t*k + r)*64 + c] = q[r*n + 64t + c] (0 past n): 64-column tiles, each contiguous.
-// One thread moves 16 bytes: a 16-byte-aligned chunk when n allows it, bytes otherwise.
+// dst[(t*kp + r)*8 + c] = q[r*n + 8t + c] (0 past n and in the pad row r = k when k is odd):
+// 8-column tiles, each contiguous. One thread writes the 16 bytes of one row pair of one tile;
+// consecutive threads take consecutive tiles of the same rows, so the reads of a wave are
+// contiguous runs of each row.
 __global__ void TileColumnsKernel(const int8_t* q, int64_t k, int64_t n, int8_t* dst, int64_t tiles) {
-  const int64_t chunks = tiles * k * (kGemvTileCols / 16);
-  const bool vec = (n % 16 == 0) && (reinterpret_cast<uintptr_t>(q) % 16 == 0);
+  const int64_t kp = k + (k & 1);
+  const int64_t chunks = tiles * (kp / 2);
+  const bool vec = (n % 8 == 0) && (reinterpret_cast<uintptr_t>(q) % 8 == 0);
   for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < chunks;
        idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t j = idx % (kGemvTileCols / 16);  // 16-byte chunk within the tile row
-    const int64_t tr = idx / (kGemvTileCols / 16);
-    const int64_t r = tr % k;
-    const int64_t t = tr / k;
-    const int64_t col = t * kGemvTileCols + j * 16;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (vec && col + 15 < n) {
-      v = *reinterpret_cast<const uint4*>(q + r * n + col);
-    } else {
-      uint32_t w[4] = {0, 0, 0, 0};
-      for (int b = 0; b < 16; ++b)
-        if (col + b < n) w[b >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(q[r * n + col + b])) << (8 * (b & 3));
-      v = make_uint4(w[0], w[1], w[2], w[3]);
+    const int64_t t = idx % tiles;
+    const int64_t rp = idx / tiles;
+    const int64_t col = t * kGemvTileCols;
+    uint32_t w[4] = {0, 0, 0, 0};
+    for (int h = 0; h < 2; ++h) {
+      const int64_t r = 2 * rp + h;
+      if (r >= k) continue;
+      if (vec && col + 7 < n) {
+        const uint2 v = *reinterpret_cast<const uint2*>(q + r * n + col);
+        w[2 * h] = v.x;
+        w[2 * h + 1] = v.y;
+      } else {
+        for (int b = 0; b < 8; ++b)
+          if (col + b < n)
+            w[2 * h + (b >> 2)] |= static_cast<uint32_t>(static_cast<uint8_t>(q[r * n + col + b])) << (8 * (b & 3));
+      }
     }
-    *reinterpret_cast<uint4*>(dst + idx * 16) = v;
+    *reinterpret_cast<uint4*>(dst + (t * kp + 2 * rp) * kGemvTileCols) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -401,7 +475,7 @@ __global__ void TileColumnsKernel(const int8_t* q, int64_t k, int64_t n, int8_t*
 
 void LaunchTileColumns(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream) {
   const int64_t tiles = (n + kGemvTileCols - 1) / kGemvTileCols;
-  const int64_t chunks = tiles * k * (kGemvTileCols / 16);
+  const int64_t chunks = tiles * ((k + 1) / 2);
   int64_t grid = (chunks + 255) / 256;
   if (grid > 65536) grid = 65536;
   hipLaunchKernelGGL(TileColumnsKernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, q, k, n, dst, tiles);
@@ -418,27 +492,52 @@ void LaunchSplitReduce(const float* partials, int32_t splits, int64_t m, int64_t
   Check(hipGetLastError(), "SplitReduceKernel launch");
 }
 
+namespace {
+
+template <int M>
+void LaunchNarrow(const GemvArgs& args, dim3 grid, bool zero, bool row_scale, bool pair_a, hipStream_t stream) {
+  const dim3 block(NarrowShape<M>::kThreads);
+  switch ((zero ? 4 : 0) | (row_scale ? 2 : 0) | (pair_a ? 1 : 0)) {
+#define ACCEL_GEMV_CASE(Z, R, P) \
+  case (Z ? 4 : 0) | (R ? 2 : 0) | (P ? 1 : 0): \
+    hipLaunchKernelGGL((GemvNarrowKernel<M, Z, R, P>), grid, block, 0, stream, args); \
+    break;
+    ACCEL_GEMV_CASE(true, true, true) ACCEL_GEMV_CASE(true, true, false) ACCEL_GEMV_CASE(true, false, true)
+    ACCEL_GEMV_CASE(true, false, false) ACCEL_GEMV_CASE(false, true, true) ACCEL_GEMV_CASE(false, true, false)
+    ACCEL_GEMV_CASE(false, false, true) ACCEL_GEMV_CASE(false, false, false)
+#undef ACCEL_GEMV_CASE
+  }
+}
+
+}  // namespace
+
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
                   hipStream_t stream) {
   if (m < 1 || m > 16 || k < 1 || n < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV shape out of range");
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
-  // The narrow kernel reads the staged column tiles; without them the wide kernel, which
-  // reads W in place, takes any m <= 16.
-  const bool narrow = m <= 4 && b.tiled != nullptr;
+  // The narrow kernel reads the staged column tiles (and indexes rows in 32 bits); without
+  // them the wide kernel, which reads W in place, takes any m <= 16.
+  const bool narrow = m <= 4 && b.tiled != nullptr && k < (int64_t(1) << 28);
   const int64_t tile_cols = narrow ? kNarrowTile : kWideTile;
   const int64_t tiles = (n + tile_cols - 1) / tile_cols;
   int64_t splits = 1;
+  int64_t rows = k;
   if (narrow) {
-    // One workgroup per tile over all of K unless the tiles leave most CUs idle on a long K.
-    if (tiles < cus / 2 && k >= 4096) splits = std::min<int64_t>((cus + tiles - 1) / tiles, k / 1024);
+    // One workgroup per tile over all of K, unless the tiles leave the CUs short of work on a
+    // K of several batches: then K is split so that about four workgroups run per CU.
+    const int64_t step_rows = m == 1 ? NarrowShape<1>::kStepRows : NarrowShape<2>::kStepRows;
+    const int64_t batch_rows = m == 1 ? NarrowShape<1>::kBatchRows : NarrowShape<2>::kBatchRows;
+    if (tiles < 4 * cus && k >= 2 * batch_rows)
+      splits = std::min<int64_t>((4 * cus + tiles - 1) / tiles, k / batch_rows);
+    rows = (k + splits - 1) / splits;
+    rows = (rows + step_rows - 1) / step_rows * step_rows;
   } else {
     splits = std::max<int64_t>((cus + tiles - 1) / tiles, (k + kWideMaxRows - 1) / kWideMaxRows);
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, (k + 255) / 256));
+    rows = (k + splits - 1) / splits;
+    rows = std::min<int64_t>((rows + 15) / 16 * 16, kWideMaxRows);
   }
-  int64_t rows = (k + splits - 1) / splits;
-  rows = (rows + 15) / 16 * 16;
-  if (!narrow) rows = std::min<int64_t>(rows, kWideMaxRows);
   splits = (k + rows - 1) / rows;
   const int64_t tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
   if (tiles_per_xcd * kXcds > 0x7fffffff || splits > 65535) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV grid too large");
@@ -466,26 +565,22 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   }
   static_assert(kNarrowTile == kGemvTileCols, "staged tiles must match the narrow kernel tile");
   args.tiled = narrow ? b.tiled : nullptr;
-  const bool vec = (n % 16 == 0) && (reinterpret_cast<uintptr_t>(b.q) % 16 == 0);
   const bool zero = b.zero != nullptr;
   const bool row_scale = b.mode == kScalePerRow;
   const dim3 grid(static_cast<uint32_t>(tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
-  const int variant = (vec ? 4 : 0) | (zero ? 2 : 0) | (row_scale ? 1 : 0);
   if (narrow) {
-    const dim3 block(kNarrowThreads);
-    switch ((m == 1 ? 4 : 0) + (zero ? 2 : 0) + (row_scale ? 1 : 0)) {
-#define ACCEL_GEMV_CASE(V, Z, R) \
-  case (V ? 4 : 0) + (Z ? 2 : 0) + (R ? 1 : 0): \
-    hipLaunchKernelGGL((GemvNarrowKernel<Z, R, V>), grid, block, 0, stream, args); \
-    break;
-      ACCEL_GEMV_CASE(true, true, true) ACCEL_GEMV_CASE(true, true, false) ACCEL_GEMV_CASE(true, false, true)
-      ACCEL_GEMV_CASE(true, false, false) ACCEL_GEMV_CASE(false, true, true) ACCEL_GEMV_CASE(false, true, false)
-      ACCEL_GEMV_CASE(false, false, true) ACCEL_GEMV_CASE(false, false, false)
-#undef ACCEL_GEMV_CASE
+    const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
+    if (m == 1) {
+      LaunchNarrow<1>(args, grid, zero, row_scale, pair_a, stream);
+    } else if (m == 2) {
+      LaunchNarrow<2>(args, grid, zero, row_scale, pair_a, stream);
+    } else {
+      LaunchNarrow<4>(args, grid, zero, row_scale, pair_a, stream);
     }
   } else {
+    const bool vec = (n % 16 == 0) && (reinterpret_cast<uintptr_t>(b.q) % 16 == 0);
     const dim3 block(kWideThreads);
-    switch (variant) {
+    switch ((vec ? 4 : 0) | (zero ? 2 : 0) | (row_scale ? 1 : 0)) {
 #define ACCEL_GEMV_CASE(V, Z, R) \
   case (V ? 4 : 0) | (Z ? 2 : 0) | (R ? 1 : 0): \
     hipLaunchKernelGGL((GemvWideKernel<V, Z, R>), grid, block, 0, stream, args); \

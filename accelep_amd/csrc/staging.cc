@@ -3,8 +3,8 @@
 // accel::MatMulQuantized receives W as the row-major [k, n] int8 bytes the EP uploaded
 // (src/ep.cc:843-900, src/runtime.cc:326-327). Read in that layout, a workgroup that owns a
 // few columns walks k rows 14 KB apart, which HBM serves at well under half its streaming
-// rate. On its first use by the GEMV, the matrix is copied once into 64-column tiles, each
-// tile's k x 64 bytes contiguous; later calls read the copy. The original bytes stay as
+// rate. On its first use by the GEMV, the matrix is copied once into 8-column tiles, each
+// tile's k x 8 bytes contiguous; later calls read the copy. The original bytes stay as
 // they are, so every counted copy and every other kernel still sees the EP's layout.
 //
 // A copy is keyed by (allocation id, byte offset, k, n) and dropped when its allocation is
@@ -78,8 +78,7 @@ const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream
     it->second.last_use = ++g_tick;
     return it->second.data;
   }
-  const int64_t tiles = (n + kGemvTileCols - 1) / kGemvTileCols;
-  const size_t bytes = static_cast<size_t>(tiles * k * kGemvTileCols);
+  const size_t bytes = StagedTileBytes(k, n);
   EvictFor(bytes);
   int8_t* dst = nullptr;
   if (hipMalloc(reinterpret_cast<void**>(&dst), bytes) != hipSuccess) return nullptr;  // fall back to raw

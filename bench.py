@@ -5,8 +5,8 @@ constant int8 weight (accel::MatMulQuantized) and its fp32-MFMA forms.
 Headline (`value`): the int8-weight decode GEMV, X fp32 [1, 4096] @ W int8 [4096, 14336]
 with a per-column fp32 scale, in algorithmic GB/s. Eight device copies of W (470 MB, more
 than the 256 MB Infinity Cache) are used round robin so every step streams W from HBM.
-A step is one accel_hip_matmul_quantized call; the K timed steps are replayed from a HIP
-graph between two HIP events on the library stream.
+A step is one accel_hip_matmul_quantized call; the K timed steps are replayed from HIP
+graphs of up to 200 steps, timed between two HIP events on the library stream.
 
 Secondary lines (same JSON object, "secondary"): the GEMV at M = 4 and 16, the fp32 MLP
 (Gemm+bias+Gelu, Gemm+bias+residual, fused epilogues) in TFLOP/s, the int8 prefill GEMM
@@ -41,6 +41,21 @@ COPIES = 8
 def gemv_bytes(m, k=K_DIM, n=N_DIM):
     """Algorithmic HBM bytes of one GEMV: int8 W once, fp32 scale, X read, C written."""
     return k * n + 4 * n + 4 * m * k + 4 * m * n
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_q8_m1_4096x14336_pmc.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed FETCH_SIZE/WRITE_SIZE
+    profile (rocprofv3 --pmc runs, scaled by a streaming kernel of known traffic), or None."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -89,21 +104,39 @@ class Hip:
         return ms
 
 
-def timed_steps(hip, step, period, steps, warmup):
-    """Warms up, captures `period` steps (and the remainder) into graphs, times exactly `steps`."""
-    # At least one call before capturing: first use may grow the split-K workspace,
-    # which synchronizes and therefore cannot happen inside a capture.
+GRAPHS = True  # --no-graph: launch every step directly (profiler counter runs see each dispatch)
+
+
+def timed_steps(hip, step, steps, warmup, period=200):
+    """Warms up, captures the timed calls into graphs of up to `period` steps, times exactly `steps`.
+
+    `period` is a multiple of the weight-copy rotation, so step i always reads copy i % 8 and
+    a replay never restarts on a copy that is still cached. Inside a graph consecutive kernels
+    start back to back; graphs of a few hundred nodes keep the per-launch queue gap off the
+    average, so the event-timed step matches the profiler's per-kernel duration."""
+    # At least one call before capturing: first use may grow the split-K workspace or stage
+    # the weight tiles, which synchronizes and therefore cannot happen inside a capture.
     for i in range(max(warmup, 1)):
         step(i)
     hip.sync()
+    if not GRAPHS:
+        hip.check(hip.L.accel_hip_event_record(0))
+        for i in range(steps):
+            step(i)
+        hip.check(hip.L.accel_hip_event_record(1))
+        return hip.L.accel_hip_event_elapsed_ms(0, 1)
+    period = min(period, steps)
     full = hip.graph(step, period)
     rest = steps % period
     tail = hip.graph(step, rest) if rest else None
     plan = [(full, steps // period)] + ([(tail, 1)] if tail else [])
-    ms = hip.time_graph(plan)
-    for g, _ in plan:
-        hip.L.accel_hip_graph_destroy(g)
-    return ms
+    try:
+        for g, _ in plan:  # the first replay of a graph uploads it
+            hip.check(hip.L.accel_hip_graph_launch(g, 1))
+        return hip.time_graph(plan)
+    finally:
+        for g, _ in plan:
+            hip.L.accel_hip_graph_destroy(g)
 
 
 def bench_gemv(hip, m, steps, warmup, copies, rng):
@@ -119,7 +152,7 @@ def bench_gemv(hip, m, steps, warmup, copies, rng):
         hip.check(hip.L.accel_hip_matmul_quantized(x.ptr, None, None, C.byref(planes[i % copies]), out.ptr, m, K_DIM,
                                                    N_DIM))
 
-    ms = timed_steps(hip, step, copies, steps, warmup)
+    ms = timed_steps(hip, step, steps, warmup, period=25 * copies)
     per = ms / steps
     return per, gemv_bytes(m) / (per * 1e-3) / 1e9
 
@@ -145,7 +178,7 @@ def bench_mlp(hip, steps, warmup, rng):
         hip.check(hip.L.accel_hip_matmul_fused(x.ptr, w1.ptr, hid.ptr, m, d, h, C.byref(e1)))
         hip.check(hip.L.accel_hip_matmul_fused(hid.ptr, w2.ptr, y.ptr, m, h, d, C.byref(e2)))
 
-    ms = timed_steps(hip, step, 1, steps, warmup)
+    ms = timed_steps(hip, step, steps, warmup)
     per = ms / steps
     flops = 2 * m * d * h * 2
     return per, flops / (per * 1e-3) / 1e12
@@ -167,9 +200,21 @@ def bench_prefill(hip, steps, warmup, rng):
         hip.check(hip.L.accel_hip_matmul_quantized_fused(x.ptr, None, None, C.byref(plane), out.ptr, m, k, n,
                                                          C.byref(e)))
 
-    ms = timed_steps(hip, step, 1, steps, warmup)
+    ms = timed_steps(hip, step, steps, warmup)
     per = ms / steps
     return per, 2 * m * k * n / (per * 1e-3) / 1e12
+
+
+def calibrate_traffic(hip):
+    """One residual add over 16 Mi floats: a streaming kernel of known HBM traffic (128 MiB read,
+    64 MiB written) whose FETCH_SIZE / WRITE_SIZE scale the GEMV's counters to bytes."""
+    count = 16 << 20
+    dst = hip.DeviceArray((count,))
+    src = hip.DeviceArray((count,))
+    hip.check(hip.L.accel_hip_residual_add(dst.buffer, src.buffer, count))
+    hip.sync()
+    dst.free()
+    src.free()
 
 
 def cpu_baseline(rng):
@@ -209,7 +254,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch each step directly instead of from HIP graphs")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run one residual add of known traffic (for profiler counter scaling)")
     args = ap.parse_args()
+    global GRAPHS
+    GRAPHS = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the hot path runs on a single MI355X and there is no "
               f"multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
@@ -221,6 +271,8 @@ def main():
     hip = Hip()
     log(f"device {hip.arch}")
 
+    if args.calibrate:
+        calibrate_traffic(hip)
     per1, gbs1 = bench_gemv(hip, 1, args.steps, args.warmup, COPIES, rng)
     log(f"gemv M=1 (HBM, {COPIES} copies): {per1 * 1e3:.2f} us/step, {gbs1:.1f} GB/s")
     secondary = {}
@@ -280,8 +332,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs1 / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "GemvQ8Kernel<4,true,false>",
+            "traffic": measured_traffic(),
+            "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
+            "kernel": "GemvNarrowKernel<1,false,false,true> (accelep_amd/csrc/gemv_q8.hip)",
             "algorithmic_bytes_per_launch": gemv_bytes(1),
             "avg_launch_us_event_timed": round(per1 * 1e3, 3),
         },

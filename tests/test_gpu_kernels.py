@@ -20,7 +20,7 @@ import pytest
 from golden_cases import (attention_cases, embed_cases, epilogue_cases, quant_cases, rmsnorm_cases, rope_cases,
                           sample_cases, silu_add_cases)
 from hip_helpers import (Buffer, Epilogue, HipError, DeviceArray, assert_gamma_bound, check, dev, dequant_host, lib,
-                         matmul_quantized, quant_plane, same_bits, stats)
+                         matmul_quantized, plane_from_spec, quant_plane, same_bits, stats)
 
 pytestmark = pytest.mark.gpu
 
@@ -189,12 +189,28 @@ def test_gemv_c3_shape(m):
     assert worst_ratio < 1.0
 
 
-@pytest.mark.parametrize("m,k,n,zero,axis", [(3, 2048, 4096, True, 1), (5, 1000, 1000, True, 0), (2, 576, 1536, False, 0),
-                                             (9, 333, 77, True, 1)])
+@pytest.mark.parametrize("m,k,n,zero,axis", [
+    (3, 2048, 4096, True, 1), (5, 1000, 1000, True, 0), (2, 576, 1536, False, 0), (9, 333, 77, True, 1),
+    # staged 8-column tiles: odd k (pad row, unpaired A loads), n not a multiple of 8,
+    # split K for m = 1 and m = 4, per-row zero, a k smaller than one row pair
+    (1, 4097, 1001, True, 1), (1, 8192, 520, False, 1), (4, 12288, 264, True, 0), (2, 999, 17, True, 1),
+    (3, 5, 9, True, 0), (1, 1, 3, False, 1)])
 def test_gemv_modes(m, k, n, zero, axis):
     case = c3_case(m, k, n, 7 * m + k, zero=zero, axis=axis)
     got = matmul_quantized(case)
     assert_gamma_bound(got, case["a"], dequant_host(case["bq"], k, n))
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_gemv_unaligned_a(m):
+    """A at a 4-byte (not 8-byte) aligned address: the row-pair loads of A must not be used."""
+    k, n = 1024, 200
+    case = c3_case(m, k, n, 500 + m)
+    plane, keep = plane_from_spec(case["bq"])
+    a_d = dev(np.concatenate([np.zeros(1, np.float32), case["a"].ravel()]))
+    c = dev(np.zeros((m, n), np.float32))
+    check(lib().accel_hip_matmul_quantized(a_d.at(1), None, None, C.byref(plane), c.ptr, m, k, n))
+    assert_gamma_bound(c.numpy(), case["a"], dequant_host(case["bq"], k, n))
 
 
 @pytest.mark.parametrize("m,k,n", [(512, 576, 1536), (64, 4096, 1024), (100, 200, 300), (2048, 576, 192)])
