@@ -55,6 +55,8 @@ SIGNATURES = {
     "accel_hip_init": (C.c_int, []),
     "accel_hip_synchronize": (C.c_int, []),
     "accel_hip_device_arch": (C.c_char_p, []),
+    "accel_hip_set_exact_products": (C.c_int, [C.c_int32]),
+    "accel_hip_exact_products": (C.c_int32, []),
     "accel_hip_allocate": (C.c_int, [C.c_size_t, C.POINTER(Buffer)]),
     "accel_hip_free": (C.c_int, [Buffer]),
     "accel_hip_copy_h2d": (C.c_int, [Buffer, C.c_void_p, C.c_size_t]),

@@ -123,7 +123,9 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
     Epilogue main = epi;
     main.rms_weight = nullptr;
     main.rms_out = nullptr;
-    if (q8 && m <= 16) {
+    if (ctx.exact_products) {
+      LaunchExactMatmul(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream);
+    } else if (q8 && m <= 16) {
       if (m <= 4) view.tiled = StagedColumnTiles(view.q, k, n, ctx.stream);
       LaunchGemvQ8(a_f, view, c, m, k, n, main, ctx.stream);
     } else {
@@ -149,6 +151,16 @@ void QuantizedChecks(const float* a, const AccelHipQuantPlane* aq, const float* 
 using namespace accel_hip;
 
 extern "C" {
+
+ACCEL_HIP_API int accel_hip_set_exact_products(int32_t on) {
+  return Guard([&] { Ctx().exact_products = on != 0; });
+}
+
+ACCEL_HIP_API int32_t accel_hip_exact_products(void) {
+  int32_t on = 0;
+  Guard([&] { on = Ctx().exact_products ? 1 : 0; });
+  return on;
+}
 
 // Device::MatMul (src/sim_device.cc:185-196).
 ACCEL_HIP_API int accel_hip_matmul(AccelHipBuffer a, AccelHipBuffer b, AccelHipBuffer c, int64_t m, int64_t k,

@@ -29,6 +29,8 @@ struct Context {
   // Scratch for split-K partial sums. Grown on demand (the stream is drained first).
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
+  // Matmuls use the exact-order kernels (exact.hip) instead of the MFMA GEMM / VALU GEMV.
+  bool exact_products = false;
 };
 
 // Initialises GPU 0 and the stream on first use.
@@ -106,6 +108,10 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
 // C[m, n] = A[m, k] @ B[k, n]; B is fp32 (b) or int8 (bq.q != nullptr). fp32 MFMA.
 void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
                    const Epilogue& epi, hipStream_t stream);
+// C = A @ B in the reference's order and rounding (one k-ordered chain per output, split
+// products, per-element dequantization); B is fp32 (b) or int8 (bq.q != nullptr).
+void LaunchExactMatmul(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
+                       const Epilogue& epi, hipStream_t stream);
 // partials [splits][m][n] -> C: sum in split order, times the column scale of `mode`
 // (none when scale is null or mode is per-row), then the epilogue.
 void LaunchSplitReduce(const float* partials, int32_t splits, int64_t m, int64_t n, float* c, int32_t mode,

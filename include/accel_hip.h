@@ -133,6 +133,15 @@ ACCEL_HIP_API int accel_hip_matmul(AccelHipBuffer a, AccelHipBuffer b, AccelHipB
 ACCEL_HIP_API int accel_hip_matmul_quantized(const float* a, const AccelHipQuantPlane* a_quant, const float* b,
                                              const AccelHipQuantPlane* b_quant, float* c, int64_t m, int64_t k,
                                              int64_t n);
+/* Exact products (no reference counterpart as a switch; it selects the reference's own
+ * arithmetic). When on, every matmul entry point sums each output in k order from zero with
+ * each product rounded before its add, and dequantizes an int8 operand per element as
+ * (float(q) - float(zero)) * scale: the bits of ReferenceMatMul / MatMulQuantized
+ * (src/sim_device.cc:387-402,541-602). When off (the default) the MFMA GEMM and the VALU
+ * GEMV add in their own order: within 2*gamma_K*(|A|@|B|) of the exact product. Process-wide;
+ * accel_hip_exact_products() reads the setting (1 on, 0 off). */
+ACCEL_HIP_API int accel_hip_set_exact_products(int32_t on);
+ACCEL_HIP_API int32_t accel_hip_exact_products(void);
 /* Fused forms of the two calls above (see AccelHipEpilogue). Count as one kernel matmul
  * each, like the unfused call; the caller notes its epilogue counters as the runtime does. */
 ACCEL_HIP_API int accel_hip_matmul_fused(const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n,

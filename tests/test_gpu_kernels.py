@@ -119,6 +119,27 @@ def test_matmul_reference_fixtures(gold):
         assert np.all(np.abs(got - want) <= 1e-5 * np.maximum(scale, 1.0))
 
 
+@pytest.fixture
+def exact_products():
+    L = lib()
+    check(L.accel_hip_set_exact_products(1))
+    assert L.accel_hip_exact_products() == 1
+    yield
+    check(L.accel_hip_set_exact_products(0))
+
+
+def test_exact_products_reproduce_reference_bits(gold, exact_products):
+    """With exact products on, MatMul and MatMulQuantized store the compiled reference's
+    bits (src/sim_device.cc:387-402,541-602) on every fixture, incl. the split-product KAT."""
+    kat = run_matmul(np.array([[0xBE2694CD, 0x3E41AF7D]], np.uint32).view(np.float32),
+                     np.array([[0x3F800000], [0x3F5C2CB8]], np.uint32).view(np.float32))
+    assert kat.view(np.uint32)[0, 0] == 0xB5200000
+    for key in [k[:-2] for k in gold if k.startswith("matmul_") and k.endswith("_a")]:
+        same_bits(run_matmul(gold[key + "_a"], gold[key + "_b"]), gold[key + "_device"])
+    for case in quant_cases():
+        same_bits(matmul_quantized(case), gold[f"quant_{case['name']}_out"])
+
+
 def test_matmul_probes_and_zero_k():
     L = lib()
     L.accel_hip_reset_packed_probes()
