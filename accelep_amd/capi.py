@@ -109,6 +109,30 @@ class HipError(RuntimeError):
         self.message = message
 
 
+class LlamaConfig(C.Structure):
+    """AccelLlamaConfig (include/accel_llama.h)."""
+
+    _fields_ = [("vocab", C.c_int32), ("hidden", C.c_int32), ("layers", C.c_int32), ("heads", C.c_int32),
+                ("kv_heads", C.c_int32), ("intermediate", C.c_int32), ("context", C.c_int32), ("eps", C.c_float),
+                ("rope_theta", C.c_float)]
+
+
+# include/accel_llama.h
+LLAMA_SIGNATURES = {
+    "accel_llama_create": (C.c_void_p, [C.POINTER(LlamaConfig)]),
+    "accel_llama_destroy": (None, [C.c_void_p]),
+    "accel_llama_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, F32P, i64, i64]),
+    "accel_llama_weight_q8": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, I8P, F32P, i64, i64]),
+    "accel_llama_generate": (C.c_int, [C.c_void_p, I32P, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_uint32,
+                                       C.c_int32, I32P, I32P]),
+    "accel_llama_forward_ids": (C.c_int, [C.c_void_p, I32P, C.c_int32, C.c_int32]),
+    "accel_llama_logit_max_abs": (C.c_int, [C.c_void_p, F32P, C.c_int32, F32P]),
+    "accel_llama_logits": (C.c_int, [C.c_void_p, F32P, C.c_int32]),
+    "accel_llama_reset": (None, [C.c_void_p]),
+    "accel_llama_last_error": (C.c_char_p, []),
+}
+
+
 def lib() -> C.CDLL:
     """Loads libaccel_hip.so (raises if it was not built)."""
     global _lib
@@ -116,7 +140,7 @@ def lib() -> C.CDLL:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m accelep_amd.build`")
         handle = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**SIGNATURES, **LLAMA_SIGNATURES}.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args

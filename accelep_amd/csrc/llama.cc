@@ -1,0 +1,524 @@
+// The Llama loop of AccelEP (src/llama_model.cc:209-247 Forward, :101-131 Generate,
+// :325-380 create, :399-422 weights) on one MI355X.
+//
+// The call sequence per layer is the reference's: RMSNorm, q/k/v projections, RoPE on q and
+// k, KV append, causal attention, o projection + residual, RMSNorm, gate/up, SiLU*up, down
+// projection + residual; then the final RMSNorm of the last row and the LM head. What
+// differs is where things live and how many passes there are:
+//  * the residual adds run in the o and down projections' stores (c = acc + hidden, in
+//    place), which gives the bits of the reference's MatMul + ResidualAdd pair;
+//  * linear layers are int8 [in, out] with a per-output-column scale (the int8 GEMV for a
+//    decode step, the int8-panel MFMA GEMM for a prompt) or fp32 [in, out];
+//  * the sampler's xorshift state and the chosen ids stay in device memory, so a generate
+//    call copies the ids back once and, with no eos id, never waits on the GPU in between.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "accel_llama.h"
+#include "common.h"
+
+namespace {
+
+using namespace accel_hip;
+
+thread_local std::string g_llama_error;
+
+// One device allocation through the library heap (counted live, zero-filled), freed on destruction.
+class DevBuf {
+ public:
+  DevBuf() = default;
+  explicit DevBuf(size_t bytes) {
+    if (accel_hip_allocate(bytes, &b_) != ACCEL_HIP_OK) Fail(ACCEL_HIP_BAD_ALLOC, accel_hip_last_error());
+  }
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  DevBuf(DevBuf&& o) noexcept : b_(o.b_) { o.b_ = AccelHipBuffer{}; }
+  DevBuf& operator=(DevBuf&& o) noexcept {
+    if (this != &o) {
+      Release();
+      b_ = o.b_;
+      o.b_ = AccelHipBuffer{};
+    }
+    return *this;
+  }
+  ~DevBuf() { Release(); }
+
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(b_.data);
+  }
+  const AccelHipBuffer& buffer() const { return b_; }
+  bool empty() const { return b_.data == nullptr; }
+
+  // Counted host-to-device copy (the reference uploads through Device::CopyHostToDevice).
+  void Upload(const void* src, size_t bytes) {
+    if (bytes != 0 && accel_hip_copy_h2d(b_, src, bytes) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+  }
+
+ private:
+  void Release() {
+    if (b_.data != nullptr) accel_hip_free(b_);
+    b_ = AccelHipBuffer{};
+  }
+  AccelHipBuffer b_{};
+};
+
+// A linear layer held as [in, out]: fp32, or int8 with one scale per output column.
+struct Linear {
+  DevBuf f;      // fp32 [in, out]
+  DevBuf q;      // int8 [in, out]
+  DevBuf scale;  // fp32 [out]
+  int64_t in = 0, out = 0;
+  bool ready() const { return !f.empty() || !q.empty(); }
+};
+
+struct LayerWeights {
+  DevBuf attn_norm, post_norm;
+  Linear q, k, v, o, gate, up, down;
+};
+
+struct Model {
+  AccelLlamaConfig cfg{};
+  int32_t head_dim = 0;
+  int32_t filled = 0;
+  std::mutex mu;
+  // Embedding: fp32 [vocab, hidden], or int8 [vocab, hidden] with a per-row scale.
+  DevBuf embed_f, embed_q, embed_scale;
+  DevBuf final_norm;
+  Linear lm_head;
+  DevBuf rope_cos, rope_sin;
+  DevBuf hidden, normed, query, key, value, mixed, gate, up, logits;
+  DevBuf chosen, prompt_ids, words;  // words: [0] embedding range flag, [1] sampler state
+  std::vector<LayerWeights> layers;
+  std::vector<DevBuf> k_cache, v_cache;
+
+  hipStream_t stream() const { return Ctx().stream; }
+
+  bool Ready() const {
+    if ((embed_f.empty() && embed_q.empty()) || final_norm.empty() || !lm_head.ready()) return false;
+    for (const LayerWeights& l : layers)
+      if (l.attn_norm.empty() || l.post_norm.empty() || !l.q.ready() || !l.k.ready() || !l.v.ready() ||
+          !l.o.ready() || !l.gate.ready() || !l.up.ready() || !l.down.ready())
+        return false;
+    return true;
+  }
+
+  // c[m, out] = a[m, in] @ W (+ residual in the store).
+  void Apply(const Linear& w, const float* a, float* c, int64_t m, const float* residual) {
+    Epilogue e;
+    e.residual = residual;
+    Context& ctx = Ctx();
+    if (!w.q.empty()) {
+      Q8View v;
+      v.q = w.q.as<int8_t>();
+      v.scale = w.scale.as<float>();
+      v.mode = kScalePerCol;
+      if (ctx.exact_products) {
+        LaunchExactMatmul(a, nullptr, v, c, m, w.in, w.out, e, ctx.stream);
+      } else if (m <= 16) {
+        if (m <= 4) v.tiled = StagedColumnTiles(v.q, w.in, w.out, ctx.stream);
+        LaunchGemvQ8(a, v, c, m, w.in, w.out, e, ctx.stream);
+      } else {
+        LaunchGemmF32(a, nullptr, v, c, m, w.in, w.out, e, ctx.stream);
+      }
+    } else if (ctx.exact_products) {
+      LaunchExactMatmul(a, w.f.as<float>(), Q8View{}, c, m, w.in, w.out, e, ctx.stream);
+    } else {
+      LaunchGemmF32(a, w.f.as<float>(), Q8View{}, c, m, w.in, w.out, e, ctx.stream);
+    }
+  }
+
+  // Forward over `seq` ids at ids[id_offset ..] (device int32) from position `filled`
+  // (src/llama_model.cc:209-247). Leaves the last row's logits in `logits`.
+  void Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids) {
+    if (ids == nullptr || seq <= 0 || filled < 0 || seq > cfg.context || filled > cfg.context - seq)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
+    const hipStream_t s = stream();
+    const int64_t H = cfg.hidden, hd = head_dim, inter = cfg.intermediate;
+    const int64_t pos = filled;
+    int32_t* flag = words.as<int32_t>();
+    if (check_ids) Check(hipMemsetAsync(flag, 0, sizeof(int32_t), s), "hipMemsetAsync");
+    LaunchEmbedding(ids + id_offset, embed_f.as<float>(), embed_q.as<int8_t>(), embed_scale.as<float>(),
+                    hidden.as<float>(), seq, H, cfg.vocab, flag, s);
+    if (check_ids) {
+      int32_t bad = 0;
+      Check(hipMemcpyAsync(&bad, flag, sizeof(bad), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+      Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+      if (bad != 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "token id is outside the vocabulary");
+    }
+    const int64_t kv_row = static_cast<int64_t>(cfg.kv_heads) * hd;
+    for (int32_t li = 0; li < cfg.layers; ++li) {
+      LayerWeights& l = layers[static_cast<size_t>(li)];
+      float* kc = k_cache[static_cast<size_t>(li)].as<float>();
+      float* vc = v_cache[static_cast<size_t>(li)].as<float>();
+      LaunchRmsNormRows(hidden.as<float>(), l.attn_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
+      Apply(l.q, normed.as<float>(), query.as<float>(), seq, nullptr);
+      Apply(l.k, normed.as<float>(), key.as<float>(), seq, nullptr);
+      Apply(l.v, normed.as<float>(), value.as<float>(), seq, nullptr);
+      LaunchRope(query.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.heads, hd, pos, s);
+      LaunchRope(key.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.kv_heads, hd, pos, s);
+      LaunchCopy(kc + pos * kv_row, key.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
+      LaunchCopy(vc + pos * kv_row, value.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
+      LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s);
+      Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, hidden.as<float>());
+      LaunchRmsNormRows(hidden.as<float>(), l.post_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
+      Apply(l.gate, normed.as<float>(), gate.as<float>(), seq, nullptr);
+      Apply(l.up, normed.as<float>(), up.as<float>(), seq, nullptr);
+      LaunchSiluMul(gate.as<float>(), up.as<float>(), seq * inter, s);
+      Apply(l.down, gate.as<float>(), hidden.as<float>(), seq, hidden.as<float>());
+    }
+    LaunchRmsNormRows(hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm.as<float>(),
+                      normed.as<float>(), 1, H, cfg.eps, s);
+    Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, nullptr);
+  }
+
+  // src/llama_model.cc:101-131.
+  void Generate(const int32_t* prompt, int32_t prompt_count, int32_t max_new, int32_t eos_id, float temperature,
+                uint32_t seed, int32_t top_k, int32_t* out_ids, int32_t* out_count) {
+    filled = 0;
+    if (prompt == nullptr || prompt_count <= 0 || prompt_count > cfg.context)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
+    prompt_ids.Upload(prompt, static_cast<size_t>(prompt_count) * sizeof(int32_t));
+    Forward(prompt_ids.as<int32_t>(), prompt_count, 0, true);
+    filled = prompt_count;
+    const uint32_t rng0 = seed == 0 ? 0x6d2b79f5u : seed;
+    uint32_t* rng = words.as<uint32_t>() + 1;
+    Check(hipMemcpyAsync(rng, &rng0, sizeof(rng0), hipMemcpyHostToDevice, stream()), "hipMemcpyAsync");
+    Check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+    int32_t produced = 0;
+    for (int32_t step = 0; step < max_new; ++step) {
+      if (produced >= cfg.context) Fail(ACCEL_HIP_INVALID_ARGUMENT, "generation exceeded the token buffer");
+      LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>() + produced, cfg.vocab, temperature, rng, top_k,
+                        stream());
+      produced += 1;
+      if (eos_id >= 0) {
+        // Only an eos id needs the chosen id on the host before the next step.
+        int32_t id = -1;
+        Check(hipMemcpyAsync(&id, chosen.as<int32_t>() + produced - 1, sizeof(id), hipMemcpyDeviceToHost, stream()),
+              "hipMemcpyAsync");
+        Check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+        if (id == eos_id) break;
+      }
+      if (filled >= cfg.context) break;
+      Forward(chosen.as<int32_t>(), 1, static_cast<int64_t>(produced) - 1, false);
+      filled += 1;
+    }
+    if (produced > 0 && accel_hip_copy_d2h(out_ids, chosen.buffer(), static_cast<size_t>(produced) * sizeof(int32_t)) !=
+                            ACCEL_HIP_OK)
+      Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+    *out_count = produced;
+  }
+};
+
+bool IsNorm(int32_t kind) {
+  return kind == ACCEL_W_FINAL_NORM || kind == ACCEL_W_ATTN_NORM || kind == ACCEL_W_POST_NORM;
+}
+
+// Expected HF shape of a weight kind (src/llama_model.cc:290-318).
+bool ShapeOk(const Model& m, int32_t kind, int64_t rows, int64_t cols) {
+  const int64_t H = m.cfg.hidden, qo = static_cast<int64_t>(m.cfg.heads) * m.head_dim,
+                ko = static_cast<int64_t>(m.cfg.kv_heads) * m.head_dim, I = m.cfg.intermediate;
+  switch (kind) {
+    case ACCEL_W_EMBED:
+    case ACCEL_W_LM_HEAD:
+      return rows == m.cfg.vocab && cols == H;
+    case ACCEL_W_FINAL_NORM:
+    case ACCEL_W_ATTN_NORM:
+    case ACCEL_W_POST_NORM:
+      return rows == H && cols == 1;
+    case ACCEL_W_Q:
+      return rows == qo && cols == H;
+    case ACCEL_W_K:
+    case ACCEL_W_V:
+      return rows == ko && cols == H;
+    case ACCEL_W_O:
+      return rows == H && cols == qo;
+    case ACCEL_W_DOWN:
+      return rows == H && cols == I;
+    case ACCEL_W_GATE:
+    case ACCEL_W_UP:
+      return rows == I && cols == H;
+    default:
+      return false;
+  }
+}
+
+Linear* LinearSlot(Model& m, int32_t kind, int32_t layer) {
+  if (kind == ACCEL_W_LM_HEAD) return &m.lm_head;
+  if (layer < 0 || layer >= m.cfg.layers) return nullptr;
+  LayerWeights& l = m.layers[static_cast<size_t>(layer)];
+  switch (kind) {
+    case ACCEL_W_Q:
+      return &l.q;
+    case ACCEL_W_K:
+      return &l.k;
+    case ACCEL_W_V:
+      return &l.v;
+    case ACCEL_W_O:
+      return &l.o;
+    case ACCEL_W_GATE:
+      return &l.gate;
+    case ACCEL_W_UP:
+      return &l.up;
+    case ACCEL_W_DOWN:
+      return &l.down;
+    default:
+      return nullptr;
+  }
+}
+
+DevBuf* NormSlot(Model& m, int32_t kind, int32_t layer) {
+  if (kind == ACCEL_W_FINAL_NORM) return &m.final_norm;
+  if (layer < 0 || layer >= m.cfg.layers) return nullptr;
+  if (kind == ACCEL_W_ATTN_NORM) return &m.layers[static_cast<size_t>(layer)].attn_norm;
+  if (kind == ACCEL_W_POST_NORM) return &m.layers[static_cast<size_t>(layer)].post_norm;
+  return nullptr;
+}
+
+// [rows, cols] -> [cols, rows] on the host.
+template <typename T>
+std::vector<T> Transposed(const T* src, int64_t rows, int64_t cols) {
+  std::vector<T> dst(static_cast<size_t>(rows * cols));
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) dst[static_cast<size_t>(c * rows + r)] = src[r * cols + c];
+  return dst;
+}
+
+template <typename F>
+int Run(F f) {
+  try {
+    f();
+    g_llama_error.clear();
+    return 0;
+  } catch (const Error& e) {
+    g_llama_error = e.message;
+  } catch (const std::bad_alloc&) {
+    g_llama_error = "out of memory";
+  } catch (const std::exception& e) {
+    g_llama_error = e.what();
+  }
+  return 1;
+}
+
+Model* Get(AccelLlama* handle) { return reinterpret_cast<Model*>(handle); }
+
+}  // namespace
+
+extern "C" {
+
+ACCEL_LLAMA_API AccelLlama* accel_llama_create(const AccelLlamaConfig* config) {
+  if (config == nullptr || config->vocab <= 0 || config->hidden <= 0 || config->layers <= 0 || config->heads <= 0 ||
+      config->kv_heads <= 0 || config->intermediate <= 0 || config->context <= 0 ||
+      config->hidden % config->heads != 0 || config->heads % config->kv_heads != 0) {
+    g_llama_error = "invalid llama config";
+    return nullptr;
+  }
+  Model* made = nullptr;
+  const int rc = Run([&] {
+    auto m = std::make_unique<Model>();
+    m->cfg = *config;
+    m->head_dim = config->hidden / config->heads;
+    m->layers.resize(static_cast<size_t>(config->layers));
+    // RoPE tables in double, as src/llama_model.cc:333-349 builds them.
+    const int32_t dim = m->head_dim, half = dim / 2;
+    const size_t ctx = static_cast<size_t>(config->context);
+    std::vector<float> cs(ctx * static_cast<size_t>(dim)), sn(ctx * static_cast<size_t>(dim));
+    for (int32_t pos = 0; pos < config->context; ++pos)
+      for (int32_t i = 0; i < half; ++i) {
+        const double inv = 1.0 / std::pow(static_cast<double>(config->rope_theta), (2.0 * i) / static_cast<double>(dim));
+        const double angle = static_cast<double>(pos) * inv;
+        const size_t at = static_cast<size_t>(pos) * static_cast<size_t>(dim) + static_cast<size_t>(i);
+        cs[at] = cs[at + static_cast<size_t>(half)] = static_cast<float>(std::cos(angle));
+        sn[at] = sn[at + static_cast<size_t>(half)] = static_cast<float>(std::sin(angle));
+      }
+    m->rope_cos = DevBuf(cs.size() * sizeof(float));
+    m->rope_cos.Upload(cs.data(), cs.size() * sizeof(float));
+    m->rope_sin = DevBuf(sn.size() * sizeof(float));
+    m->rope_sin.Upload(sn.data(), sn.size() * sizeof(float));
+    const size_t f = sizeof(float);
+    const size_t q_n = ctx * static_cast<size_t>(config->heads) * dim;
+    const size_t k_n = ctx * static_cast<size_t>(config->kv_heads) * dim;
+    m->hidden = DevBuf(ctx * config->hidden * f);
+    m->normed = DevBuf(ctx * config->hidden * f);
+    m->query = DevBuf(q_n * f);
+    m->key = DevBuf(k_n * f);
+    m->value = DevBuf(k_n * f);
+    m->mixed = DevBuf(q_n * f);
+    m->gate = DevBuf(ctx * config->intermediate * f);
+    m->up = DevBuf(ctx * config->intermediate * f);
+    m->logits = DevBuf(static_cast<size_t>(config->vocab) * f);
+    m->chosen = DevBuf(ctx * sizeof(int32_t));
+    m->prompt_ids = DevBuf(ctx * sizeof(int32_t));
+    m->words = DevBuf(64);
+    for (int32_t l = 0; l < config->layers; ++l) {
+      m->k_cache.emplace_back(k_n * f);
+      m->v_cache.emplace_back(k_n * f);
+    }
+    made = m.release();
+  });
+  return rc == 0 ? reinterpret_cast<AccelLlama*>(made) : nullptr;
+}
+
+ACCEL_LLAMA_API void accel_llama_destroy(AccelLlama* model) {
+  if (model == nullptr) return;
+  accel_hip_synchronize();
+  delete Get(model);
+}
+
+ACCEL_LLAMA_API int accel_llama_weight(AccelLlama* handle, int32_t kind, int32_t layer, const float* data,
+                                       int64_t rows, int64_t cols) {
+  Model* m = Get(handle);
+  if (m == nullptr || data == nullptr || rows <= 0 || cols <= 0 || !ShapeOk(*m, kind, rows, cols)) {
+    g_llama_error = "invalid weight";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    const size_t bytes = static_cast<size_t>(rows * cols) * sizeof(float);
+    if (IsNorm(kind)) {
+      DevBuf* slot = NormSlot(*m, kind, layer);
+      if (slot == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
+      DevBuf b(bytes);
+      b.Upload(data, bytes);
+      *slot = std::move(b);
+    } else if (kind == ACCEL_W_EMBED) {
+      DevBuf b(bytes);
+      b.Upload(data, bytes);
+      m->embed_f = std::move(b);
+      m->embed_q = DevBuf();
+      m->embed_scale = DevBuf();
+    } else {
+      Linear* slot = LinearSlot(*m, kind, layer);
+      if (slot == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
+      const std::vector<float> t = Transposed(data, rows, cols);
+      Linear w;
+      w.in = cols;
+      w.out = rows;
+      w.f = DevBuf(bytes);
+      w.f.Upload(t.data(), bytes);
+      *slot = std::move(w);
+    }
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_weight_q8(AccelLlama* handle, int32_t kind, int32_t layer, const int8_t* q,
+                                          const float* row_scale, int64_t rows, int64_t cols) {
+  Model* m = Get(handle);
+  if (m == nullptr || q == nullptr || row_scale == nullptr || rows <= 0 || cols <= 0 || IsNorm(kind) ||
+      !ShapeOk(*m, kind, rows, cols)) {
+    g_llama_error = "invalid weight";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    const size_t bytes = static_cast<size_t>(rows * cols);
+    const size_t sbytes = static_cast<size_t>(rows) * sizeof(float);
+    if (kind == ACCEL_W_EMBED) {
+      DevBuf qb(bytes), sb(sbytes);
+      qb.Upload(q, bytes);
+      sb.Upload(row_scale, sbytes);
+      m->embed_q = std::move(qb);
+      m->embed_scale = std::move(sb);
+      m->embed_f = DevBuf();
+      return;
+    }
+    Linear* slot = LinearSlot(*m, kind, layer);
+    if (slot == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
+    const std::vector<int8_t> t = Transposed(q, rows, cols);
+    Linear w;
+    w.in = cols;
+    w.out = rows;
+    w.q = DevBuf(bytes);
+    w.q.Upload(t.data(), bytes);
+    w.scale = DevBuf(sbytes);
+    w.scale.Upload(row_scale, sbytes);
+    *slot = std::move(w);
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_generate(AccelLlama* handle, const int32_t* prompt, int32_t prompt_count,
+                                         int32_t max_new, int32_t eos_id, float temperature, uint32_t seed,
+                                         int32_t top_k, int32_t* out_ids, int32_t* out_count) {
+  Model* m = Get(handle);
+  if (m == nullptr || prompt == nullptr || out_ids == nullptr || out_count == nullptr || prompt_count <= 0 ||
+      max_new < 0) {
+    g_llama_error = "invalid generate";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    if (!m->Ready()) Fail(ACCEL_HIP_INVALID_ARGUMENT, "llama weights are incomplete");
+    m->Generate(prompt, prompt_count, max_new, eos_id, temperature, seed, top_k, out_ids, out_count);
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_forward_ids(AccelLlama* handle, const int32_t* ids, int32_t count, int32_t reset) {
+  Model* m = Get(handle);
+  if (m == nullptr) {
+    g_llama_error = "invalid forward";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    if (!m->Ready()) Fail(ACCEL_HIP_INVALID_ARGUMENT, "llama weights are incomplete");
+    if (ids == nullptr || count <= 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "invalid forward");
+    if (reset) m->filled = 0;
+    if (m->filled < 0 || count > m->cfg.context - m->filled) Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
+    m->prompt_ids.Upload(ids, static_cast<size_t>(count) * sizeof(int32_t));
+    m->Forward(m->prompt_ids.as<int32_t>(), count, 0, true);
+    m->filled += count;
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_logits(AccelLlama* handle, float* out, int32_t count) {
+  Model* m = Get(handle);
+  if (m == nullptr || out == nullptr || count != (m ? m->cfg.vocab : 0)) {
+    g_llama_error = "invalid logit read";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    if (accel_hip_peek(out, m->logits.as<float>(), static_cast<size_t>(count) * sizeof(float)) != ACCEL_HIP_OK)
+      Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_logit_max_abs(AccelLlama* handle, const float* reference, int32_t count,
+                                             float* out_max_abs) {
+  Model* m = Get(handle);
+  if (m == nullptr || reference == nullptr || out_max_abs == nullptr || count != m->cfg.vocab) {
+    g_llama_error = "invalid logit reference";
+    return 1;
+  }
+  return Run([&] {
+    std::vector<float> row(static_cast<size_t>(count));
+    {
+      std::lock_guard<std::mutex> lock(m->mu);
+      if (accel_hip_peek(row.data(), m->logits.as<float>(), row.size() * sizeof(float)) != ACCEL_HIP_OK)
+        Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+    }
+    float worst = 0.f;
+    for (int32_t i = 0; i < count; ++i) {
+      const float d = std::fabs(row[static_cast<size_t>(i)] - reference[i]);
+      if (d > worst) worst = d;
+    }
+    *out_max_abs = worst;
+  });
+}
+
+ACCEL_LLAMA_API void accel_llama_reset(AccelLlama* handle) {
+  Model* m = Get(handle);
+  if (m == nullptr) return;
+  std::lock_guard<std::mutex> lock(m->mu);
+  m->filled = 0;
+}
+
+ACCEL_LLAMA_API const char* accel_llama_last_error(void) { return g_llama_error.c_str(); }
+
+}  // extern "C"

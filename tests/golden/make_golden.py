@@ -6,7 +6,9 @@ fixtures are data only: seeded inputs plus what the reference computed on them. 
 check the oracle restatement and the HIP kernels against them where the reference tree
 is absent (a GPU host without the reference sources).
 
-Run: python tests/golden/make_golden.py
+Run: python tests/golden/make_golden.py               (reference_outputs.npz)
+     python tests/golden/make_golden.py --llama-full   (llama_smol_full.npz: the SmolLM2-135M-shape
+                                                       forward, 30 layers, 512 + 128 tokens; minutes)
 """
 
 from __future__ import annotations
@@ -21,14 +23,22 @@ sys.path.insert(0, str(HERE.parent))
 
 from oracle_ctypes import QuantPlane, fill_lcg, lcg_int8, make_plane, reference  # noqa: E402
 from golden_cases import (  # noqa: E402
-    attention_cases, embed_cases, epilogue_cases, llama_cases, quant_cases, rmsnorm_cases, rope_cases,
-    sample_cases, silu_add_cases)
+    attention_cases, embed_cases, epilogue_cases, llama_cases, llama_full_case, quant_cases, rmsnorm_cases,
+    rope_cases, sample_cases, silu_add_cases)
 
 
 def main():
     ref = reference()
     if ref is None:
         raise SystemExit("oracle/_ref/libaccel_ref.so is missing: run `make -C oracle` with the reference tree present")
+    if "--llama-full" in sys.argv:
+        import time
+        case = llama_full_case()
+        t0 = time.time()
+        toks, logits = run_reference_llama(ref, case)
+        np.savez_compressed(HERE / "llama_smol_full.npz", ids=toks, prefill_logits=logits)
+        print(f"wrote {HERE / 'llama_smol_full.npz'}: {toks.size} ids in {time.time() - t0:.0f} s")
+        return
     out = {}
 
     # SimDevice::MatMul and ReferenceMatMul on the reference test's LCG shapes (tests/test_runtime.cc:258-259).

@@ -165,6 +165,9 @@ def llama_config(name):
     if name == "tiny":
         return dict(vocab=256, hidden=64, layers=2, heads=4, kv_heads=2, intermediate=128, context=48, eps=1e-5,
                     rope_theta=100000.0)
+    if name == "smol":  # SmolLM2-135M shape
+        return dict(vocab=49152, hidden=576, layers=30, heads=9, kv_heads=3, intermediate=1536, context=640, eps=1e-5,
+                    rope_theta=100000.0)
     if name == "smol3":  # SmolLM2-135M widths, 3 layers, short context
         return dict(vocab=49152, hidden=576, layers=3, heads=9, kv_heads=3, intermediate=1536, context=40, eps=1e-5,
                     rope_theta=100000.0)
@@ -226,13 +229,22 @@ def llama_cases():
     cfg = llama_config("tiny")
     w, _ = llama_weights(cfg, 101)
     prompt = _rng(102).integers(0, cfg["vocab"], size=16).astype(np.int32)
-    cases.append(dict(name="tiny_greedy", config=cfg, weights=w, prompt=prompt, max_new=24, eos=-1,
+    cases.append(dict(name="tiny_greedy", config=cfg, weights=w, weight_seed=101, prompt=prompt, max_new=24, eos=-1,
                       temperature=0.0, seed=0, top_k=0))
-    cases.append(dict(name="tiny_topk", config=cfg, weights=w, prompt=prompt, max_new=24, eos=-1,
+    cases.append(dict(name="tiny_topk", config=cfg, weights=w, weight_seed=101, prompt=prompt, max_new=24, eos=-1,
                       temperature=0.8, seed=7, top_k=12))
     cfg3 = llama_config("smol3")
     w3, _ = llama_weights(cfg3, 103)
     prompt3 = _rng(104).integers(0, cfg3["vocab"], size=20).astype(np.int32)
-    cases.append(dict(name="smol3_greedy", config=cfg3, weights=w3, prompt=prompt3, max_new=12, eos=-1,
-                      temperature=0.0, seed=0, top_k=0))
+    cases.append(dict(name="smol3_greedy", config=cfg3, weights=w3, weight_seed=103, prompt=prompt3, max_new=12,
+                      eos=-1, temperature=0.0, seed=0, top_k=0))
     return cases
+
+
+def llama_full_case():
+    """The SmolLM2-135M-shape forward: 30 layers, 512 prompt ids, 128 greedy tokens."""
+    cfg = llama_config("smol")
+    w, q = llama_weights(cfg, 105)
+    prompt = _rng(106).integers(0, cfg["vocab"], size=512).astype(np.int32)
+    return dict(name="smol_full_greedy", config=cfg, weights=w, quant=q, prompt=prompt, max_new=128, eos=-1,
+                temperature=0.0, seed=0, top_k=0)

@@ -14,6 +14,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "accel_hip.h"
+LLAMA_HEADER = ROOT / "include" / "accel_llama.h"
 LIB = ROOT / "accelep_amd" / "libaccel_hip.so"
 RUNTIME_LIB = ROOT / "accelep_amd" / "libaccel_runtime.so"
 
@@ -49,10 +50,23 @@ def test_python_mirror_binds_every_symbol():
     assert set(declared_entry_points()) == set(SIGNATURES)
 
 
+def declared_llama_entry_points():
+    return re.findall(r"ACCEL_LLAMA_API\s+[\w\s\*]+?\b(accel_llama_\w+)\s*\(", LLAMA_HEADER.read_text())
+
+
 def test_library_exports_nothing_else():
     out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout
     exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
-    assert exported == set(declared_entry_points())
+    assert exported == set(declared_entry_points()) | set(declared_llama_entry_points())
+
+
+def test_llama_api_mirrors_the_reference_names():
+    from accelep_amd.capi import LLAMA_SIGNATURES
+
+    names = set(declared_llama_entry_points())
+    assert names == set(LLAMA_SIGNATURES)
+    for want in ["create", "destroy", "weight", "generate", "forward_ids", "logit_max_abs", "reset", "last_error"]:
+        assert f"accel_llama_{want}" in names
 
 
 CPP_API = [

@@ -27,12 +27,6 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_outputs.npz"
 
 
-@pytest.fixture(scope="module")
-def gold():
-    with np.load(GOLDEN, allow_pickle=False) as z:
-        return {k: z[k] for k in z.files}
-
-
 @pytest.fixture(scope="module", autouse=True)
 def device():
     check(lib().accel_hip_init())

@@ -1,0 +1,155 @@
+"""The Llama loop on the GPU (include/accel_llama.h, accelep_amd/csrc/llama.cc) against the
+compiled reference's outputs (AccelEP src/llama_model.cc through oracle/_ref, stored in
+tests/golden/): the generated ids must be identical (greedy and top-k sampling), the
+prefill logit row within max|diff| <= 1e-3 (the repository's logit gate,
+tests/test_serve.py:353). The bound is needed because SiLU and attention use the device's
+expf (within 1 ulp of glibc's, not bit-identical) and, by default, the matmuls add in
+another order; with exact products on, only the expf differences remain.
+
+Weights are the same seeded values given either as floats fl(q*s) (what the reference
+receives) or as int8 q with per-row scales s (the HIP engine's int8 path); both must give the
+reference's ids.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import time
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from accelep_amd.capi import F32P, I8P, I32P, LlamaConfig, check, lib
+from golden_cases import llama_cases, llama_full_case, llama_weights
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+FULL_GOLDEN = Path(__file__).resolve().parent / "golden" / "llama_smol_full.npz"
+
+
+class Engine:
+    def __init__(self, config, weights, quant=None):
+        self.L = lib()
+        self.config = config
+        self.h = self.L.accel_llama_create(C.byref(LlamaConfig(**config)))
+        assert self.h, self.L.accel_llama_last_error()
+        for (kind, layer, w) in weights:
+            if quant is not None and (kind, layer) in quant:
+                q, s = quant[(kind, layer)]
+                q = np.ascontiguousarray(q, np.int8)
+                s = np.ascontiguousarray(s, np.float32)
+                rc = self.L.accel_llama_weight_q8(self.h, kind, layer, q.ctypes.data_as(I8P), s.ctypes.data_as(F32P),
+                                                  q.shape[0], q.shape[1])
+            else:
+                w = np.ascontiguousarray(w, np.float32)
+                rows, cols = (w.shape[0], 1) if w.ndim == 1 else w.shape
+                rc = self.L.accel_llama_weight(self.h, kind, layer, w.ctypes.data_as(F32P), rows, cols)
+            assert rc == 0, self.L.accel_llama_last_error()
+
+    def close(self):
+        self.L.accel_llama_destroy(self.h)
+
+    def prefill_logits(self, prompt):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        assert self.L.accel_llama_forward_ids(self.h, prompt.ctypes.data_as(I32P), prompt.size, 1) == 0, \
+            self.L.accel_llama_last_error()
+        row = np.zeros(self.config["vocab"], np.float32)
+        assert self.L.accel_llama_logits(self.h, row.ctypes.data_as(F32P), row.size) == 0
+        return row
+
+    def generate(self, case):
+        prompt = np.ascontiguousarray(case["prompt"], np.int32)
+        ids = np.zeros(case["max_new"], np.int32)
+        count = C.c_int32()
+        rc = self.L.accel_llama_generate(self.h, prompt.ctypes.data_as(I32P), prompt.size, case["max_new"],
+                                         case["eos"], case["temperature"], case["seed"], case["top_k"],
+                                         ids.ctypes.data_as(I32P), C.byref(count))
+        assert rc == 0, self.L.accel_llama_last_error()
+        return ids[: count.value]
+
+
+@pytest.fixture(params=[False, True], ids=["fast", "exact"])
+def products(request):
+    L = lib()
+    check(L.accel_hip_set_exact_products(1 if request.param else 0))
+    yield request.param
+    check(L.accel_hip_set_exact_products(0))
+
+
+@pytest.mark.parametrize("weights", ["float", "int8"])
+def test_llama_matches_reference_fixtures(gold, weights, products):
+    for case in llama_cases():
+        print(f"case {case['name']} weights={weights} exact={products}", flush=True)
+        quant = llama_weights(case["config"], case["weight_seed"])[1] if weights == "int8" else None
+        eng = Engine(case["config"], case["weights"], quant)
+        try:
+            row = eng.prefill_logits(case["prompt"])
+            want = gold[f"llama_{case['name']}_prefill_logits"]
+            worst = float(np.abs(row.astype(np.float64) - want).max())
+            print(f"  prefill logits max|diff| = {worst:.3g}", flush=True)
+            assert worst <= LOGIT_TOL
+            assert int(np.argmax(row)) == int(np.argmax(want))
+            ids = eng.generate(case)
+            np.testing.assert_array_equal(ids, gold[f"llama_{case['name']}_ids"])
+        finally:
+            eng.close()
+
+
+def test_llama_full_size_matches_reference():
+    """SmolLM2-135M shape (30 layers, 512 prompt ids, 128 greedy tokens), int8 weights."""
+    if not FULL_GOLDEN.exists():
+        pytest.skip("tests/golden/llama_smol_full.npz has not been generated")
+    gold = np.load(FULL_GOLDEN)
+    case = llama_full_case()
+    eng = Engine(case["config"], case["weights"], case["quant"])
+    try:
+        row = eng.prefill_logits(case["prompt"])
+        worst = float(np.abs(row.astype(np.float64) - gold["prefill_logits"]).max())
+        print(f"prefill logits max|diff| = {worst:.3g}", flush=True)
+        assert worst <= LOGIT_TOL
+        t0 = time.perf_counter()
+        ids = eng.generate(case)
+        dt = time.perf_counter() - t0
+        print(f"generate: 512 prompt + {ids.size} new tokens in {dt * 1e3:.1f} ms", flush=True)
+        np.testing.assert_array_equal(ids, gold["ids"])
+    finally:
+        eng.close()
+
+
+def test_llama_errors():
+    L = lib()
+    bad = LlamaConfig(vocab=16, hidden=30, layers=1, heads=4, kv_heads=2, intermediate=8, context=4, eps=1e-5,
+                      rope_theta=1e4)
+    assert not L.accel_llama_create(C.byref(bad))
+    assert b"invalid llama config" in L.accel_llama_last_error()
+    cfg = dict(vocab=32, hidden=16, layers=1, heads=2, kv_heads=1, intermediate=8, context=8, eps=1e-5,
+               rope_theta=1e4)
+    h = L.accel_llama_create(C.byref(LlamaConfig(**cfg)))
+    assert h
+    try:
+        w = np.zeros((5, 5), np.float32)
+        assert L.accel_llama_weight(h, 6, 0, w.ctypes.data_as(F32P), 5, 5) == 1
+        assert b"invalid weight" in L.accel_llama_last_error()
+        prompt = np.array([1, 2], np.int32)
+        out = np.zeros(4, np.int32)
+        n = C.c_int32()
+        assert L.accel_llama_generate(h, prompt.ctypes.data_as(I32P), 2, 4, -1, 0.0, 0, 0, out.ctypes.data_as(I32P),
+                                      C.byref(n)) == 1
+        assert b"incomplete" in L.accel_llama_last_error()
+        weights, _ = llama_weights(cfg, 5, quantize=False)
+        eng = Engine.__new__(Engine)
+        eng.L, eng.config, eng.h = L, cfg, h
+        for (kind, layer, wt) in weights:
+            wt = np.ascontiguousarray(wt, np.float32)
+            rows, cols = (wt.shape[0], 1) if wt.ndim == 1 else wt.shape
+            assert L.accel_llama_weight(h, kind, layer, wt.ctypes.data_as(F32P), rows, cols) == 0
+        oov = np.array([1, 99], np.int32)
+        assert L.accel_llama_forward_ids(h, oov.ctypes.data_as(I32P), 2, 1) == 1
+        assert b"outside the vocabulary" in L.accel_llama_last_error()
+        long = np.ones(9, np.int32)
+        assert L.accel_llama_forward_ids(h, long.ctypes.data_as(I32P), 9, 1) == 1
+        assert b"exceeds context" in L.accel_llama_last_error()
+    finally:
+        L.accel_llama_destroy(h)

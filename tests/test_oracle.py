@@ -23,12 +23,6 @@ from oracle_ctypes import (F32P, I32P, LlamaConfig, bits, fill_lcg, from_bits, m
 GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_outputs.npz"
 
 
-@pytest.fixture(scope="module")
-def gold():
-    with np.load(GOLDEN, allow_pickle=False) as z:
-        return {k: z[k] for k in z.files}
-
-
 def same_bits(got, want):
     got = np.asarray(got, np.float32)
     want = np.asarray(want, np.float32)
