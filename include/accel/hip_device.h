@@ -6,6 +6,8 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
+#include <vector>
 
 #include "accel/runtime.h"
 
@@ -22,6 +24,10 @@ struct FusedEpilogue {
   Activation activation = Activation::None;
   const float* residual = nullptr;
 };
+
+// The MI355X device (also declared in accel/device.h; repeated here so that a source built
+// against another copy of accel/device.h, such as AccelEP's own, needs only this header).
+std::unique_ptr<Device> CreateHipDevice();
 
 // True for devices made by CreateHipDevice().
 bool IsHipDevice(const Device& device);
