@@ -126,15 +126,26 @@ void LaunchTranspose(const float* src, float* dst, int64_t rows, int64_t cols, h
 void LaunchResidualAdd(float* dest, const float* extra, int64_t count, hipStream_t stream);
 void LaunchSiluMul(float* gate, const float* up, int64_t count, hipStream_t stream);
 // Writes 1 into *bad if any id is out of range (the output rows of good ids are written).
+// The launchers below that take a `*_dev` pointer read that value (an id index or a
+// position) from device memory when it is non-null, so a decode step can be replayed from
+// a HIP graph; the scalar argument is used otherwise.
 void LaunchEmbedding(const int32_t* ids, const float* table, const int8_t* qtable, const float* row_scale, float* out,
-                     int64_t seq, int64_t hidden, int64_t vocab, int32_t* bad, hipStream_t stream);
+                     int64_t seq, int64_t hidden, int64_t vocab, int32_t* bad, hipStream_t stream,
+                     const int32_t* index_dev = nullptr);
 void LaunchRope(float* states, const float* cos_table, const float* sin_table, int64_t seq, int64_t heads,
-                int64_t head_dim, int64_t position, hipStream_t stream);
+                int64_t head_dim, int64_t position, hipStream_t stream, const int32_t* position_dev = nullptr);
 void LaunchCopy(void* dst, const void* src, size_t bytes, hipStream_t stream);
+// cache[*position_dev * row_elems + i] = src[i] for i < count.
+void LaunchAppendRows(const float* src, float* cache, int64_t count, int64_t row_elems, const int32_t* position_dev,
+                      hipStream_t stream);
+// state[0] += 1, state[1] += 1 (position and produced count of a decode loop).
+void LaunchAdvance(int32_t* state, hipStream_t stream);
+// max_position: with position_dev, the largest position the device word may hold.
 void LaunchAttention(const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position,
-                     int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream);
-// rng_inout is a device word holding the xorshift32 state.
+                     int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
+                     const int32_t* position_dev = nullptr, int64_t max_position = 0);
+// rng_inout is a device word holding the xorshift32 state; index_dev offsets `chosen`.
 void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
-                       int32_t top_k, hipStream_t stream);
+                       int32_t top_k, hipStream_t stream, const int32_t* index_dev = nullptr);
 
 }  // namespace accel_hip

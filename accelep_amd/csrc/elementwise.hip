@@ -93,9 +93,9 @@ __global__ void SiluMulKernel(float* gate, const float* up, int64_t count) {
 // SimEmbed (src/sim_embed.cc:9-20). Float table, or int8 table with a per-row scale
 // (value = float(q) * scale[id], the fl(q*s) a float table quantized per row holds).
 __global__ void EmbeddingKernel(const int32_t* ids, const float* table, const int8_t* qtable, const float* row_scale,
-                                float* out, int64_t hidden, int64_t vocab, int32_t* bad) {
+                                float* out, int64_t hidden, int64_t vocab, int32_t* bad, const int32_t* index_dev) {
   const int64_t s = blockIdx.x;
-  const int32_t id = ids[s];
+  const int32_t id = ids[(index_dev != nullptr ? *index_dev : 0) + s];
   if (id < 0 || id >= vocab) {
     if (threadIdx.x == 0) *bad = 1;
     return;
@@ -113,7 +113,8 @@ __global__ void EmbeddingKernel(const int32_t* ids, const float* table, const in
 
 // SimRope (src/sim_rope.cc:5-21): rotate-half at absolute position (position + s).
 __global__ void RopeKernel(float* states, const float* cos_t, const float* sin_t, int64_t seq, int64_t heads,
-                           int64_t head_dim, int64_t position) {
+                           int64_t head_dim, int64_t position_arg, const int32_t* position_dev) {
+  const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
   const int64_t half = head_dim / 2;
   const int64_t total = seq * heads * half;
   for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
@@ -128,6 +129,24 @@ __global__ void RopeKernel(float* states, const float* cos_t, const float* sin_t
     const float x1 = row[half + i];
     row[i] = __fsub_rn(__fmul_rn(x0, cs[i]), __fmul_rn(x1, sn[i]));
     row[half + i] = __fadd_rn(__fmul_rn(x1, cs[half + i]), __fmul_rn(x0, sn[half + i]));
+  }
+}
+
+// SimAppendCache (src/sim_cache.cc:8-13): cache rows [position, position + rows) = src, with
+// the position read from device memory (a decode step replayed from a graph).
+__global__ void AppendRowsKernel(const float* src, float* cache, int64_t count, int64_t row_elems,
+                                 const int32_t* position_dev) {
+  float* dst = cache + static_cast<int64_t>(*position_dev) * row_elems;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    dst[i] = src[i];
+}
+
+// One decode step done: position and produced count both move on by one.
+__global__ void AdvanceKernel(int32_t* state) {
+  if (threadIdx.x == 0) {
+    state[0] = state[0] + 1;
+    state[1] = state[1] + 1;
   }
 }
 
@@ -198,21 +217,35 @@ void LaunchSiluMul(float* gate, const float* up, int64_t count, hipStream_t stre
 }
 
 void LaunchEmbedding(const int32_t* ids, const float* table, const int8_t* qtable, const float* row_scale, float* out,
-                     int64_t seq, int64_t hidden, int64_t vocab, int32_t* bad, hipStream_t stream) {
+                     int64_t seq, int64_t hidden, int64_t vocab, int32_t* bad, hipStream_t stream,
+                     const int32_t* index_dev) {
   if (seq <= 0 || hidden <= 0) return;
   if (seq > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Embedding is too large");
   hipLaunchKernelGGL(EmbeddingKernel, dim3(static_cast<uint32_t>(seq)), dim3(kBlock), 0, stream, ids, table, qtable,
-                     row_scale, out, hidden, vocab, bad);
+                     row_scale, out, hidden, vocab, bad, index_dev);
   Check(hipGetLastError(), "EmbeddingKernel launch");
 }
 
 void LaunchRope(float* states, const float* cos_table, const float* sin_table, int64_t seq, int64_t heads,
-                int64_t head_dim, int64_t position, hipStream_t stream) {
+                int64_t head_dim, int64_t position, hipStream_t stream, const int32_t* position_dev) {
   const int64_t total = seq * heads * (head_dim / 2);
   if (total <= 0) return;
   hipLaunchKernelGGL(RopeKernel, dim3(static_cast<uint32_t>(GridFor(total))), dim3(kBlock), 0, stream, states,
-                     cos_table, sin_table, seq, heads, head_dim, position);
+                     cos_table, sin_table, seq, heads, head_dim, position, position_dev);
   Check(hipGetLastError(), "RopeKernel launch");
+}
+
+void LaunchAppendRows(const float* src, float* cache, int64_t count, int64_t row_elems, const int32_t* position_dev,
+                      hipStream_t stream) {
+  if (count <= 0) return;
+  hipLaunchKernelGGL(AppendRowsKernel, dim3(static_cast<uint32_t>(GridFor(count))), dim3(kBlock), 0, stream, src,
+                     cache, count, row_elems, position_dev);
+  Check(hipGetLastError(), "AppendRowsKernel launch");
+}
+
+void LaunchAdvance(int32_t* state, hipStream_t stream) {
+  hipLaunchKernelGGL(AdvanceKernel, dim3(1), dim3(64), 0, stream, state);
+  Check(hipGetLastError(), "AdvanceKernel launch");
 }
 
 void LaunchCopy(void* dst, const void* src, size_t bytes, hipStream_t stream) {

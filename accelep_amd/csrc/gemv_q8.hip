@@ -295,11 +295,12 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNa
   const int ke32 = static_cast<int>(ke);
   const int kw32 = static_cast<int>(kw);
   // Whole batches (every row below ke, a workgroup-uniform test) issue all their loads at
-  // once and skip the clamps and selects. The last, partial batch goes two loads at a time,
-  // so its clamped form does not raise the register count of the kernel (which sets how many
-  // workgroups share a CU). sched_barrier keeps the scheduler from moving conversions between
+  // once and skip the clamps and selects. The last, partial batch goes half a batch at a
+  // time and stops where the rows end, so its clamped form does not raise the register count
+  // of the kernel (which sets how many workgroups share a CU) and a short K waits on memory
+  // once or twice. sched_barrier keeps the scheduler from moving conversions between
   // the loads, which would make each load wait for the one before it.
-  constexpr int kTailUnroll = 2;
+  constexpr int kTailUnroll = S::kUnroll / 2;
   static_assert(S::kUnroll % kTailUnroll == 0, "tail steps");
   for (int r0 = static_cast<int>(kb) + 2 * tid; r0 - 2 * tid < ke32; r0 += static_cast<int>(S::kBatchRows)) {
     if (r0 - 2 * tid + static_cast<int>(S::kBatchRows) <= ke32) {
@@ -311,6 +312,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNa
 #pragma unroll 1
       for (int u = 0; u < S::kUnroll; u += kTailUnroll) {
         const int rt = r0 + u * static_cast<int>(S::kStepRows);
+        if (rt - 2 * tid >= ke32) break;  // the rest of the batch lies past ke (workgroup-uniform)
         NarrowBatch<M, kTailUnroll> bt;
         LoadNarrowBatch<M, kTailUnroll, kZero, kRowScale, kPairA, true>(p, arow, rt, ke32, kw32, tbase, bt);
         __builtin_amdgcn_sched_barrier(0);

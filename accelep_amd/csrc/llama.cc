@@ -10,7 +10,9 @@
 //  * linear layers are int8 [in, out] with a per-output-column scale (the int8 GEMV for a
 //    decode step, the int8-panel MFMA GEMM for a prompt) or fp32 [in, out];
 //  * the sampler's xorshift state and the chosen ids stay in device memory, so a generate
-//    call copies the ids back once and, with no eos id, never waits on the GPU in between.
+//    call copies the ids back once and, with no eos id, never waits on the GPU in between;
+//  * the decode step reads its position and id index from device memory and is replayed
+//    from a HIP graph, so a token costs its kernels' time and not ~450 host launches.
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -94,7 +96,22 @@ struct Model {
   Linear lm_head;
   DevBuf rope_cos, rope_sin;
   DevBuf hidden, normed, query, key, value, mixed, gate, up, logits;
-  DevBuf chosen, prompt_ids, words;  // words: [0] embedding range flag, [1] sampler state
+  // words (int32): [0] embedding range flag, [1] sampler state, [2] position and [3] produced
+  // count of the decode loop (read by the kernels of a replayed decode step).
+  DevBuf chosen, prompt_ids, words;
+  // The decode step (forward of the last chosen id + advance of [2], [3]) as a HIP graph,
+  // captured on the second decode step of a generate (the first one stages the weights) and
+  // replayed for every step after it. Dropped when a weight changes or the product mode does.
+  void* decode_graph = nullptr;
+  bool decode_graph_exact = false;
+  bool decode_warm = false;
+
+  void DropDecodeGraph() {
+    if (decode_graph != nullptr) accel_hip_graph_destroy(decode_graph);
+    decode_graph = nullptr;
+    decode_warm = false;
+  }
+  ~Model() { DropDecodeGraph(); }
   std::vector<LayerWeights> layers;
   std::vector<DevBuf> k_cache, v_cache;
 
@@ -136,7 +153,9 @@ struct Model {
 
   // Forward over `seq` ids at ids[id_offset ..] (device int32) from position `filled`
   // (src/llama_model.cc:209-247). Leaves the last row's logits in `logits`.
-  void Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids) {
+  // With `state` (device int32 [position, produced], seq == 1) the position and the id index
+  // are read on the device, so the launches do not depend on the step.
+  void Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids, const int32_t* state = nullptr) {
     if (ids == nullptr || seq <= 0 || filled < 0 || seq > cfg.context || filled > cfg.context - seq)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
     const hipStream_t s = stream();
@@ -144,8 +163,9 @@ struct Model {
     const int64_t pos = filled;
     int32_t* flag = words.as<int32_t>();
     if (check_ids) Check(hipMemsetAsync(flag, 0, sizeof(int32_t), s), "hipMemsetAsync");
-    LaunchEmbedding(ids + id_offset, embed_f.as<float>(), embed_q.as<int8_t>(), embed_scale.as<float>(),
-                    hidden.as<float>(), seq, H, cfg.vocab, flag, s);
+    LaunchEmbedding(state != nullptr ? ids : ids + id_offset, embed_f.as<float>(), embed_q.as<int8_t>(),
+                    embed_scale.as<float>(), hidden.as<float>(), seq, H, cfg.vocab, flag, s,
+                    state != nullptr ? state + 1 : nullptr);
     if (check_ids) {
       int32_t bad = 0;
       Check(hipMemcpyAsync(&bad, flag, sizeof(bad), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
@@ -161,11 +181,17 @@ struct Model {
       Apply(l.q, normed.as<float>(), query.as<float>(), seq, nullptr);
       Apply(l.k, normed.as<float>(), key.as<float>(), seq, nullptr);
       Apply(l.v, normed.as<float>(), value.as<float>(), seq, nullptr);
-      LaunchRope(query.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.heads, hd, pos, s);
-      LaunchRope(key.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.kv_heads, hd, pos, s);
-      LaunchCopy(kc + pos * kv_row, key.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
-      LaunchCopy(vc + pos * kv_row, value.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
-      LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s);
+      LaunchRope(query.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.heads, hd, pos, s, state);
+      LaunchRope(key.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.kv_heads, hd, pos, s, state);
+      if (state != nullptr) {
+        LaunchAppendRows(key.as<float>(), kc, seq * kv_row, kv_row, state, s);
+        LaunchAppendRows(value.as<float>(), vc, seq * kv_row, kv_row, state, s);
+      } else {
+        LaunchCopy(kc + pos * kv_row, key.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
+        LaunchCopy(vc + pos * kv_row, value.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
+      }
+      LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s, state,
+                      cfg.context - 1);
       Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, hidden.as<float>());
       LaunchRmsNormRows(hidden.as<float>(), l.post_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
       Apply(l.gate, normed.as<float>(), gate.as<float>(), seq, nullptr);
@@ -176,6 +202,35 @@ struct Model {
     LaunchRmsNormRows(hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm.as<float>(),
                       normed.as<float>(), 1, H, cfg.eps, s);
     Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, nullptr);
+  }
+
+  // One decode step: forward of chosen[produced] at `position`, then both advance. The
+  // first call runs it directly (staging the weights and sizing the workspaces), the second
+  // captures it into a graph, and later calls replay the graph.
+  void DecodeStep(int32_t* state) {
+    const bool exact = Ctx().exact_products;
+    if (decode_graph != nullptr && decode_graph_exact != exact) DropDecodeGraph();
+    if (decode_graph == nullptr && !decode_warm) {
+      Forward(chosen.as<int32_t>(), 1, 0, false, state);
+      LaunchAdvance(state, stream());
+      decode_warm = true;
+      return;
+    }
+    if (decode_graph == nullptr) {
+      if (accel_hip_capture_begin() != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+      try {
+        Forward(chosen.as<int32_t>(), 1, 0, false, state);
+        LaunchAdvance(state, stream());
+      } catch (...) {
+        void* broken = nullptr;
+        accel_hip_capture_end(&broken);
+        if (broken != nullptr) accel_hip_graph_destroy(broken);
+        throw;
+      }
+      if (accel_hip_capture_end(&decode_graph) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+      decode_graph_exact = exact;
+    }
+    if (accel_hip_graph_launch(decode_graph, 1) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
   }
 
   // src/llama_model.cc:101-131.
@@ -191,11 +246,15 @@ struct Model {
     uint32_t* rng = words.as<uint32_t>() + 1;
     Check(hipMemcpyAsync(rng, &rng0, sizeof(rng0), hipMemcpyHostToDevice, stream()), "hipMemcpyAsync");
     Check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+    int32_t* state = words.as<int32_t>() + 2;
+    const int32_t state0[2] = {filled, 0};
+    Check(hipMemcpyAsync(state, state0, sizeof(state0), hipMemcpyHostToDevice, stream()), "hipMemcpyAsync");
+    Check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
     int32_t produced = 0;
     for (int32_t step = 0; step < max_new; ++step) {
       if (produced >= cfg.context) Fail(ACCEL_HIP_INVALID_ARGUMENT, "generation exceeded the token buffer");
-      LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>() + produced, cfg.vocab, temperature, rng, top_k,
-                        stream());
+      LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
+                        state + 1);
       produced += 1;
       if (eos_id >= 0) {
         // Only an eos id needs the chosen id on the host before the next step.
@@ -206,7 +265,7 @@ struct Model {
         if (id == eos_id) break;
       }
       if (filled >= cfg.context) break;
-      Forward(chosen.as<int32_t>(), 1, static_cast<int64_t>(produced) - 1, false);
+      DecodeStep(state);
       filled += 1;
     }
     if (produced > 0 && accel_hip_copy_d2h(out_ids, chosen.buffer(), static_cast<size_t>(produced) * sizeof(int32_t)) !=
@@ -380,6 +439,7 @@ ACCEL_LLAMA_API int accel_llama_weight(AccelLlama* handle, int32_t kind, int32_t
   }
   return Run([&] {
     std::lock_guard<std::mutex> lock(m->mu);
+    m->DropDecodeGraph();
     const size_t bytes = static_cast<size_t>(rows * cols) * sizeof(float);
     if (IsNorm(kind)) {
       DevBuf* slot = NormSlot(*m, kind, layer);
@@ -417,6 +477,7 @@ ACCEL_LLAMA_API int accel_llama_weight_q8(AccelLlama* handle, int32_t kind, int3
   }
   return Run([&] {
     std::lock_guard<std::mutex> lock(m->mu);
+    m->DropDecodeGraph();
     const size_t bytes = static_cast<size_t>(rows * cols);
     const size_t sbytes = static_cast<size_t>(rows) * sizeof(float);
     if (kind == ACCEL_W_EMBED) {

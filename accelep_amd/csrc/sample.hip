@@ -94,7 +94,9 @@ __device__ Best BlockArgmax(Best b, float* sv, int64_t* si) {
 }
 
 __global__ __launch_bounds__(kThreads) void SampleKernel(const float* logits, int32_t* chosen, int64_t vocab,
-                                                         float temperature, uint32_t* rng, int32_t top_k) {
+                                                         float temperature, uint32_t* rng, int32_t top_k,
+                                                         const int32_t* index_dev) {
+  if (index_dev != nullptr) chosen += *index_dev;  // the slot is read from device memory
   __shared__ float sv[kWaves];
   __shared__ int64_t si[kWaves];
   __shared__ double sd[kWaves];
@@ -266,9 +268,9 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* logits, in
 }  // namespace
 
 void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
-                       int32_t top_k, hipStream_t stream) {
+                       int32_t top_k, hipStream_t stream, const int32_t* index_dev) {
   hipLaunchKernelGGL(SampleKernel, dim3(1), dim3(kThreads), 0, stream, logits, chosen, vocab, temperature, rng_inout,
-                     top_k);
+                     top_k, index_dev);
   Check(hipGetLastError(), "SampleKernel launch");
 }
 

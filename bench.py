@@ -205,6 +205,70 @@ def bench_prefill(hip, steps, warmup, rng):
     return per, 2 * m * k * n / (per * 1e-3) / 1e12
 
 
+SMOL = dict(vocab=49152, hidden=576, layers=30, heads=9, kv_heads=3, intermediate=1536, context=640, eps=1e-5,
+            rope_theta=100000.0)
+
+
+def bench_llama(hip, rng, reps=3):
+    """SmolLM2-135M-shape Llama on the GPU (accel_llama_*): random int8 weights with per-row
+    scales, 512 prompt ids, greedy. Prefill = generate with one new token; decode = the extra
+    time of 128 more tokens. Best of `reps`."""
+    from accelep_amd.capi import F32P, I8P, I32P, LlamaConfig
+
+    L = hip.L
+    cfg = SMOL
+    h = L.accel_llama_create(C.byref(LlamaConfig(**cfg)))
+    if not h:
+        raise RuntimeError(L.accel_llama_last_error().decode())
+    H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
+    hd = H // cfg["heads"]
+    shapes = {6: (cfg["heads"] * hd, H), 7: (cfg["kv_heads"] * hd, H), 8: (cfg["kv_heads"] * hd, H),
+              9: (H, cfg["heads"] * hd), 10: (I, H), 11: (I, H), 12: (H, I)}
+
+    def q8(kind, layer, rows, cols):
+        q = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+        s = np.full(rows, 0.02 / 127 * 3, np.float32)
+        assert L.accel_llama_weight_q8(h, kind, layer, q.ctypes.data_as(I8P), s.ctypes.data_as(F32P), rows,
+                                       cols) == 0, L.accel_llama_last_error()
+
+    def norm(kind, layer):
+        w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        assert L.accel_llama_weight(h, kind, layer, w.ctypes.data_as(F32P), H, 1) == 0
+
+    try:
+        q8(1, -1, V, H)
+        q8(3, -1, V, H)
+        norm(2, -1)
+        for layer in range(cfg["layers"]):
+            norm(4, layer)
+            norm(5, layer)
+            for kind, (rows, cols) in shapes.items():
+                q8(kind, layer, rows, cols)
+        prompt = rng.integers(0, V, size=512).astype(np.int32)
+        out = np.zeros(129, np.int32)
+        count = C.c_int32()
+
+        def generate(new):
+            t0 = time.perf_counter()
+            rc = L.accel_llama_generate(h, prompt.ctypes.data_as(I32P), prompt.size, new, -1, 0.0, 0, 0,
+                                        out.ctypes.data_as(I32P), C.byref(count))
+            dt = time.perf_counter() - t0
+            if rc != 0:
+                raise RuntimeError(L.accel_llama_last_error().decode())
+            return dt
+
+        generate(129)  # warm-up: staging of the int8 weights, workspaces
+        pre = min(generate(1) for _ in range(reps))
+        full = min(generate(129) for _ in range(reps))
+        decode = max(full - pre, 1e-9)
+        return {"prefill_ms": round(pre * 1e3, 2), "prefill_tok_s": round(512 / pre, 1),
+                "decode_ms_per_token": round(decode / 128 * 1e3, 4), "decode_tok_s": round(128 / decode, 1),
+                "config": "SmolLM2-135M shape (30 layers, hidden 576, 9/3 heads, inter 1536, vocab 49152), "
+                          "int8 weights, 512 prompt ids, 128 greedy tokens, wall clock, best of 3"}
+    finally:
+        L.accel_llama_destroy(h)
+
+
 def calibrate_traffic(hip):
     """One residual add over 16 Mi floats: a streaming kernel of known HBM traffic (128 MiB read,
     64 MiB written) whose FETCH_SIZE / WRITE_SIZE scale the GEMV's counters to bytes."""
@@ -254,6 +318,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--only-llama", action="store_true", help="run only the Llama decode leg (for profiling)")
     ap.add_argument("--no-graph", action="store_true", help="launch each step directly instead of from HIP graphs")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one residual add of known traffic (for profiler counter scaling)")
@@ -271,6 +336,10 @@ def main():
     hip = Hip()
     log(f"device {hip.arch}")
 
+    if args.only_llama:
+        llama = bench_llama(hip, np.random.default_rng(11))
+        print(json.dumps({"llama_decode": llama}), flush=True)
+        return
     if args.calibrate:
         calibrate_traffic(hip)
     per1, gbs1 = bench_gemv(hip, 1, args.steps, args.warmup, COPIES, rng)
@@ -299,7 +368,10 @@ def main():
                                              "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "steps": steps4,
                                              "config": "X[2048,4096] @ int8 W[4096,14336] + RMSNorm(eps 1e-5)"}
         log(f"prefill int8+rms: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
-        secondary["decode_tok_s"] = None
+        llama = bench_llama(hip, np.random.default_rng(11))
+        secondary["llama_decode"] = llama
+        log(f"llama: prefill {llama['prefill_ms']} ms ({llama['prefill_tok_s']} tok/s), "
+            f"decode {llama['decode_ms_per_token']} ms/token ({llama['decode_tok_s']} tok/s)")
 
     cpu = None
     if not args.no_cpu:
