@@ -1,13 +1,15 @@
-// Causal grouped-query attention (SimAttend, src/sim_attend.cc:9-46). One workgroup per
-// (query row, head): query s sees keys 0..position+s, head h reads kv head
-// h / (heads / kv_heads), scores = (q . k) * (1 / sqrt(head_dim)), softmax with the max
-// subtracted, out[d] = sum_t (p_t / sum) * v[t][d].
+// Causal grouped-query attention (SimAttend, src/sim_attend.cc:9-46): query s sees keys
+// 0..position+s, head h reads kv head h / (heads / kv_heads), scores = (q . k) / sqrt(head_dim),
+// softmax with the max subtracted, out[d] = sum_t (p_t / sum) * v[t][d].
+//
+// For a prompt (seq > 4), one 512-thread workgroup per (query row, head) holds all of that
+// row's scores in LDS. For a decode step the positions are split over workgroups
+// (AttentionChunkKernel + AttentionCombineKernel below).
 //
 // Each dot product runs over d in order with separately rounded products, as the
-// reference does, so scores match it bit for bit; exp, the softmax sum (a fixed tree) and
-// the weighted sum (8 interleaved partial sums per d at head_dim 64, combined in order)
-// differ from the reference's sequential loops only by rounding. 512 threads per (query
-// row, head): a decode step has few such rows, so each spreads over a whole CU.
+// reference does, so scores match it bit for bit; exp, the softmax sums and the weighted
+// sums (interleaved partial sums combined in a fixed order) differ from the reference's
+// sequential loops only by rounding.
 #include "device_common.h"
 
 namespace accel_hip {
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(kThreads) void AttentionKernel(const float* q, cons
   __shared__ float lds_scores[kLdsScores];
   __shared__ float qs[256];
   __shared__ float red[kThreads / 64];
-  __shared__ float acc_part[kThreads];
+  __shared__ float acc_part[kThreads * 4];  // [group][column]: groups * head_dim <= 4 * kThreads
 
   const int64_t s = blockIdx.x / heads;
   const int64_t h = blockIdx.x % heads;
@@ -91,29 +93,57 @@ __global__ __launch_bounds__(kThreads) void AttentionKernel(const float* q, cons
   for (int64_t t = tid; t < total; t += kThreads) scores[t] = __fdiv_rn(scores[t], sum);
   __syncthreads();
 
-  // out[d] = sum_t p_t * v[t][d]: thread (g, d) adds t = g, g + G, ... (G groups), then
-  // the G partial sums are added in group order.
-  const int64_t groups = kThreads / head_dim;
-  const int64_t d = tid % head_dim;
-  const int64_t g = tid / head_dim;
-  float acc = 0.f;
+  // out[d] = sum_t p_t * v[t][d]. Thread (g, c) adds t = g, g + G, ... (G groups) for the
+  // columns of chunk c (4 columns, one 16-byte load, when kVec > 0; else 1 column); then the G
+  // partial sums of each column are added in group order.
+  constexpr int kCols = kVec > 0 ? 4 : 1;
+  const int64_t chunks = head_dim / kCols;
+  const int64_t groups = kThreads / chunks;
+  const int64_t c = tid % chunks;
+  const int64_t g = tid / chunks;
+  float acc[kCols];
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) acc[j] = 0.f;
   if (g < groups) {
-    const float* vcol = v + kv * head_dim + d;
+    const float* vcol = v + kv * head_dim + c * kCols;
     const int64_t vstride = kv_heads * head_dim;
+    auto load = [&](int64_t t, float (&x)[kCols]) {
+      if (kVec > 0) {
+        const float4 q4 = *reinterpret_cast<const float4*>(vcol + t * vstride);
+        x[0] = q4.x;
+        x[1 % kCols] = q4.y;
+        x[2 % kCols] = q4.z;
+        x[3 % kCols] = q4.w;
+      } else {
+        x[0] = vcol[t * vstride];
+      }
+    };
     int64_t t = g;
     for (; t + 3 * groups < total; t += 4 * groups) {
-      const float v0 = vcol[t * vstride];
-      const float v1 = vcol[(t + groups) * vstride];
-      const float v2 = vcol[(t + 2 * groups) * vstride];
-      const float v3 = vcol[(t + 3 * groups) * vstride];
-      acc = __fadd_rn(acc, __fmul_rn(scores[t], v0));
-      acc = __fadd_rn(acc, __fmul_rn(scores[t + groups], v1));
-      acc = __fadd_rn(acc, __fmul_rn(scores[t + 2 * groups], v2));
-      acc = __fadd_rn(acc, __fmul_rn(scores[t + 3 * groups], v3));
+      float x0[kCols], x1[kCols], x2[kCols], x3[kCols];
+      load(t, x0);
+      load(t + groups, x1);
+      load(t + 2 * groups, x2);
+      load(t + 3 * groups, x3);
+#pragma unroll
+      for (int j = 0; j < kCols; ++j) {
+        acc[j] = __fadd_rn(acc[j], __fmul_rn(scores[t], x0[j]));
+        acc[j] = __fadd_rn(acc[j], __fmul_rn(scores[t + groups], x1[j]));
+        acc[j] = __fadd_rn(acc[j], __fmul_rn(scores[t + 2 * groups], x2[j]));
+        acc[j] = __fadd_rn(acc[j], __fmul_rn(scores[t + 3 * groups], x3[j]));
+      }
     }
-    for (; t < total; t += groups) acc = __fadd_rn(acc, __fmul_rn(scores[t], vcol[t * vstride]));
+    for (; t < total; t += groups) {
+      float x0[kCols];
+      load(t, x0);
+#pragma unroll
+      for (int j = 0; j < kCols; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(scores[t], x0[j]));
+    }
   }
-  acc_part[tid] = acc;
+  // acc_part[g][column]
+#pragma unroll
+  for (int j = 0; j < kCols; ++j)
+    if (g < groups) acc_part[g * head_dim + c * kCols + j] = acc[j];
   __syncthreads();
   if (tid < head_dim) {
     float o = acc_part[tid];
@@ -122,46 +152,213 @@ __global__ __launch_bounds__(kThreads) void AttentionKernel(const float* q, cons
   }
 }
 
+// ---- decode: positions split over workgroups --------------------------------------------
+// A decode step has seq * heads = 9 (query row, head) pairs: one workgroup each would leave
+// the GPU idle. Here each pair's positions are cut into 64-position chunks, one workgroup per
+// (pair, chunk): it writes the chunk's max score m, l = sum exp(score - m) and the unscaled
+// sum acc[d] = sum exp(score - m) * v[t][d]; a second kernel combines the chunks with the
+// usual rescaling, out[d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c. Scores are
+// the reference's bits; the softmax differs from its global-max form only by rounding.
+constexpr int kChunk = 64;
+constexpr int kSplitThreads = 256;
+
+template <int kVec>
+__global__ __launch_bounds__(kSplitThreads) void AttentionChunkKernel(const float* q, const float* k, const float* v,
+                                                                      int64_t seq, int64_t position_arg,
+                                                                      int64_t heads, int64_t kv_heads,
+                                                                      int64_t head_dim, int64_t chunks,
+                                                                      float* partial, const int32_t* position_dev) {
+  __shared__ float qs[256];
+  __shared__ float es[kChunk];
+  __shared__ float acc_part[kSplitThreads * 4];
+  __shared__ float red[2];
+  const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
+  const int64_t row = blockIdx.x;  // s * heads + h
+  const int64_t c = blockIdx.y;
+  const int64_t s = row / heads;
+  const int64_t h = row % heads;
+  const int64_t kv = h / (heads / kv_heads);
+  const int64_t total = position + s + 1;
+  const int64_t t0 = c * kChunk;
+  const int tid = threadIdx.x;
+  float* out = partial + (row * chunks + c) * (2 + head_dim);
+  if (t0 >= total) {  // nothing in this chunk (the position is read on the device)
+    if (tid == 0) {
+      out[0] = -INFINITY;
+      out[1] = 0.f;
+    }
+    for (int64_t d = tid; d < head_dim; d += kSplitThreads) out[2 + d] = 0.f;
+    return;
+  }
+  const int64_t n = min<int64_t>(kChunk, total - t0);
+  for (int64_t d = tid; d < head_dim; d += kSplitThreads) qs[d] = q[row * head_dim + d];
+  __syncthreads();
+  const float scale = __fdiv_rn(1.f, __fsqrt_rn(static_cast<float>(head_dim)));
+  if (tid < n) es[tid] = __fmul_rn(Dot<kVec>(qs, k + ((t0 + tid) * kv_heads + kv) * head_dim, head_dim), scale);
+  __syncthreads();
+  if (tid < 64) {  // wave 0: chunk max, exps, their sum
+    const float x = tid < n ? es[tid] : -INFINITY;
+    float m = x;
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float e = tid < n ? expf(__fsub_rn(x, m)) : 0.f;
+    if (tid < n) es[tid] = e;
+    float l = e;
+    for (int off = 32; off > 0; off >>= 1) l = __fadd_rn(l, __shfl_xor(l, off));
+    if (tid == 0) {
+      red[0] = m;
+      red[1] = l;
+    }
+  }
+  __syncthreads();
+  // acc[d] over the chunk: thread (g, col chunk) adds positions g, g + G, ...
+  constexpr int kCols = kVec > 0 ? 4 : 1;
+  const int64_t col_chunks = head_dim / kCols;
+  const int64_t groups = kSplitThreads / col_chunks;
+  const int64_t cc = tid % col_chunks;
+  const int64_t g = tid / col_chunks;
+  float acc[kCols];
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) acc[j] = 0.f;
+  if (g < groups) {
+    const float* vcol = v + kv * head_dim + cc * kCols;
+    const int64_t vstride = kv_heads * head_dim;
+    for (int64_t t = g; t < n; t += groups) {
+      const float e = es[t];
+      if (kVec > 0) {
+        const float4 x4 = *reinterpret_cast<const float4*>(vcol + (t0 + t) * vstride);
+        const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+        for (int j = 0; j < kCols; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(e, xs[j]));
+      } else {
+        acc[0] = __fadd_rn(acc[0], __fmul_rn(e, vcol[(t0 + t) * vstride]));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kCols; ++j) acc_part[g * head_dim + cc * kCols + j] = acc[j];
+  }
+  __syncthreads();
+  for (int64_t d = tid; d < head_dim; d += kSplitThreads) {
+    float o = acc_part[d];
+    for (int64_t gg = 1; gg < groups; ++gg) o = __fadd_rn(o, acc_part[gg * head_dim + d]);
+    out[2 + d] = o;
+  }
+  if (tid == 0) {
+    out[0] = red[0];
+    out[1] = red[1];
+  }
+}
+
+constexpr int kMaxChunks = 1024;  // kMaxChunks * kChunk positions: 65536
+
+// One workgroup of 64 threads per (query row, head). The chunks' (m, l) pairs are loaded in
+// parallel into LDS and turned into weights w_c = e^(m_c - M) (0 for an empty chunk), then
+// each thread adds w_c * acc_c[d] over the chunks with its loads issued 8 at a time.
+__global__ __launch_bounds__(64) void AttentionCombineKernel(const float* partial, float* out, int64_t chunks,
+                                                             int64_t head_dim) {
+  __shared__ float wts[kMaxChunks];
+  __shared__ float lsum[kMaxChunks];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t stride = 2 + head_dim;
+  const float* p = partial + row * chunks * stride;
+  float big = -INFINITY;
+  for (int64_t c = tid; c < chunks; c += 64) {
+    wts[c] = p[c * stride];
+    lsum[c] = p[c * stride + 1];
+    big = fmaxf(big, wts[c]);
+  }
+  for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+  __syncthreads();
+  for (int64_t c = tid; c < chunks; c += 64) wts[c] = wts[c] == -INFINITY ? 0.f : expf(__fsub_rn(wts[c], big));
+  __syncthreads();
+  float l = 0.f;
+  for (int64_t c = 0; c < chunks; ++c) l = __fadd_rn(l, __fmul_rn(wts[c], lsum[c]));
+  for (int64_t d = tid; d < head_dim; d += 64) {
+    float o = 0.f;
+    int64_t c = 0;
+    for (; c + 8 <= chunks; c += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = p[(c + u) * stride + 2 + d];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o = __fadd_rn(o, __fmul_rn(wts[c + u], x[u]));
+    }
+    for (; c < chunks; ++c) o = __fadd_rn(o, __fmul_rn(wts[c], p[c * stride + 2 + d]));
+    out[row * head_dim + d] = __fdiv_rn(o, l);
+  }
+}
+
+constexpr int64_t kSplitMaxSeq = 4;
+
 }  // namespace
+
+size_t AttentionWorkBytes(int64_t seq, int64_t heads, int64_t max_position, int64_t head_dim) {
+  const int64_t rows = max_position + seq;
+  if (seq <= kSplitMaxSeq) {
+    const int64_t chunks = (rows + kChunk - 1) / kChunk;
+    return static_cast<size_t>(seq * heads * chunks * (2 + head_dim)) * sizeof(float);
+  }
+  if (rows > kLdsScores) return static_cast<size_t>(seq * heads * rows) * sizeof(float);
+  return 0;
+}
 
 void LaunchAttention(const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position,
                      int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream, const int32_t* position_dev,
-                     int64_t max_position) {
+                     int64_t max_position, float* work, size_t work_bytes) {
   if (seq <= 0 || heads <= 0) return;
   if (head_dim <= 0 || head_dim > 256) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention head_dim must be in 1..256");
   const int64_t blocks = seq * heads;
   if (blocks > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
-  // With a device position the scores must fit the largest position it can hold.
-  const int64_t rows = (position_dev != nullptr ? max_position : position) + seq;
-  float* spill = nullptr;
-  if (rows > kLdsScores) {
-    Context& ctx = Scratch(static_cast<size_t>(blocks * rows) * sizeof(float));
-    spill = static_cast<float*>(ctx.workspace);
+  // With a device position the scratch must fit the largest position it can hold.
+  const int64_t top = position_dev != nullptr ? max_position : position;
+  const int64_t rows = top + seq;
+  const size_t need = AttentionWorkBytes(seq, heads, top, head_dim);
+  float* scratch = nullptr;
+  if (need > 0) {
+    if (work != nullptr) {
+      if (work_bytes < need) Fail(ACCEL_HIP_INVALID_ARGUMENT, "attention scratch is too small");
+      scratch = work;
+    } else {
+      scratch = static_cast<float*>(Scratch(need).workspace);
+    }
   }
-  const bool aligned = (reinterpret_cast<uintptr_t>(k) % 16 == 0) && head_dim % 4 == 0;
+  const bool aligned = (reinterpret_cast<uintptr_t>(k) % 16 == 0) && (reinterpret_cast<uintptr_t>(v) % 16 == 0) &&
+                       head_dim % 4 == 0;
+  const int vec = aligned ? static_cast<int>(head_dim) : 0;
+  if (seq <= kSplitMaxSeq) {
+    const int64_t chunks = (rows + kChunk - 1) / kChunk;
+    if (chunks > kMaxChunks) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention context is too long for a decode step");
+    const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(chunks)), block(kSplitThreads);
+#define ACCEL_ATTN_CHUNK(V)                                                                                        \
+  hipLaunchKernelGGL(AttentionChunkKernel<V>, grid, block, 0, stream, q, k, v, seq, position, heads, kv_heads, \
+                     head_dim, chunks, scratch, position_dev)
+    switch (vec) {
+      case 16: ACCEL_ATTN_CHUNK(4); break;
+      case 32: ACCEL_ATTN_CHUNK(8); break;
+      case 64: ACCEL_ATTN_CHUNK(16); break;
+      case 128: ACCEL_ATTN_CHUNK(32); break;
+      default: ACCEL_ATTN_CHUNK(0); break;
+    }
+#undef ACCEL_ATTN_CHUNK
+    Check(hipGetLastError(), "AttentionChunkKernel launch");
+    hipLaunchKernelGGL(AttentionCombineKernel, dim3(static_cast<uint32_t>(blocks)), dim3(64), 0, stream, scratch, out,
+                       chunks, head_dim);
+    Check(hipGetLastError(), "AttentionCombineKernel launch");
+    return;
+  }
+  float* spill = rows > kLdsScores ? scratch : nullptr;
   const dim3 grid(static_cast<uint32_t>(blocks)), block(kThreads);
-  switch (aligned ? head_dim : 0) {
-    case 16:
-      hipLaunchKernelGGL(AttentionKernel<4>, grid, block, 0, stream, q, k, v, out, seq, position, heads, kv_heads,
-                         head_dim, spill, rows, position_dev);
-      break;
-    case 32:
-      hipLaunchKernelGGL(AttentionKernel<8>, grid, block, 0, stream, q, k, v, out, seq, position, heads, kv_heads,
-                         head_dim, spill, rows, position_dev);
-      break;
-    case 64:
-      hipLaunchKernelGGL(AttentionKernel<16>, grid, block, 0, stream, q, k, v, out, seq, position, heads, kv_heads,
-                         head_dim, spill, rows, position_dev);
-      break;
-    case 128:
-      hipLaunchKernelGGL(AttentionKernel<32>, grid, block, 0, stream, q, k, v, out, seq, position, heads, kv_heads,
-                         head_dim, spill, rows, position_dev);
-      break;
-    default:
-      hipLaunchKernelGGL(AttentionKernel<0>, grid, block, 0, stream, q, k, v, out, seq, position, heads, kv_heads,
-                         head_dim, spill, rows, position_dev);
-      break;
+#define ACCEL_ATTN(V)                                                                                          \
+  hipLaunchKernelGGL(AttentionKernel<V>, grid, block, 0, stream, q, k, v, out, seq, position, heads, kv_heads, \
+                     head_dim, spill, rows, position_dev)
+  switch (vec) {
+    case 16: ACCEL_ATTN(4); break;
+    case 32: ACCEL_ATTN(8); break;
+    case 64: ACCEL_ATTN(16); break;
+    case 128: ACCEL_ATTN(32); break;
+    default: ACCEL_ATTN(0); break;
   }
+#undef ACCEL_ATTN
   Check(hipGetLastError(), "AttentionKernel launch");
 }
 

@@ -74,6 +74,9 @@ inline size_t StagedTileBytes(int64_t k, int64_t n) {
 // The staged copy of the [k, n] int8 matrix at q, built on first use; nullptr when q is not
 // inside a live allocation of this library (then the raw layout is read).
 const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);
+// Incremented whenever a staged copy is freed: a HIP graph that captured kernels reading
+// staged copies is stale once this has moved.
+uint64_t StagingEpoch();
 // Every write into device memory through this library calls this for the written range;
 // staged copies of that allocation are dropped.
 void NoteDeviceWrite(const void* ptr, size_t bytes);
@@ -93,6 +96,13 @@ struct Epilogue {
   const float* rms_weight = nullptr;
   float rms_eps = 0.f;
   float* rms_out = nullptr;
+  // Column split of the output (split[0] == 0: none, C is one [m, n] matrix). Otherwise
+  // columns [0, split[0]) go to c as an [m, split[0]] matrix, [split[0], split[1]) to c2 and
+  // [split[1], n) to c3, each row-major with its own width: one matmul over concatenated
+  // weights fills several outputs (q/k/v, gate/up). Not combined with residual or rms.
+  int64_t split[2] = {0, 0};
+  float* c2 = nullptr;
+  float* c3 = nullptr;
   // True when only alpha*acc with alpha == 1 and nothing else applies.
   bool Identity() const {
     return alpha == 1.f && bias == nullptr && activation == ACCEL_HIP_ACT_NONE && residual == nullptr &&
@@ -135,15 +145,22 @@ void LaunchEmbedding(const int32_t* ids, const float* table, const int8_t* qtabl
 void LaunchRope(float* states, const float* cos_table, const float* sin_table, int64_t seq, int64_t heads,
                 int64_t head_dim, int64_t position, hipStream_t stream, const int32_t* position_dev = nullptr);
 void LaunchCopy(void* dst, const void* src, size_t bytes, hipStream_t stream);
-// cache[*position_dev * row_elems + i] = src[i] for i < count.
-void LaunchAppendRows(const float* src, float* cache, int64_t count, int64_t row_elems, const int32_t* position_dev,
-                      hipStream_t stream);
+// Rope on q [seq, heads, dim] in place and on k [seq, kv_heads, dim], with the rotated k and
+// v [seq, kv_heads, dim] stored into cache rows [position, position + seq).
+void LaunchRopeAppend(float* q, const float* k, const float* v, float* k_cache, float* v_cache, const float* cos_table,
+                      const float* sin_table, int64_t seq, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                      int64_t position, hipStream_t stream, const int32_t* position_dev = nullptr);
 // state[0] += 1, state[1] += 1 (position and produced count of a decode loop).
 void LaunchAdvance(int32_t* state, hipStream_t stream);
-// max_position: with position_dev, the largest position the device word may hold.
+// max_position: with position_dev, the largest position the device word may hold. work /
+// work_bytes: caller-owned scratch (at least AttentionWorkBytes); null uses the library
+// workspace.
 void LaunchAttention(const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position,
                      int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
-                     const int32_t* position_dev = nullptr, int64_t max_position = 0);
+                     const int32_t* position_dev = nullptr, int64_t max_position = 0, float* work = nullptr,
+                     size_t work_bytes = 0);
+// Scratch bytes LaunchAttention needs for these sizes (0 when none).
+size_t AttentionWorkBytes(int64_t seq, int64_t heads, int64_t max_position, int64_t head_dim);
 // rng_inout is a device word holding the xorshift32 state; index_dev offsets `chosen`.
 void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
                        int32_t top_k, hipStream_t stream, const int32_t* index_dev = nullptr);

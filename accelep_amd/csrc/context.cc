@@ -106,12 +106,17 @@ Context& Ctx() {
   return g_ctx;
 }
 
+// Workspaces only grow, and a replaced block is kept, not freed: a HIP graph captured before
+// the growth still holds the old address and may be replayed. Each growth at least doubles,
+// so the kept blocks add up to less than the current one.
+std::vector<void*> g_retired;
+
 Context& Scratch(size_t bytes) {
   Context& ctx = Ctx();
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (bytes > ctx.workspace_bytes) {
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
-    if (ctx.workspace != nullptr) Check(hipFree(ctx.workspace), "hipFree(workspace)");
+    if (ctx.workspace != nullptr) g_retired.push_back(ctx.workspace);
     ctx.workspace = nullptr;
     const size_t grown = std::max(bytes, ctx.workspace_bytes * 2);
     Check(hipMalloc(&ctx.workspace, grown), "hipMalloc(workspace)");
@@ -127,7 +132,7 @@ void* Temp(TempSlot slot, size_t bytes) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (bytes > sizes[slot]) {
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
-    if (buffers[slot] != nullptr) Check(hipFree(buffers[slot]), "hipFree(temp)");
+    if (buffers[slot] != nullptr) g_retired.push_back(buffers[slot]);
     buffers[slot] = nullptr;
     const size_t grown = std::max<size_t>(bytes, std::max<size_t>(sizes[slot] * 2, 256));
     Check(hipMalloc(&buffers[slot], grown), "hipMalloc(temp)");

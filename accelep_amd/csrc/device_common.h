@@ -34,6 +34,19 @@ __device__ __forceinline__ float ApplyEpilogue(float acc, int64_t i, int64_t j, 
   return v;
 }
 
+// Stores output element (i, j) of an [m, n] product, following the epilogue's column split.
+__device__ __forceinline__ void StoreC(float* c, int64_t i, int64_t j, int64_t n, const Epilogue& e, float v) {
+  if (e.split[0] == 0) {
+    c[i * n + j] = v;
+  } else if (j < e.split[0]) {
+    c[i * e.split[0] + j] = v;
+  } else if (j < e.split[1]) {
+    e.c2[i * (e.split[1] - e.split[0]) + (j - e.split[0])] = v;
+  } else {
+    e.c3[i * (n - e.split[1]) + (j - e.split[1])] = v;
+  }
+}
+
 // Signed byte b of a dword to float, exact.
 __device__ __forceinline__ float ByteToFloat(uint32_t word, int b) {
   return static_cast<float>(static_cast<int32_t>(word << (24 - 8 * b)) >> 24);

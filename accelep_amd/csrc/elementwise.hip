@@ -132,14 +132,50 @@ __global__ void RopeKernel(float* states, const float* cos_t, const float* sin_t
   }
 }
 
-// SimAppendCache (src/sim_cache.cc:8-13): cache rows [position, position + rows) = src, with
-// the position read from device memory (a decode step replayed from a graph).
-__global__ void AppendRowsKernel(const float* src, float* cache, int64_t count, int64_t row_elems,
+// The reference's Rope(q), Rope(k), AppendCache(k), AppendCache(v) (src/llama_model.cc:222-225)
+// as one pass: q and k rotated (rotate-half, same roundings as RopeKernel), the rotated k and
+// v written into cache rows [position, position + seq). q is rotated in place; k and v are
+// only read.
+__global__ void RopeAppendKernel(float* q, const float* k, const float* v, float* k_cache, float* v_cache,
+                                 const float* cos_t, const float* sin_t, int64_t seq, int64_t heads,
+                                 int64_t kv_heads, int64_t head_dim, int64_t position_arg,
                                  const int32_t* position_dev) {
-  float* dst = cache + static_cast<int64_t>(*position_dev) * row_elems;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < count;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    dst[i] = src[i];
+  const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
+  const int64_t half = head_dim / 2;
+  const int64_t q_pairs = seq * heads * half;
+  const int64_t k_pairs = seq * kv_heads * half;
+  const int64_t v_elems = seq * kv_heads * head_dim;
+  const int64_t total = q_pairs + k_pairs + v_elems;
+  const int64_t kv_row = kv_heads * head_dim;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (idx < q_pairs + k_pairs) {
+      const bool is_q = idx < q_pairs;
+      const int64_t e = is_q ? idx : idx - q_pairs;
+      const int64_t nh = is_q ? heads : kv_heads;
+      const int64_t i = e % half;
+      const int64_t sh = e / half;  // s * nh + h
+      const int64_t s = sh / nh;
+      const float* cs = cos_t + (position + s) * head_dim;
+      const float* sn = sin_t + (position + s) * head_dim;
+      const float* src = (is_q ? q : k) + sh * head_dim;
+      const float x0 = src[i];
+      const float x1 = src[half + i];
+      const float y0 = __fsub_rn(__fmul_rn(x0, cs[i]), __fmul_rn(x1, sn[i]));
+      const float y1 = __fadd_rn(__fmul_rn(x1, cs[half + i]), __fmul_rn(x0, sn[half + i]));
+      if (is_q) {
+        q[sh * head_dim + i] = y0;
+        q[sh * head_dim + half + i] = y1;
+      } else {
+        float* dst = k_cache + position * kv_row + sh * head_dim;
+        dst[i] = y0;
+        dst[half + i] = y1;
+      }
+    } else {
+      const int64_t e = idx - q_pairs - k_pairs;
+      v_cache[position * kv_row + e] = v[e];
+    }
+  }
 }
 
 // One decode step done: position and produced count both move on by one.
@@ -235,12 +271,14 @@ void LaunchRope(float* states, const float* cos_table, const float* sin_table, i
   Check(hipGetLastError(), "RopeKernel launch");
 }
 
-void LaunchAppendRows(const float* src, float* cache, int64_t count, int64_t row_elems, const int32_t* position_dev,
-                      hipStream_t stream) {
-  if (count <= 0) return;
-  hipLaunchKernelGGL(AppendRowsKernel, dim3(static_cast<uint32_t>(GridFor(count))), dim3(kBlock), 0, stream, src,
-                     cache, count, row_elems, position_dev);
-  Check(hipGetLastError(), "AppendRowsKernel launch");
+void LaunchRopeAppend(float* q, const float* k, const float* v, float* k_cache, float* v_cache, const float* cos_table,
+                      const float* sin_table, int64_t seq, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                      int64_t position, hipStream_t stream, const int32_t* position_dev) {
+  const int64_t total = seq * (heads + kv_heads) * (head_dim / 2) + seq * kv_heads * head_dim;
+  if (total <= 0) return;
+  hipLaunchKernelGGL(RopeAppendKernel, dim3(static_cast<uint32_t>(GridFor(total))), dim3(kBlock), 0, stream, q, k, v,
+                     k_cache, v_cache, cos_table, sin_table, seq, heads, kv_heads, head_dim, position, position_dev);
+  Check(hipGetLastError(), "RopeAppendKernel launch");
 }
 
 void LaunchAdvance(int32_t* state, hipStream_t stream) {

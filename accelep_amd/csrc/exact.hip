@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kGemvThreads) void ExactGemvKernel(const float* a, 
   }
 #pragma unroll
   for (int r = 0; r < kGemvMaxRows; ++r)
-    if (r < m) c[r * n + j] = ApplyEpilogue(acc[r], r, j, n, epi);
+    if (r < m) StoreC(c, r, j, n, epi, ApplyEpilogue(acc[r], r, j, n, epi));
 }
 
 constexpr int kTile = 64;
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kGemmThreads) void ExactGemmKernel(const float* a, 
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
       const int64_t j = col0 + tx + 16 * cc;
-      if (j < n) c[i * n + j] = ApplyEpilogue(acc[r][cc], i, j, n, epi);
+      if (j < n) StoreC(c, i, j, n, epi, ApplyEpilogue(acc[r][cc], i, j, n, epi));
     }
   }
 }

@@ -259,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r) {
         const int64_t gr = row_of(i, r);
         const int64_t gc = col_of(j);
-        if (gr < p.m && gc < p.n) p.c[gr * p.n + gc] = ApplyEpilogue(acc[i][j][r], gr, gc, p.n, p.epi);
+        if (gr < p.m && gc < p.n) StoreC(p.c, gr, gc, p.n, p.epi, ApplyEpilogue(acc[i][j][r], gr, gc, p.n, p.epi));
       }
 }
 

@@ -103,7 +103,7 @@ __device__ __forceinline__ void Emit(const GemvArgs& p, int split, int64_t mm, i
   if (p.splits > 1) {
     p.partials[(static_cast<int64_t>(split) * p.m + mm) * p.n + col] = s;
   } else {
-    p.c[mm * p.n + col] = ApplyEpilogue(__fmul_rn(s, ColScale(p, col)), mm, col, p.n, p.epi);
+    StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(s, ColScale(p, col)), mm, col, p.n, p.epi));
   }
 }
 
@@ -338,7 +338,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNa
         p.partials[(static_cast<int64_t>(split) * p.m + mm) * p.n + col] = s;
       } else {
         const float cs = p.mode == kScalePerRow ? 1.f : col_scale;
-        p.c[mm * p.n + col] = ApplyEpilogue(__fmul_rn(s, cs), mm, col, p.n, p.epi);
+        StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(s, cs), mm, col, p.n, p.epi));
       }
     }
   }
@@ -438,7 +438,7 @@ __global__ void SplitReduceKernel(const float* partials, int32_t splits, int64_t
     float cs = 1.f;
     if (scale != nullptr && mode == kScalePerCol) cs = scale[j];
     if (scale != nullptr && mode == kScaleConst) cs = scale[const_index];
-    c[idx] = ApplyEpilogue(__fmul_rn(s, cs), i, j, n, epi);
+    StoreC(c, i, j, n, epi, ApplyEpilogue(__fmul_rn(s, cs), i, j, n, epi));
   }
 }
 

@@ -4,7 +4,11 @@
 // The call sequence per layer is the reference's: RMSNorm, q/k/v projections, RoPE on q and
 // k, KV append, causal attention, o projection + residual, RMSNorm, gate/up, SiLU*up, down
 // projection + residual; then the final RMSNorm of the last row and the LM head. What
-// differs is where things live and how many passes there are:
+// differs is where things live and how many passes there are (9 kernels per layer where the
+// reference makes 15 device calls):
+//  * q/k/v and gate/up are one matmul each over concatenated weights, storing into the
+//    separate outputs (a column-split store); RoPE of q and k and both KV appends are one
+//    kernel;
 //  * the residual adds run in the o and down projections' stores (c = acc + hidden, in
 //    place), which gives the bits of the reference's MatMul + ResidualAdd pair;
 //  * linear layers are int8 [in, out] with a per-output-column scale (the int8 GEMV for a
@@ -71,18 +75,30 @@ class DevBuf {
   AccelHipBuffer b_{};
 };
 
-// A linear layer held as [in, out]: fp32, or int8 with one scale per output column.
+// A linear layer held as [in, out]: fp32, or int8 with one scale per output column. The
+// q/k/v projections share one such matrix (columns [q | k | v]) and so do gate/up
+// ([gate | up]): one matmul fills both or all three outputs through a column-split store.
+// Each part arrives through its own weight call; `filled` marks the parts loaded.
 struct Linear {
   DevBuf f;      // fp32 [in, out]
   DevBuf q;      // int8 [in, out]
   DevBuf scale;  // fp32 [out]
   int64_t in = 0, out = 0;
-  bool ready() const { return !f.empty() || !q.empty(); }
+  bool int8 = false;
+  uint32_t filled = 0, parts = 1;
+  bool ready() const { return (!f.empty() || !q.empty()) && filled == (1u << parts) - 1; }
+};
+
+// Where the HF weight of `kind` goes inside its Linear.
+struct Part {
+  Linear* linear = nullptr;
+  int index = 0, parts = 1;
+  int64_t col0 = 0, width = 0, in = 0, total = 0;
 };
 
 struct LayerWeights {
   DevBuf attn_norm, post_norm;
-  Linear q, k, v, o, gate, up, down;
+  Linear qkv, o, gu, down;
 };
 
 struct Model {
@@ -104,7 +120,11 @@ struct Model {
   // replayed for every step after it. Dropped when a weight changes or the product mode does.
   void* decode_graph = nullptr;
   bool decode_graph_exact = false;
+  uint64_t decode_graph_epoch = 0;
   bool decode_warm = false;
+  // Attention partials of a decode step ([heads][context / 64 chunks][2 + head_dim]): owned
+  // here so a captured step never points into a workspace that later grows.
+  DevBuf attn_work;
 
   void DropDecodeGraph() {
     if (decode_graph != nullptr) accel_hip_graph_destroy(decode_graph);
@@ -120,16 +140,14 @@ struct Model {
   bool Ready() const {
     if ((embed_f.empty() && embed_q.empty()) || final_norm.empty() || !lm_head.ready()) return false;
     for (const LayerWeights& l : layers)
-      if (l.attn_norm.empty() || l.post_norm.empty() || !l.q.ready() || !l.k.ready() || !l.v.ready() ||
-          !l.o.ready() || !l.gate.ready() || !l.up.ready() || !l.down.ready())
+      if (l.attn_norm.empty() || l.post_norm.empty() || !l.qkv.ready() || !l.o.ready() || !l.gu.ready() ||
+          !l.down.ready())
         return false;
     return true;
   }
 
-  // c[m, out] = a[m, in] @ W (+ residual in the store).
-  void Apply(const Linear& w, const float* a, float* c, int64_t m, const float* residual) {
-    Epilogue e;
-    e.residual = residual;
+  // c[m, out] = a[m, in] @ W with the epilogue in the store (residual, column split).
+  void Apply(const Linear& w, const float* a, float* c, int64_t m, const Epilogue& e) {
     Context& ctx = Ctx();
     if (!w.q.empty()) {
       Q8View v;
@@ -172,36 +190,37 @@ struct Model {
       Check(hipStreamSynchronize(s), "hipStreamSynchronize");
       if (bad != 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "token id is outside the vocabulary");
     }
-    const int64_t kv_row = static_cast<int64_t>(cfg.kv_heads) * hd;
+    const int64_t q_out = static_cast<int64_t>(cfg.heads) * hd, kv_out = static_cast<int64_t>(cfg.kv_heads) * hd;
+    Epilogue qkv;  // [q | k | v] -> query, key, value
+    qkv.split[0] = q_out;
+    qkv.split[1] = q_out + kv_out;
+    qkv.c2 = key.as<float>();
+    qkv.c3 = value.as<float>();
+    Epilogue gu;  // [gate | up] -> gate, up
+    gu.split[0] = inter;
+    gu.split[1] = 2 * inter;
+    gu.c2 = up.as<float>();
+    Epilogue residual;  // c = acc + hidden, written over hidden
+    residual.residual = hidden.as<float>();
     for (int32_t li = 0; li < cfg.layers; ++li) {
       LayerWeights& l = layers[static_cast<size_t>(li)];
       float* kc = k_cache[static_cast<size_t>(li)].as<float>();
       float* vc = v_cache[static_cast<size_t>(li)].as<float>();
       LaunchRmsNormRows(hidden.as<float>(), l.attn_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
-      Apply(l.q, normed.as<float>(), query.as<float>(), seq, nullptr);
-      Apply(l.k, normed.as<float>(), key.as<float>(), seq, nullptr);
-      Apply(l.v, normed.as<float>(), value.as<float>(), seq, nullptr);
-      LaunchRope(query.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.heads, hd, pos, s, state);
-      LaunchRope(key.as<float>(), rope_cos.as<float>(), rope_sin.as<float>(), seq, cfg.kv_heads, hd, pos, s, state);
-      if (state != nullptr) {
-        LaunchAppendRows(key.as<float>(), kc, seq * kv_row, kv_row, state, s);
-        LaunchAppendRows(value.as<float>(), vc, seq * kv_row, kv_row, state, s);
-      } else {
-        LaunchCopy(kc + pos * kv_row, key.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
-        LaunchCopy(vc + pos * kv_row, value.as<float>(), static_cast<size_t>(seq * kv_row) * sizeof(float), s);
-      }
+      Apply(l.qkv, normed.as<float>(), query.as<float>(), seq, qkv);
+      LaunchRopeAppend(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc, rope_cos.as<float>(),
+                       rope_sin.as<float>(), seq, cfg.heads, cfg.kv_heads, hd, pos, s, state);
       LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s, state,
-                      cfg.context - 1);
-      Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, hidden.as<float>());
+                      cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes);
+      Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, residual);
       LaunchRmsNormRows(hidden.as<float>(), l.post_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
-      Apply(l.gate, normed.as<float>(), gate.as<float>(), seq, nullptr);
-      Apply(l.up, normed.as<float>(), up.as<float>(), seq, nullptr);
+      Apply(l.gu, normed.as<float>(), gate.as<float>(), seq, gu);
       LaunchSiluMul(gate.as<float>(), up.as<float>(), seq * inter, s);
-      Apply(l.down, gate.as<float>(), hidden.as<float>(), seq, hidden.as<float>());
+      Apply(l.down, gate.as<float>(), hidden.as<float>(), seq, residual);
     }
     LaunchRmsNormRows(hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm.as<float>(),
                       normed.as<float>(), 1, H, cfg.eps, s);
-    Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, nullptr);
+    Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, Epilogue{});
   }
 
   // One decode step: forward of chosen[produced] at `position`, then both advance. The
@@ -209,7 +228,8 @@ struct Model {
   // captures it into a graph, and later calls replay the graph.
   void DecodeStep(int32_t* state) {
     const bool exact = Ctx().exact_products;
-    if (decode_graph != nullptr && decode_graph_exact != exact) DropDecodeGraph();
+    if (decode_graph != nullptr && (decode_graph_exact != exact || decode_graph_epoch != StagingEpoch()))
+      DropDecodeGraph();
     if (decode_graph == nullptr && !decode_warm) {
       Forward(chosen.as<int32_t>(), 1, 0, false, state);
       LaunchAdvance(state, stream());
@@ -229,6 +249,7 @@ struct Model {
       }
       if (accel_hip_capture_end(&decode_graph) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       decode_graph_exact = exact;
+      decode_graph_epoch = StagingEpoch();
     }
     if (accel_hip_graph_launch(decode_graph, 1) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
   }
@@ -308,28 +329,88 @@ bool ShapeOk(const Model& m, int32_t kind, int64_t rows, int64_t cols) {
   }
 }
 
-Linear* LinearSlot(Model& m, int32_t kind, int32_t layer) {
-  if (kind == ACCEL_W_LM_HEAD) return &m.lm_head;
-  if (layer < 0 || layer >= m.cfg.layers) return nullptr;
+Part PartOf(Model& m, int32_t kind, int32_t layer) {
+  const int64_t H = m.cfg.hidden, qo = static_cast<int64_t>(m.cfg.heads) * m.head_dim,
+                ko = static_cast<int64_t>(m.cfg.kv_heads) * m.head_dim, I = m.cfg.intermediate;
+  Part p;
+  if (kind == ACCEL_W_LM_HEAD) {
+    p.linear = &m.lm_head;
+    p.width = p.total = m.cfg.vocab;
+    p.in = H;
+    return p;
+  }
+  if (layer < 0 || layer >= m.cfg.layers) return p;
   LayerWeights& l = m.layers[static_cast<size_t>(layer)];
   switch (kind) {
     case ACCEL_W_Q:
-      return &l.q;
     case ACCEL_W_K:
-      return &l.k;
     case ACCEL_W_V:
-      return &l.v;
+      p.linear = &l.qkv;
+      p.parts = 3;
+      p.index = kind - ACCEL_W_Q;
+      p.col0 = kind == ACCEL_W_Q ? 0 : kind == ACCEL_W_K ? qo : qo + ko;
+      p.width = kind == ACCEL_W_Q ? qo : ko;
+      p.in = H;
+      p.total = qo + 2 * ko;
+      break;
     case ACCEL_W_O:
-      return &l.o;
+      p.linear = &l.o;
+      p.width = p.total = H;
+      p.in = qo;
+      break;
     case ACCEL_W_GATE:
-      return &l.gate;
     case ACCEL_W_UP:
-      return &l.up;
+      p.linear = &l.gu;
+      p.parts = 2;
+      p.index = kind - ACCEL_W_GATE;
+      p.col0 = kind == ACCEL_W_GATE ? 0 : I;
+      p.width = I;
+      p.in = H;
+      p.total = 2 * I;
+      break;
     case ACCEL_W_DOWN:
-      return &l.down;
+      p.linear = &l.down;
+      p.width = p.total = H;
+      p.in = I;
+      break;
     default:
-      return nullptr;
+      break;
   }
+  return p;
+}
+
+// Writes one part (its [in, width] block, already transposed) into its Linear.
+void UploadPart(const Part& p, bool int8, const void* block, const float* scale) {
+  Linear& w = *p.linear;
+  if (w.f.empty() && w.q.empty()) {
+    w.in = p.in;
+    w.out = p.total;
+    w.int8 = int8;
+    w.parts = static_cast<uint32_t>(p.parts);
+    w.filled = 0;
+    if (int8) {
+      w.q = DevBuf(static_cast<size_t>(p.in * p.total));
+      w.scale = DevBuf(static_cast<size_t>(p.total) * sizeof(float));
+    } else {
+      w.f = DevBuf(static_cast<size_t>(p.in * p.total) * sizeof(float));
+    }
+  } else if (w.int8 != int8) {
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "a projection group mixes int8 and float weights");
+  }
+  const size_t elem = int8 ? 1 : sizeof(float);
+  char* base = int8 ? w.q.as<char>() : w.f.as<char>();
+  Check(hipMemcpy2D(base + p.col0 * elem, static_cast<size_t>(p.total) * elem, block, static_cast<size_t>(p.width) * elem,
+                    static_cast<size_t>(p.width) * elem, static_cast<size_t>(p.in), hipMemcpyHostToDevice),
+        "hipMemcpy2D");
+  NoteBytesToDevice(static_cast<size_t>(p.in * p.width) * elem);
+  NoteDeviceWrite(base, static_cast<size_t>(p.in * p.total) * elem);  // drops a staged copy of the old bytes
+  if (int8) {
+    Check(hipMemcpy(w.scale.as<float>() + p.col0, scale, static_cast<size_t>(p.width) * sizeof(float),
+                    hipMemcpyHostToDevice),
+          "hipMemcpy");
+    NoteBytesToDevice(static_cast<size_t>(p.width) * sizeof(float));
+  }
+  w.filled |= 1u << p.index;
 }
 
 DevBuf* NormSlot(Model& m, int32_t kind, int32_t layer) {
@@ -415,6 +496,7 @@ ACCEL_LLAMA_API AccelLlama* accel_llama_create(const AccelLlamaConfig* config) {
     m->chosen = DevBuf(ctx * sizeof(int32_t));
     m->prompt_ids = DevBuf(ctx * sizeof(int32_t));
     m->words = DevBuf(64);
+    m->attn_work = DevBuf(AttentionWorkBytes(1, config->heads, config->context - 1, dim));
     for (int32_t l = 0; l < config->layers; ++l) {
       m->k_cache.emplace_back(k_n * f);
       m->v_cache.emplace_back(k_n * f);
@@ -454,15 +536,10 @@ ACCEL_LLAMA_API int accel_llama_weight(AccelLlama* handle, int32_t kind, int32_t
       m->embed_q = DevBuf();
       m->embed_scale = DevBuf();
     } else {
-      Linear* slot = LinearSlot(*m, kind, layer);
-      if (slot == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
+      const Part p = PartOf(*m, kind, layer);
+      if (p.linear == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
       const std::vector<float> t = Transposed(data, rows, cols);
-      Linear w;
-      w.in = cols;
-      w.out = rows;
-      w.f = DevBuf(bytes);
-      w.f.Upload(t.data(), bytes);
-      *slot = std::move(w);
+      UploadPart(p, false, t.data(), nullptr);
     }
   });
 }
@@ -489,17 +566,10 @@ ACCEL_LLAMA_API int accel_llama_weight_q8(AccelLlama* handle, int32_t kind, int3
       m->embed_f = DevBuf();
       return;
     }
-    Linear* slot = LinearSlot(*m, kind, layer);
-    if (slot == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
+    const Part p = PartOf(*m, kind, layer);
+    if (p.linear == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "unknown weight");
     const std::vector<int8_t> t = Transposed(q, rows, cols);
-    Linear w;
-    w.in = cols;
-    w.out = rows;
-    w.q = DevBuf(bytes);
-    w.q.Upload(t.data(), bytes);
-    w.scale = DevBuf(sbytes);
-    w.scale.Upload(row_scale, sbytes);
-    *slot = std::move(w);
+    UploadPart(p, true, t.data(), row_scale);
   });
 }
 

@@ -106,8 +106,20 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* logits, in
   const int tid = threadIdx.x;
 
   if (!(temperature > 0.f)) {
+    // 8 loads in flight per thread; Better is a total order (larger value, then smaller
+    // id), so the order in which candidates meet does not change the winner.
+    constexpr int kUnroll = 8;
     Best b{0.f, -1};
-    for (int64_t i = tid; i < vocab; i += kThreads) {
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * kThreads < vocab; i += kUnroll * kThreads) {
+      float v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) v[u] = logits[i + u * kThreads];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        if (!isnan(v[u])) b = Better(b, Best{v[u], i + u * kThreads});
+    }
+    for (; i < vocab; i += kThreads) {
       const float v = logits[i];
       if (!isnan(v)) b = Better(b, Best{v, i});
     }

@@ -41,6 +41,7 @@ std::map<Key, Entry> g_staged;
 size_t g_staged_bytes = 0;
 uint64_t g_tick = 0;
 std::atomic<bool> g_any{false};  // fast path for writes when nothing is staged
+std::atomic<uint64_t> g_epoch{0};  // counts dropped copies (a captured graph may hold one)
 constexpr size_t kStagedLimit = size_t(64) << 30;
 
 void FreeEntry(Entry& e) {
@@ -48,6 +49,7 @@ void FreeEntry(Entry& e) {
   Check(hipStreamSynchronize(Ctx().stream), "hipStreamSynchronize");
   Check(hipFree(e.data), "hipFree(staged)");
   g_staged_bytes -= e.bytes;
+  g_epoch.fetch_add(1);
 }
 
 void EvictFor(size_t bytes) {
@@ -88,6 +90,8 @@ const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream
   g_any.store(true);
   return dst;
 }
+
+uint64_t StagingEpoch() { return g_epoch.load(); }
 
 void NoteDeviceWrite(const void* ptr, size_t bytes) {
   if (!g_any.load() || ptr == nullptr) return;
