@@ -11,7 +11,8 @@
 //    next panel is fetched into registers while the current one feeds the MFMAs.
 //  * The int8 panel is dequantized on its way into LDS with the reference's rounding,
 //    w = (float(q) - float(zero)) * scale, so only the summation order differs from the
-//    reference's k-ascending loop.
+//    reference's k-ascending loop. Its bytes stay raw in registers while the current panel
+//    is multiplied, and the column scales are loaded once per workgroup.
 //  * Split-K over workgroups when the tile count cannot fill the GPU: partial tiles go to
 //    the workspace and a second kernel sums them in split order and applies the epilogue
 //    (deterministic, no synchronization between workgroups).
@@ -43,27 +44,33 @@ struct GemmArgs {
   Epilogue epi;
 };
 
-__device__ __forceinline__ float Dequant(const GemmArgs& p, int8_t qv, int64_t row, int64_t col) {
-  int64_t idx = p.const_index;
-  if (p.mode == kScalePerCol) idx = col;
-  if (p.mode == kScalePerRow) idx = row;
-  const float z = p.zero != nullptr ? static_cast<float>(p.zero[idx]) : 0.f;
-  return __fmul_rn(static_cast<float>(qv) - z, p.scale[idx]);
-}
-
 template <int BM, int BN, bool kQ8>
 struct Panels {
   // A: BM rows x 16 k, loaded as float4 along k. B fp32: 16 x BN as float4 along n.
-  // B int8: 16 x BN bytes.
+  // B int8: 16 x BN bytes, kBBytes consecutive columns of one row per thread, kept as loaded
+  // (dequantized only when stored to LDS, so the load is not waited for early).
   static constexpr int kAVec = BM * kBK / 4 / kThreads;  // float4 per thread
   static constexpr int kBVec = kQ8 ? 1 : BN * kBK / 4 / kThreads;
   static constexpr int kBBytes = BN * kBK / kThreads;  // int8 bytes per thread (4 or 8)
   float4 a[kAVec];
   float4 b[kBVec];
-  float bq[kQ8 ? kBBytes : 1];
+  uint32_t bq[kQ8 ? kBBytes / 4 : 1];
+  float row_scale;  // per-row mode: scale and zero of this thread's row
+  float row_zero;
 };
 
-template <int BM, int BN, bool kQ8>
+// Where thread `tid` puts its int8 bytes: row of the 16-row panel and first column.
+template <int BN>
+__device__ __forceinline__ void Q8Slot(int tid, int* row, int* c0) {
+  constexpr int kPerThread = BN * kBK / kThreads;
+  constexpr int kThreadsPerRow = BN / kPerThread;
+  *row = tid / kThreadsPerRow;
+  *c0 = (tid % kThreadsPerRow) * kPerThread;
+}
+
+// kFull: the tile lies inside [m, n], the chunk inside k and the rows are aligned, so the
+// loads need no checks.
+template <int BM, int BN, bool kQ8, bool kFull>
 __device__ __forceinline__ void LoadPanels(const GemmArgs& p, int64_t m0, int64_t n0, int64_t kc, int tid,
                                            Panels<BM, BN, kQ8>& r) {
   using P = Panels<BM, BN, kQ8>;
@@ -75,6 +82,10 @@ __device__ __forceinline__ void LoadPanels(const GemmArgs& p, int64_t m0, int64_
     const int kq = idx & 3;
     const int64_t gr = m0 + row;
     const int64_t gk = kc + kq * 4;
+    if (kFull) {
+      r.a[v] = *reinterpret_cast<const float4*>(p.a + gr * p.k + gk);
+      continue;
+    }
     float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
     if (gr < p.m) {
       const float* src = p.a + gr * p.k + gk;
@@ -98,6 +109,10 @@ __device__ __forceinline__ void LoadPanels(const GemmArgs& p, int64_t m0, int64_
       const int c4 = idx % kQuadsPerRow;
       const int64_t gk = kc + row;
       const int64_t gc = n0 + c4 * 4;
+      if (kFull) {
+        r.b[v] = *reinterpret_cast<const float4*>(p.b + gk * p.n + gc);
+        continue;
+      }
       float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
       if (gk < p.k) {
         const float* src = p.b + gk * p.n + gc;
@@ -113,37 +128,59 @@ __device__ __forceinline__ void LoadPanels(const GemmArgs& p, int64_t m0, int64_
       r.b[v] = val;
     }
   } else {
-    constexpr int kPerThread = P::kBBytes;  // 4 or 8 consecutive columns of one row
-    constexpr int kThreadsPerRow = BN / kPerThread;
-    const int row = tid / kThreadsPerRow;
-    const int c0 = (tid % kThreadsPerRow) * kPerThread;
+    constexpr int kPerThread = P::kBBytes;
+    int row, c0;
+    Q8Slot<BN>(tid, &row, &c0);
     const int64_t gk = kc + row;
     const int64_t gc = n0 + c0;
-    if (gk < p.k) {
+    for (int w = 0; w < kPerThread / 4; ++w) r.bq[w] = 0;
+    if (kFull || gk < p.k) {
       const int8_t* src = p.q + gk * p.n + gc;
-      int8_t bytes[kPerThread];
-      if (p.vec_b && gc + kPerThread - 1 < p.n) {
+      if (kFull || (p.vec_b && gc + kPerThread - 1 < p.n)) {
         if (kPerThread == 8) {
           const uint2 w = *reinterpret_cast<const uint2*>(src);
-          for (int e = 0; e < 4; ++e) bytes[e] = static_cast<int8_t>(w.x >> (8 * e));
-          for (int e = 0; e < 4; ++e) bytes[4 + e] = static_cast<int8_t>(w.y >> (8 * e));
+          r.bq[0] = w.x;
+          r.bq[kPerThread / 4 - 1] = w.y;
         } else {
-          const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
-          for (int e = 0; e < 4; ++e) bytes[e] = static_cast<int8_t>(w >> (8 * e));
+          r.bq[0] = *reinterpret_cast<const uint32_t*>(src);
         }
       } else {
-        for (int e = 0; e < kPerThread; ++e) bytes[e] = gc + e < p.n ? src[e] : 0;
+        for (int e = 0; e < kPerThread; ++e)
+          if (gc + e < p.n) r.bq[e >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(src[e])) << (8 * (e & 3));
       }
-      for (int e = 0; e < kPerThread; ++e) r.bq[e] = gc + e < p.n ? Dequant(p, bytes[e], gk, gc + e) : 0.f;
-    } else {
-      for (int e = 0; e < kPerThread; ++e) r.bq[e] = 0.f;
+      if (p.mode == kScalePerRow) {
+        r.row_scale = p.scale[gk];
+        r.row_zero = p.zero != nullptr ? static_cast<float>(p.zero[gk]) : 0.f;
+      }
     }
   }
 }
 
-template <int BM, int BN, bool kQ8>
-__device__ __forceinline__ void StorePanels(float (*As)[BM + 4], float (*Bs)[BN + 4], int tid,
-                                            const Panels<BM, BN, kQ8>& r) {
+// Per-thread constants of the int8 panel: the scale and zero of the thread's columns (per-
+// column or whole-tensor modes), loaded once per workgroup.
+template <int BN>
+struct ColumnQuant {
+  float scale[BN * kBK / kThreads];
+  float zero[BN * kBK / kThreads];
+};
+
+template <int BN>
+__device__ __forceinline__ void LoadColumnQuant(const GemmArgs& p, int64_t n0, int tid, ColumnQuant<BN>& cq) {
+  constexpr int kPerThread = BN * kBK / kThreads;
+  int row, c0;
+  Q8Slot<BN>(tid, &row, &c0);
+  for (int e = 0; e < kPerThread; ++e) {
+    const int64_t gc = min(n0 + c0 + e, p.n - 1);
+    const int64_t idx = p.mode == kScalePerCol ? gc : p.const_index;
+    cq.scale[e] = p.mode == kScalePerRow ? 1.f : p.scale[idx];
+    cq.zero[e] = (p.mode == kScalePerRow || p.zero == nullptr) ? 0.f : static_cast<float>(p.zero[idx]);
+  }
+}
+
+template <int BM, int BN, bool kQ8, bool kFull>
+__device__ __forceinline__ void StorePanels(const GemmArgs& p, float (*As)[BM + 4], float (*Bs)[BN + 4], int64_t n0,
+                                            int64_t kc, int tid, const Panels<BM, BN, kQ8>& r,
+                                            const ColumnQuant<BN>& cq) {
   using P = Panels<BM, BN, kQ8>;
 #pragma unroll
   for (int v = 0; v < P::kAVec; ++v) {
@@ -165,24 +202,32 @@ __device__ __forceinline__ void StorePanels(float (*As)[BM + 4], float (*Bs)[BN 
       *reinterpret_cast<float4*>(&Bs[row][c4 * 4]) = r.b[v];
     }
   } else {
+    // w = (float(q) - float(zero)) * scale, the reference's rounding; 0 past k or n.
     constexpr int kPerThread = P::kBBytes;
-    constexpr int kThreadsPerRow = BN / kPerThread;
-    const int row = tid / kThreadsPerRow;
-    const int c0 = (tid % kThreadsPerRow) * kPerThread;
+    int row, c0;
+    Q8Slot<BN>(tid, &row, &c0);
+    const bool row_ok = kc + row < p.k;
+    float w[kPerThread];
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      const float q = ByteToFloat(r.bq[e >> 2], e & 3);
+      const float s = p.mode == kScalePerRow ? r.row_scale : cq.scale[e];
+      const float z = p.mode == kScalePerRow ? r.row_zero : cq.zero[e];
+      const bool ok = kFull || (row_ok && n0 + c0 + e < p.n);
+      w[e] = ok ? __fmul_rn(__fsub_rn(q, z), s) : 0.f;
+    }
+#pragma unroll
     for (int e = 0; e < kPerThread; e += 4)
-      *reinterpret_cast<float4*>(&Bs[row][c0 + e]) = make_float4(r.bq[e], r.bq[e + 1], r.bq[e + 2], r.bq[e + 3]);
+      *reinterpret_cast<float4*>(&Bs[row][c0 + e]) = make_float4(w[e], w[e + 1], w[e + 2], w[e + 3]);
   }
 }
 
-template <int BM, int BN, bool kQ8>
-__global__ __launch_bounds__(kThreads) void GemmKernel(GemmArgs p) {
+template <int BM, int BN, bool kQ8, bool kFull>
+__device__ __forceinline__ void GemmTile(const GemmArgs& p, float (*As)[kBK][BM + 4], float (*Bs)[kBK][BN + 4]) {
   constexpr int WM = BM / 2;
   constexpr int WN = BN / 2;
   constexpr int SM = WM / 32;
   constexpr int SN = WN / 32;
-  __shared__ float As[2][kBK][BM + 4];
-  __shared__ float Bs[2][kBK][BN + 4];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -203,17 +248,19 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  ColumnQuant<BN> cq;
+  if (kQ8) LoadColumnQuant<BN>(p, n0, tid, cq);
   Panels<BM, BN, kQ8> regs;
   if (chunks > 0) {
-    LoadPanels<BM, BN, kQ8>(p, m0, n0, kb, tid, regs);
-    StorePanels<BM, BN, kQ8>(As[0], Bs[0], tid, regs);
+    LoadPanels<BM, BN, kQ8, kFull>(p, m0, n0, kb, tid, regs);
+    StorePanels<BM, BN, kQ8, kFull>(p, As[0], Bs[0], n0, kb, tid, regs, cq);
   }
   __syncthreads();
   // Panels past ke read zeros only when ke == k; a split boundary inside k is a multiple
   // of kBK, so every chunk of a split lies inside [kb, ke).
   for (int ch = 0; ch < chunks; ++ch) {
     const int cur = ch & 1;
-    if (ch + 1 < chunks) LoadPanels<BM, BN, kQ8>(p, m0, n0, kb + (ch + 1) * kBK, tid, regs);
+    if (ch + 1 < chunks) LoadPanels<BM, BN, kQ8, kFull>(p, m0, n0, kb + (ch + 1) * kBK, tid, regs);
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 2) {
       float av[SM];
@@ -227,40 +274,86 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-    if (ch + 1 < chunks) StorePanels<BM, BN, kQ8>(As[cur ^ 1], Bs[cur ^ 1], tid, regs);
+    if (ch + 1 < chunks)
+      StorePanels<BM, BN, kQ8, kFull>(p, As[cur ^ 1], Bs[cur ^ 1], n0, kb + (ch + 1) * kBK, tid, regs, cq);
     __syncthreads();
   }
 
-  // Element r of a 32x32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
-  auto row_of = [&](int i, int r) -> int64_t {
-    return m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-  };
-  auto col_of = [&](int j) -> int64_t { return n0 + wn * WN + j * 32 + (lane & 31); };
-
-  if (p.splits > 1) {
-    float* part = p.partials + static_cast<int64_t>(split) * p.m * p.n;
+  // Epilogue through LDS: for each i, every wave parks its 32-row band acc[i][*] in the
+  // stage ([64 rows][BN + 4], reusing the panel buffers), then the workgroup walks the 64 x BN
+  // band in float4 steps along rows. Keeps the per-element epilogue out of the unrolled
+  // accumulator code (register use) and makes the stores row-contiguous.
+  float* stage = &As[0][0][0];
+  constexpr int kStride = BN + 4;
+  constexpr int kQuads = 64 * BN / 4;
+  const bool vec_c = (p.n & 3) == 0 &&
+                     (p.splits > 1 ? (reinterpret_cast<uintptr_t>(p.partials) & 15) == 0
+                                   : p.epi.split[0] == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0);
+  float* part = p.splits > 1 ? p.partials + static_cast<int64_t>(split) * p.m * p.n : nullptr;
 #pragma unroll
-    for (int i = 0; i < SM; ++i)
-#pragma unroll
-      for (int j = 0; j < SN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t gr = row_of(i, r);
-          const int64_t gc = col_of(j);
-          if (gr < p.m && gc < p.n) part[gr * p.n + gc] = acc[i][j][r];
-        }
-    return;  // SplitReduceKernel adds the splits in order and applies the epilogue
-  }
-#pragma unroll
-  for (int i = 0; i < SM; ++i)
+  for (int i = 0; i < SM; ++i) {
+    __syncthreads();  // the last panel reads, or the previous band's, are done
+    // Element r of a 32x32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
 #pragma unroll
     for (int j = 0; j < SN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t gr = row_of(i, r);
-        const int64_t gc = col_of(j);
-        if (gr < p.m && gc < p.n) StoreC(p.c, gr, gc, p.n, p.epi, ApplyEpilogue(acc[i][j][r], gr, gc, p.n, p.epi));
+        const int sr = wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        stage[sr * kStride + wn * WN + j * 32 + (lane & 31)] = acc[i][j][r];
       }
+    __syncthreads();
+    for (int e = tid; e < kQuads; e += kThreads) {
+      const int sr = e / (BN / 4);
+      const int c4 = e % (BN / 4);
+      const float4 v = *reinterpret_cast<const float4*>(&stage[sr * kStride + c4 * 4]);
+      const int64_t gr = m0 + (sr >> 5) * WM + i * 32 + (sr & 31);
+      const int64_t gc = n0 + c4 * 4;
+      if (!kFull && gr >= p.m) continue;
+      const float vals[4] = {v.x, v.y, v.z, v.w};
+      if (part != nullptr) {  // SplitReduceKernel adds the splits in order and applies the epilogue
+        if (vec_c && (kFull || gc + 3 < p.n)) {
+          *reinterpret_cast<float4*>(part + gr * p.n + gc) = v;
+        } else {
+          for (int t = 0; t < 4; ++t)
+            if (gc + t < p.n) part[gr * p.n + gc + t] = vals[t];
+        }
+        continue;
+      }
+      if (vec_c && (kFull || gc + 3 < p.n)) {
+        float4 o;
+        o.x = ApplyEpilogue(v.x, gr, gc + 0, p.n, p.epi);
+        o.y = ApplyEpilogue(v.y, gr, gc + 1, p.n, p.epi);
+        o.z = ApplyEpilogue(v.z, gr, gc + 2, p.n, p.epi);
+        o.w = ApplyEpilogue(v.w, gr, gc + 3, p.n, p.epi);
+        *reinterpret_cast<float4*>(p.c + gr * p.n + gc) = o;
+      } else {
+        for (int t = 0; t < 4; ++t)
+          if (gc + t < p.n) StoreC(p.c, gr, gc + t, p.n, p.epi, ApplyEpilogue(vals[t], gr, gc + t, p.n, p.epi));
+      }
+    }
+  }
+}
+
+// Four waves per SIMD (at most 128 registers a lane): the accumulators then live in the
+// unified register file next to the panels, and four workgroups share a CU.
+template <int BM, int BN, bool kQ8>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void GemmKernel(GemmArgs p) {
+  // Panels (double buffered A and B) and, after the main loop, the epilogue stage.
+  static_assert(BM == BN, "the epilogue stage [64][BN + 4] must fit the panel buffers");
+  constexpr int kPanelFloats = 2 * kBK * (BM + 4) + 2 * kBK * (BN + 4);
+  static_assert(64 * (BN + 4) <= kPanelFloats, "epilogue stage larger than the panels");
+  __shared__ __align__(16) float lds[kPanelFloats];
+  auto* As = reinterpret_cast<float(*)[kBK][BM + 4]>(lds);
+  auto* Bs = reinterpret_cast<float(*)[kBK][BN + 4]>(lds + 2 * kBK * (BM + 4));
+  // Interior tiles (most of a large product) take the unchecked loads; edge tiles and
+  // unaligned operands the checked ones. The choice is uniform across the workgroup.
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const int64_t kb = static_cast<int64_t>(blockIdx.z) * p.k_per_split;
+  const int64_t ke = min(p.k, kb + p.k_per_split);
+  const bool full = p.vec_a && p.vec_b && m0 + BM <= p.m && n0 + BN <= p.n && (ke - kb) % kBK == 0;
+  if (full) GemmTile<BM, BN, kQ8, true>(p, As, Bs);
+  else GemmTile<BM, BN, kQ8, false>(p, As, Bs);
 }
 
 template <int BM, int BN>
