@@ -319,6 +319,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--only-llama", action="store_true", help="run only the Llama decode leg (for profiling)")
+    ap.add_argument("--only-gemm", action="store_true",
+                    help="run only the MFMA legs (int8 prefill GEMM + RMSNorm, fp32 MLP), for profiling")
     ap.add_argument("--no-graph", action="store_true", help="launch each step directly instead of from HIP graphs")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one residual add of known traffic (for profiler counter scaling)")
@@ -339,6 +341,15 @@ def main():
     if args.only_llama:
         llama = bench_llama(hip, np.random.default_rng(11))
         print(json.dumps({"llama_decode": llama}), flush=True)
+        return
+    if args.only_gemm:
+        out = {}
+        for name, leg in (("prefill_int8_rmsnorm", bench_prefill), ("mlp_fp32", bench_mlp)):
+            per, tf = leg(hip, args.steps, args.warmup, rng)
+            out[name] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
+                         "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+            log(f"{name}: {per:.4f} ms/step, {tf:.1f} TFLOP/s")
+        print(json.dumps(out), flush=True)
         return
     if args.calibrate:
         calibrate_traffic(hip)
