@@ -112,9 +112,23 @@ struct Epilogue {
 
 // ---- kernel launchers (defined in *.hip) ----------------------------------------------
 
-// C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV).
+// A transform the m = 1 GEMV applies to its input row before the product, inside each
+// workgroup (the row is at most kGemvPrologueMaxK long):
+//  * rms_weight: a = fl(float(double(x) * inv) * w), inv = 1/sqrt(sum(double(x)^2)/k + eps),
+//    the sum taken exactly as RmsNormKernel takes it (same bits as the separate pass);
+//  * silu_up: a = fl(fl(x / fl(1 + expf(-x))) * up), SiluMulKernel's formula.
+struct GemvPrologue {
+  const float* rms_weight = nullptr;
+  float rms_eps = 0.f;
+  const float* silu_up = nullptr;
+};
+constexpr int64_t kGemvPrologueMaxK = 4096;
+
+// C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV). A prologue needs m == 1,
+// staged tiles, a per-column or whole-tensor scale without zero points and k <=
+// kGemvPrologueMaxK.
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
-                  hipStream_t stream);
+                  hipStream_t stream, const GemvPrologue* prologue = nullptr);
 // C[m, n] = A[m, k] @ B[k, n]; B is fp32 (b) or int8 (bq.q != nullptr). fp32 MFMA.
 void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
                    const Epilogue& epi, hipStream_t stream);

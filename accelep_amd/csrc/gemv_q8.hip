@@ -52,6 +52,7 @@ struct GemvArgs {
   // its [k, n] layout.
   const int8_t* tiled;
   Epilogue epi;
+  GemvPrologue pro;  // narrow m = 1 kernel with kAOp != 0
 };
 
 // The 16 bytes at columns [col, col + 16) of one row (`row` must point inside W); zero past
@@ -141,15 +142,24 @@ struct NarrowBatch {
 // sends only k < 2^28 here.
 // kPairA: k even and A 8-byte aligned, so (a[r], a[r + 1]) is one aligned 8-byte load.
 // kClamp false: the caller has checked that every row of the batch lies below ke.
-template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
-__device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
-                                                int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
+template <int M, int U, bool kClamp>
+__device__ __forceinline__ void LoadNarrowW(int r0, int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
   using S = NarrowShape<M>;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int r = r0 + u * static_cast<int>(S::kStepRows);
     const int rw = !kClamp || r < kw - 2 ? r : kw - 2;
     b.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u));
+  }
+}
+
+template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
+__device__ __forceinline__ void LoadNarrowA(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
+                                            NarrowBatch<M, U>& b) {
+  using S = NarrowShape<M>;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int r = r0 + u * static_cast<int>(S::kStepRows);
     const int r1 = !kClamp || r < ke - 1 ? r : ke - 1;
     const int r2 = !kClamp || r + 1 < ke - 1 ? r + 1 : ke - 1;
 #pragma unroll
@@ -176,6 +186,13 @@ __device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, const float* 
       b.z[u][1] = p.zero[static_cast<uint32_t>(r2)];
     }
   }
+}
+
+template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
+__device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
+                                                int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
+  LoadNarrowW<M, U, kClamp>(r0, kw, tbase, b);
+  LoadNarrowA<M, U, kZero, kRowScale, kPairA, kClamp>(p, arow, r0, ke, b);
 }
 
 template <int M, int U, bool kZero, bool kRowScale, bool kClamp>
@@ -239,19 +256,59 @@ __device__ __forceinline__ float WaveColumnSum8(const float (&v8)[kNarrowTile], 
 }
 
 // Waves per SIMD the register budget must allow. For m = 1 with a per-column or whole-tensor
-// scale, 7 (<= 72 VGPRs): the 1792 tiles of a 4096 x 14336 matrix put 7 workgroups of 4 waves
-// on each of 256 CUs, all resident at once. Other forms need more registers and take what
-// the compiler gives them (1: no bound).
-template <int M, bool kRowScale>
+// scale and no input prologue, 7 (<= 72 VGPRs): the 1792 tiles of a 4096 x 14336 matrix put
+// 7 workgroups of 4 waves on each of 256 CUs, all resident at once. Other forms need more
+// registers and take what the compiler gives them (1: no bound).
+template <int M, bool kRowScale, int kAOp>
 constexpr int NarrowMinWaves() {
-  return (M == 1 && !kRowScale) ? 7 : 1;
+  return (M == 1 && !kRowScale && kAOp == 0) ? 7 : 1;
 }
 
-template <int M, bool kZero, bool kRowScale, bool kPairA>
+// Input transforms of the m = 1 kernel (GemvPrologue).
+constexpr int kAOpNone = 0;
+constexpr int kAOpRms = 1;
+constexpr int kAOpSiluUp = 2;
+
+// Writes the transformed input row (kAOp) into a_stage; every thread of the workgroup takes
+// part and the row is complete when this returns.
+template <int kAOp, int kThreads>
+__device__ __forceinline__ void StageInputRow(const GemvArgs& p, float* a_stage, double* part) {
+  const int tid = threadIdx.x;
+  const int k32 = static_cast<int>(p.k);
+  if (kAOp == kAOpRms) {
+    double ss = 0.0;
+    for (int i = tid; i < k32; i += kThreads) {
+      const double v = static_cast<double>(p.a[i]);
+      ss += v * v;
+    }
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    double total = 0.0;
+    for (int wv = 0; wv < kThreads / 64; ++wv) total += part[wv];
+    const double inv = 1.0 / sqrt(total / static_cast<double>(p.k) + static_cast<double>(p.pro.rms_eps));
+    for (int i = tid; i < k32; i += kThreads)
+      a_stage[i] = __fmul_rn(static_cast<float>(static_cast<double>(p.a[i]) * inv), p.pro.rms_weight[i]);
+  } else {
+    for (int i = tid; i < k32; i += kThreads) {
+      const float x = p.a[i];
+      a_stage[i] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.f, expf(-x))), p.pro.silu_up[i]);
+    }
+  }
+  __syncthreads();
+}
+
+// kAOp != kAOpNone (m = 1, k <= one batch, no split): the workgroup issues its whole tile's
+// loads, then writes the transformed input row into LDS while they are in flight, and the
+// product reads the row from there. The RMS sum runs in RmsNormKernel's order (256 threads,
+// stride 256, wave then fixed-order LDS sums), so the row equals that pass's output.
+template <int M, bool kZero, bool kRowScale, bool kPairA, int kAOp = kAOpNone>
 __global__ __launch_bounds__(NarrowShape<M>::kThreads)
-__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNarrowKernel(GemvArgs p) {
+__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale, kAOp>()))) void GemvNarrowKernel(GemvArgs p) {
   using S = NarrowShape<M>;
+  static_assert(kAOp == kAOpNone || (M == 1 && S::kThreads == 256), "prologue: m = 1, RmsNormKernel's block");
   __shared__ float red[S::kWaves][M][kNarrowTile];
+  __shared__ __align__(16) float a_stage[kAOp != kAOpNone ? kGemvPrologueMaxK : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -292,6 +349,17 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNa
   const float* arow[M];
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) arow[mm] = p.a + static_cast<int64_t>(mm < p.m ? mm : p.m - 1) * p.k;
+  if (kAOp != kAOpNone) {
+    // One clamped batch covers k (the launcher checks k <= kBatchRows and sends no split).
+    __shared__ double part[S::kWaves];
+    arow[0] = a_stage;
+    const int r0 = 2 * tid;
+    NarrowBatch<M, S::kUnroll> bx;
+    LoadNarrowW<M, S::kUnroll, true>(r0, static_cast<int>(kw), tbase, bx);
+    StageInputRow<kAOp, S::kThreads>(p, a_stage, part);
+    LoadNarrowA<M, S::kUnroll, false, false, kPairA, true>(p, arow, r0, static_cast<int>(ke), bx);
+    ComputeNarrowBatch<M, S::kUnroll, false, false, true>(bx, r0, static_cast<int>(ke), zc, acc);
+  }
   const int ke32 = static_cast<int>(ke);
   const int kw32 = static_cast<int>(kw);
   // Whole batches (every row below ke, a workgroup-uniform test) issue all their loads at
@@ -302,7 +370,8 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale>()))) void GemvNa
   // the loads, which would make each load wait for the one before it.
   constexpr int kTailUnroll = S::kUnroll / 2;
   static_assert(S::kUnroll % kTailUnroll == 0, "tail steps");
-  for (int r0 = static_cast<int>(kb) + 2 * tid; r0 - 2 * tid < ke32; r0 += static_cast<int>(S::kBatchRows)) {
+  for (int r0 = static_cast<int>(kb) + 2 * tid; kAOp == kAOpNone && r0 - 2 * tid < ke32;
+       r0 += static_cast<int>(S::kBatchRows)) {
     if (r0 - 2 * tid + static_cast<int>(S::kBatchRows) <= ke32) {
       NarrowBatch<M, S::kUnroll> bx;
       LoadNarrowBatch<M, S::kUnroll, kZero, kRowScale, kPairA, false>(p, arow, r0, ke32, kw32, tbase, bx);
@@ -514,8 +583,16 @@ void LaunchNarrow(const GemvArgs& args, dim3 grid, bool zero, bool row_scale, bo
 }  // namespace
 
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
-                  hipStream_t stream) {
+                  hipStream_t stream, const GemvPrologue* prologue) {
   if (m < 1 || m > 16 || k < 1 || n < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV shape out of range");
+  const int a_op = prologue == nullptr ? kAOpNone
+                   : prologue->rms_weight != nullptr ? kAOpRms
+                   : prologue->silu_up != nullptr    ? kAOpSiluUp
+                                                     : kAOpNone;
+  static_assert(kGemvPrologueMaxK <= NarrowShape<1>::kBatchRows, "prologue rows fit one batch");
+  if (a_op != kAOpNone && (m != 1 || b.tiled == nullptr || b.zero != nullptr || b.mode == kScalePerRow ||
+                           k > kGemvPrologueMaxK))
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV input prologue needs m = 1, staged tiles, no zero points, k <= 4096");
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // The narrow kernel reads the staged column tiles (and indexes rows in 32 bits); without
@@ -541,6 +618,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     rows = std::min<int64_t>((rows + 15) / 16 * 16, kWideMaxRows);
   }
   splits = (k + rows - 1) / rows;
+  if (a_op != kAOpNone && splits != 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV input prologue needs one split");
   const int64_t tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
   if (tiles_per_xcd * kXcds > 0x7fffffff || splits > 65535) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV grid too large");
 
@@ -567,12 +645,24 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   }
   static_assert(kNarrowTile == kGemvTileCols, "staged tiles must match the narrow kernel tile");
   args.tiled = narrow ? b.tiled : nullptr;
+  if (prologue != nullptr) args.pro = *prologue;
   const bool zero = b.zero != nullptr;
   const bool row_scale = b.mode == kScalePerRow;
   const dim3 grid(static_cast<uint32_t>(tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
   if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
-    if (m == 1) {
+    if (a_op == kAOpRms) {
+      // The staged row in LDS is 16-byte aligned and k is whole, so pairs load as one.
+      if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpRms>), grid,
+                                         dim3(NarrowShape<1>::kThreads), 0, stream, args);
+      else hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, false, kAOpRms>), grid,
+                              dim3(NarrowShape<1>::kThreads), 0, stream, args);
+    } else if (a_op == kAOpSiluUp) {
+      if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpSiluUp>), grid,
+                                         dim3(NarrowShape<1>::kThreads), 0, stream, args);
+      else hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, false, kAOpSiluUp>), grid,
+                              dim3(NarrowShape<1>::kThreads), 0, stream, args);
+    } else if (m == 1) {
       LaunchNarrow<1>(args, grid, zero, row_scale, pair_a, stream);
     } else if (m == 2) {
       LaunchNarrow<2>(args, grid, zero, row_scale, pair_a, stream);

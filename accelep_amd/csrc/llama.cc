@@ -18,6 +18,7 @@
 //  * the decode step reads its position and id index from device memory and is replayed
 //    from a HIP graph, so a token costs its kernels' time and not ~450 host launches.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -169,6 +170,43 @@ struct Model {
     }
   }
 
+  // One row through an int8 weight on the GEMV, with the input transform done inside it.
+  bool Fusable(const Linear& w, int64_t m) const {
+    return m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
+  }
+  void ApplyPrologue(const Linear& w, const float* x, float* c, const Epilogue& e, const GemvPrologue& pro) {
+    Context& ctx = Ctx();
+    Q8View v;
+    v.q = w.q.as<int8_t>();
+    v.scale = w.scale.as<float>();
+    v.mode = kScalePerCol;
+    v.tiled = StagedColumnTiles(v.q, w.in, w.out, ctx.stream);
+    LaunchGemvQ8(x, v, c, 1, w.in, w.out, e, ctx.stream, &pro);
+  }
+  // c = RMSNorm(x; norm) @ W: one kernel for a decode row, else the norm pass into `normed`.
+  void ApplyNormed(const Linear& w, const float* x, const DevBuf& norm, float* c, int64_t m, const Epilogue& e) {
+    if (Fusable(w, m)) {
+      GemvPrologue pro;
+      pro.rms_weight = norm.as<float>();
+      pro.rms_eps = cfg.eps;
+      ApplyPrologue(w, x, c, e, pro);
+      return;
+    }
+    LaunchRmsNormRows(x, norm.as<float>(), normed.as<float>(), m, cfg.hidden, cfg.eps, stream());
+    Apply(w, normed.as<float>(), c, m, e);
+  }
+  // c = (SiLU(gate) * up) @ W: one kernel for a decode row, else SiLU*up in place first.
+  void ApplySiluUp(const Linear& w, float* g, const float* u, float* c, int64_t m, const Epilogue& e) {
+    if (Fusable(w, m)) {
+      GemvPrologue pro;
+      pro.silu_up = u;
+      ApplyPrologue(w, g, c, e, pro);
+      return;
+    }
+    LaunchSiluMul(g, u, m * cfg.intermediate, stream());
+    Apply(w, g, c, m, e);
+  }
+
   // Forward over `seq` ids at ids[id_offset ..] (device int32) from position `filled`
   // (src/llama_model.cc:209-247). Leaves the last row's logits in `logits`.
   // With `state` (device int32 [position, produced], seq == 1) the position and the id index
@@ -206,21 +244,17 @@ struct Model {
       LayerWeights& l = layers[static_cast<size_t>(li)];
       float* kc = k_cache[static_cast<size_t>(li)].as<float>();
       float* vc = v_cache[static_cast<size_t>(li)].as<float>();
-      LaunchRmsNormRows(hidden.as<float>(), l.attn_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
-      Apply(l.qkv, normed.as<float>(), query.as<float>(), seq, qkv);
+      ApplyNormed(l.qkv, hidden.as<float>(), l.attn_norm, query.as<float>(), seq, qkv);
       LaunchRopeAppend(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc, rope_cos.as<float>(),
                        rope_sin.as<float>(), seq, cfg.heads, cfg.kv_heads, hd, pos, s, state);
       LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s, state,
                       cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes);
       Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, residual);
-      LaunchRmsNormRows(hidden.as<float>(), l.post_norm.as<float>(), normed.as<float>(), seq, H, cfg.eps, s);
-      Apply(l.gu, normed.as<float>(), gate.as<float>(), seq, gu);
-      LaunchSiluMul(gate.as<float>(), up.as<float>(), seq * inter, s);
-      Apply(l.down, gate.as<float>(), hidden.as<float>(), seq, residual);
+      ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
+      ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
     }
-    LaunchRmsNormRows(hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm.as<float>(),
-                      normed.as<float>(), 1, H, cfg.eps, s);
-    Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, Epilogue{});
+    ApplyNormed(lm_head, hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm, logits.as<float>(), 1,
+                Epilogue{});
   }
 
   // One decode step: forward of chosen[produced] at `position`, then both advance. The
@@ -230,7 +264,12 @@ struct Model {
     const bool exact = Ctx().exact_products;
     if (decode_graph != nullptr && (decode_graph_exact != exact || decode_graph_epoch != StagingEpoch()))
       DropDecodeGraph();
-    if (decode_graph == nullptr && !decode_warm) {
+    // ACCEL_LLAMA_EAGER=1 launches every step directly (a profiler then sees each dispatch).
+    static const bool eager = [] {
+      const char* v = std::getenv("ACCEL_LLAMA_EAGER");
+      return v != nullptr && v[0] == '1';
+    }();
+    if (eager || (decode_graph == nullptr && !decode_warm)) {
       Forward(chosen.as<int32_t>(), 1, 0, false, state);
       LaunchAdvance(state, stream());
       decode_warm = true;
