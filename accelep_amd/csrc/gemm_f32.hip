@@ -222,7 +222,7 @@ __device__ __forceinline__ void StorePanels(const GemmArgs& p, float (*As)[BM + 
   }
 }
 
-template <int BM, int BN, bool kQ8, bool kFull>
+template <int BM, int BN, bool kQ8, bool kFull, int kPF>
 __device__ __forceinline__ void GemmTile(const GemmArgs& p, float (*As)[kBK][BM + 4], float (*Bs)[kBK][BN + 4]) {
   constexpr int WM = BM / 2;
   constexpr int WN = BN / 2;
@@ -250,17 +250,26 @@ __device__ __forceinline__ void GemmTile(const GemmArgs& p, float (*As)[kBK][BM 
 
   ColumnQuant<BN> cq;
   if (kQ8) LoadColumnQuant<BN>(p, n0, tid, cq);
-  Panels<BM, BN, kQ8> regs;
-  if (chunks > 0) {
-    LoadPanels<BM, BN, kQ8, kFull>(p, m0, n0, kb, tid, regs);
-    StorePanels<BM, BN, kQ8, kFull>(p, As[0], Bs[0], n0, kb, tid, regs, cq);
-  }
+  // kStages register sets: chunk ch + kStages is requested while chunk ch is multiplied, so a
+  // panel's global latency is covered by kStages chunks of MFMA work (the LDS stays double
+  // buffered). Edge tiles keep one set.
+  constexpr int kStages = kFull ? kPF : 1;
+  Panels<BM, BN, kQ8> regs[kStages];
+#pragma unroll
+  for (int st = 0; st < kStages; ++st)
+    if (st < chunks) LoadPanels<BM, BN, kQ8, kFull>(p, m0, n0, kb + st * kBK, tid, regs[st]);
+  if (chunks > 0) StorePanels<BM, BN, kQ8, kFull>(p, As[0], Bs[0], n0, kb, tid, regs[0], cq);
   __syncthreads();
   // Panels past ke read zeros only when ke == k; a split boundary inside k is a multiple
-  // of kBK, so every chunk of a split lies inside [kb, ke).
-  for (int ch = 0; ch < chunks; ++ch) {
+  // of kBK, so every chunk of a split lies inside [kb, ke). The chunk loop is unrolled by
+  // kStages so that every register set is named at compile time.
+  for (int base = 0; base < chunks; base += kStages) {
+#pragma unroll
+  for (int st = 0; st < kStages; ++st) {
+    const int ch = base + st;
+    if (ch >= chunks) break;  // workgroup-uniform
     const int cur = ch & 1;
-    if (ch + 1 < chunks) LoadPanels<BM, BN, kQ8, kFull>(p, m0, n0, kb + (ch + 1) * kBK, tid, regs);
+    if (ch + kStages < chunks) LoadPanels<BM, BN, kQ8, kFull>(p, m0, n0, kb + (ch + kStages) * kBK, tid, regs[st]);
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 2) {
       float av[SM];
@@ -275,8 +284,10 @@ __device__ __forceinline__ void GemmTile(const GemmArgs& p, float (*As)[kBK][BM 
         for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
     if (ch + 1 < chunks)
-      StorePanels<BM, BN, kQ8, kFull>(p, As[cur ^ 1], Bs[cur ^ 1], n0, kb + (ch + 1) * kBK, tid, regs, cq);
+      StorePanels<BM, BN, kQ8, kFull>(p, As[cur ^ 1], Bs[cur ^ 1], n0, kb + (ch + 1) * kBK, tid,
+                                      regs[(st + 1) % kStages], cq);
     __syncthreads();
+  }
   }
 
   // Epilogue through LDS: for each i, every wave parks its 32-row band acc[i][*] in the
@@ -334,10 +345,16 @@ __device__ __forceinline__ void GemmTile(const GemmArgs& p, float (*As)[kBK][BM 
   }
 }
 
-// Four waves per SIMD (at most 128 registers a lane): the accumulators then live in the
-// unified register file next to the panels, and four workgroups share a CU.
+// Waves per SIMD the register budget must allow. 128x128: 3 (at most 168 registers a lane),
+// which holds the 64 accumulators and three panel sets without spilling; 64x64: 4.
+template <int BM>
+constexpr int GemmMinWaves() {
+  return BM == 128 ? 3 : 4;
+}
+
 template <int BM, int BN, bool kQ8>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void GemmKernel(GemmArgs p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(GemmMinWaves<BM>()))) void GemmKernel(
+    GemmArgs p) {
   // Panels (double buffered A and B) and, after the main loop, the epilogue stage.
   static_assert(BM == BN, "the epilogue stage [64][BN + 4] must fit the panel buffers");
   constexpr int kPanelFloats = 2 * kBK * (BM + 4) + 2 * kBK * (BN + 4);
@@ -352,8 +369,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int64_t kb = static_cast<int64_t>(blockIdx.z) * p.k_per_split;
   const int64_t ke = min(p.k, kb + p.k_per_split);
   const bool full = p.vec_a && p.vec_b && m0 + BM <= p.m && n0 + BN <= p.n && (ke - kb) % kBK == 0;
-  if (full) GemmTile<BM, BN, kQ8, true>(p, As, Bs);
-  else GemmTile<BM, BN, kQ8, false>(p, As, Bs);
+  constexpr int kPF = BM == 128 ? 3 : 4;  // register sets of the interior path
+  if (full) GemmTile<BM, BN, kQ8, true, kPF>(p, As, Bs);
+  else GemmTile<BM, BN, kQ8, false, kPF>(p, As, Bs);
 }
 
 template <int BM, int BN>
@@ -380,8 +398,10 @@ void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
   const int64_t tiles_m = (m + bm - 1) / bm;
   const int64_t tiles_n = (n + bn - 1) / bn;
   const int64_t tiles = tiles_m * tiles_n;
+  // Split K only when the tiles leave CUs idle: with a tile per CU the partial-sum traffic and
+  // the extra pass cost more than the second wave per SIMD gains.
   int64_t splits = 1;
-  if (tiles < 2 * cus) splits = std::min<int64_t>((2 * cus + tiles - 1) / tiles, std::max<int64_t>(1, k / 256));
+  if (tiles < cus) splits = std::min<int64_t>((2 * cus + tiles - 1) / tiles, std::max<int64_t>(1, k / 256));
   int64_t kper = (k + splits - 1) / splits;
   kper = (kper + kBK - 1) / kBK * kBK;
   splits = (k + kper - 1) / kper;
