@@ -128,6 +128,7 @@ LLAMA_SIGNATURES = {
     "accel_llama_forward_ids": (C.c_int, [C.c_void_p, I32P, C.c_int32, C.c_int32]),
     "accel_llama_logit_max_abs": (C.c_int, [C.c_void_p, F32P, C.c_int32, F32P]),
     "accel_llama_logits": (C.c_int, [C.c_void_p, F32P, C.c_int32]),
+    "accel_llama_set_fused_inputs": (C.c_int, [C.c_void_p, C.c_int32]),
     "accel_llama_reset": (None, [C.c_void_p]),
     "accel_llama_last_error": (C.c_char_p, []),
 }

@@ -142,57 +142,59 @@ struct NarrowBatch {
 // sends only k < 2^28 here.
 // kPairA: k even and A 8-byte aligned, so (a[r], a[r + 1]) is one aligned 8-byte load.
 // kClamp false: the caller has checked that every row of the batch lies below ke.
+// Load u of a batch: the W pair.
 template <int M, int U, bool kClamp>
-__device__ __forceinline__ void LoadNarrowW(int r0, int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
+__device__ __forceinline__ void LoadNarrowWAt(int u, int r0, int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
   using S = NarrowShape<M>;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int r = r0 + u * static_cast<int>(S::kStepRows);
-    const int rw = !kClamp || r < kw - 2 ? r : kw - 2;
-    b.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u));
-  }
+  const int r = r0 + u * static_cast<int>(S::kStepRows);
+  const int rw = !kClamp || r < kw - 2 ? r : kw - 2;
+  b.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u));
 }
 
+// Load u of a batch: the A rows (and per-row scale and zero).
 template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
-__device__ __forceinline__ void LoadNarrowA(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
-                                            NarrowBatch<M, U>& b) {
+__device__ __forceinline__ void LoadNarrowAAt(int u, const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
+                                              NarrowBatch<M, U>& b) {
   using S = NarrowShape<M>;
+  const int r = r0 + u * static_cast<int>(S::kStepRows);
+  const int r1 = !kClamp || r < ke - 1 ? r : ke - 1;
+  const int r2 = !kClamp || r + 1 < ke - 1 ? r + 1 : ke - 1;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int r = r0 + u * static_cast<int>(S::kStepRows);
-    const int r1 = !kClamp || r < ke - 1 ? r : ke - 1;
-    const int r2 = !kClamp || r + 1 < ke - 1 ? r + 1 : ke - 1;
-#pragma unroll
-    for (int mm = 0; mm < M; ++mm) {
-      // Offsets as 32-bit values from the uniform row base: one VGPR per address.
-      const char* abase = reinterpret_cast<const char*>(arow[mm]);
-      if (kPairA) {
-        // k is even here, so ke is even and the pair (rp, rp + 1) is whole.
-        const int rp = !kClamp || r < ke - 2 ? r : ke - 2;
-        const float2 v = *reinterpret_cast<const float2*>(abase + static_cast<uint32_t>(rp) * 4u);
-        b.a[u][mm][0] = v.x;
-        b.a[u][mm][1] = v.y;
-      } else {
-        b.a[u][mm][0] = *reinterpret_cast<const float*>(abase + static_cast<uint32_t>(r1) * 4u);
-        b.a[u][mm][1] = *reinterpret_cast<const float*>(abase + static_cast<uint32_t>(r2) * 4u);
-      }
+  for (int mm = 0; mm < M; ++mm) {
+    // Offsets as 32-bit values from the uniform row base: one VGPR per address.
+    const char* abase = reinterpret_cast<const char*>(arow[mm]);
+    if (kPairA) {
+      // k is even here, so ke is even and the pair (rp, rp + 1) is whole.
+      const int rp = !kClamp || r < ke - 2 ? r : ke - 2;
+      const float2 v = *reinterpret_cast<const float2*>(abase + static_cast<uint32_t>(rp) * 4u);
+      b.a[u][mm][0] = v.x;
+      b.a[u][mm][1] = v.y;
+    } else {
+      b.a[u][mm][0] = *reinterpret_cast<const float*>(abase + static_cast<uint32_t>(r1) * 4u);
+      b.a[u][mm][1] = *reinterpret_cast<const float*>(abase + static_cast<uint32_t>(r2) * 4u);
     }
-    if (kRowScale) {
-      b.s[u][0] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.scale) + static_cast<uint32_t>(r1) * 4u);
-      b.s[u][1] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.scale) + static_cast<uint32_t>(r2) * 4u);
-    }
-    if (kZero && kRowScale) {
-      b.z[u][0] = p.zero[static_cast<uint32_t>(r1)];
-      b.z[u][1] = p.zero[static_cast<uint32_t>(r2)];
-    }
+  }
+  if (kRowScale) {
+    b.s[u][0] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.scale) + static_cast<uint32_t>(r1) * 4u);
+    b.s[u][1] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.scale) + static_cast<uint32_t>(r2) * 4u);
+  }
+  if (kZero && kRowScale) {
+    b.z[u][0] = p.zero[static_cast<uint32_t>(r1)];
+    b.z[u][1] = p.zero[static_cast<uint32_t>(r2)];
   }
 }
 
+// The whole batch, each W load followed by its A loads: loads complete in issue order, so
+// load u's data is ready as soon as the first u loads are, and the products of u start while
+// the later loads are still in flight.
 template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
 __device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
                                                 int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
-  LoadNarrowW<M, U, kClamp>(r0, kw, tbase, b);
-  LoadNarrowA<M, U, kZero, kRowScale, kPairA, kClamp>(p, arow, r0, ke, b);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    LoadNarrowWAt<M, U, kClamp>(u, r0, kw, tbase, b);
+    LoadNarrowAAt<M, U, kZero, kRowScale, kPairA, kClamp>(u, p, arow, r0, ke, b);
+  }
 }
 
 template <int M, int U, bool kZero, bool kRowScale, bool kClamp>
@@ -355,9 +357,12 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kRowScale, kAOp>()))) void 
     arow[0] = a_stage;
     const int r0 = 2 * tid;
     NarrowBatch<M, S::kUnroll> bx;
-    LoadNarrowW<M, S::kUnroll, true>(r0, static_cast<int>(kw), tbase, bx);
+#pragma unroll
+    for (int u = 0; u < S::kUnroll; ++u) LoadNarrowWAt<M, S::kUnroll, true>(u, r0, static_cast<int>(kw), tbase, bx);
     StageInputRow<kAOp, S::kThreads>(p, a_stage, part);
-    LoadNarrowA<M, S::kUnroll, false, false, kPairA, true>(p, arow, r0, static_cast<int>(ke), bx);
+#pragma unroll
+    for (int u = 0; u < S::kUnroll; ++u)
+      LoadNarrowAAt<M, S::kUnroll, false, false, kPairA, true>(u, p, arow, r0, static_cast<int>(ke), bx);
     ComputeNarrowBatch<M, S::kUnroll, false, false, true>(bx, r0, static_cast<int>(ke), zc, acc);
   }
   const int ke32 = static_cast<int>(ke);

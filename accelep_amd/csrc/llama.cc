@@ -123,6 +123,7 @@ struct Model {
   bool decode_graph_exact = false;
   uint64_t decode_graph_epoch = 0;
   bool decode_warm = false;
+  bool fuse_inputs = true;  // decode rows: RMSNorm and SiLU*up inside the next GEMV
   // Attention partials of a decode step ([heads][context / 64 chunks][2 + head_dim]): owned
   // here so a captured step never points into a workspace that later grows.
   DevBuf attn_work;
@@ -172,7 +173,7 @@ struct Model {
 
   // One row through an int8 weight on the GEMV, with the input transform done inside it.
   bool Fusable(const Linear& w, int64_t m) const {
-    return m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
+    return fuse_inputs && m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
   }
   void ApplyPrologue(const Linear& w, const float* x, float* c, const Epilogue& e, const GemvPrologue& pro) {
     Context& ctx = Ctx();
@@ -679,6 +680,19 @@ ACCEL_LLAMA_API int accel_llama_logit_max_abs(AccelLlama* handle, const float* r
       if (d > worst) worst = d;
     }
     *out_max_abs = worst;
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_set_fused_inputs(AccelLlama* handle, int32_t enable) {
+  Model* m = Get(handle);
+  if (m == nullptr) {
+    g_llama_error = "invalid model";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    if (m->fuse_inputs != (enable != 0)) m->DropDecodeGraph();  // the graph holds the other kernels
+    m->fuse_inputs = enable != 0;
   });
 }
 

@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 from accelep_amd.capi import F32P, I8P, I32P, LlamaConfig, check, lib
-from golden_cases import llama_cases, llama_full_case, llama_weights
+from golden_cases import llama_cases, llama_config, llama_full_case, llama_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -114,6 +114,29 @@ def test_llama_full_size_matches_reference():
         dt = time.perf_counter() - t0
         print(f"generate: 512 prompt + {ids.size} new tokens in {dt * 1e3:.1f} ms", flush=True)
         np.testing.assert_array_equal(ids, gold["ids"])
+    finally:
+        eng.close()
+
+
+def test_decode_row_fused_inputs_match_separate_passes():
+    """A one-row forward folds the RMSNorms and SiLU*up into the next int8 GEMV; the logits
+    must carry exactly the bits of the separate-kernel forward."""
+    cfg = llama_config("smol3")
+    w, q = llama_weights(cfg, 103)
+    prompt = np.random.default_rng(5).integers(0, cfg["vocab"], size=9).astype(np.int32)
+    eng = Engine(cfg, w, q)
+    try:
+        rows = {}
+        for fused in (1, 0):
+            assert eng.L.accel_llama_set_fused_inputs(eng.h, fused) == 0
+            head, last = np.ascontiguousarray(prompt[:-1]), np.ascontiguousarray(prompt[-1:])
+            assert eng.L.accel_llama_forward_ids(eng.h, head.ctypes.data_as(I32P), head.size, 1) == 0
+            assert eng.L.accel_llama_forward_ids(eng.h, last.ctypes.data_as(I32P), 1, 0) == 0
+            row = np.zeros(cfg["vocab"], np.float32)
+            assert eng.L.accel_llama_logits(eng.h, row.ctypes.data_as(F32P), row.size) == 0
+            rows[fused] = row
+        assert np.isfinite(rows[1]).all()
+        np.testing.assert_array_equal(rows[1].view(np.uint32), rows[0].view(np.uint32))
     finally:
         eng.close()
 
