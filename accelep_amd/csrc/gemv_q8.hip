@@ -425,6 +425,43 @@ constexpr int kWideTile = 256;
 constexpr int kWideMaxRows = 1024;
 constexpr int kWideUnroll = 4;
 
+// One step of the wide kernel: row group g = g0 + u * waves holds rows 4g .. 4g + 3, lane row
+// l / 16 of it; rows past `rows` read a clamped row and are zeroed through A.
+template <bool kVec>
+__device__ __forceinline__ void WideLoad(const GemvArgs& p, const int8_t* wbase, int64_t col, int rows, int groups,
+                                         int g0, int lane_row, uint4 (&w)[kWideUnroll]) {
+#pragma unroll
+  for (int u = 0; u < kWideUnroll; ++u) {
+    const int g = g0 + u * kWideWaves;
+    const int r = g * 4 + lane_row;
+    const bool valid = g < groups && r < rows;
+    const int rc = valid ? r : rows - 1;
+    w[u] = LoadRow16<kVec>(wbase + static_cast<int64_t>(rc) * p.n, col, p.n, valid);
+  }
+}
+
+template <bool kZero, bool kRowScale>
+__device__ __forceinline__ void WideStep(const GemvArgs& p, const float* smem, int64_t k0, int rows, int groups, int g0,
+                                         int lane_row, int lane_col, const float (&zc)[16],
+                                         const uint4 (&w)[kWideUnroll], v4f (&acc)[16]) {
+#pragma unroll
+  for (int u = 0; u < kWideUnroll; ++u) {
+    const int g = g0 + u * kWideWaves;
+    const int r = g * 4 + lane_row;
+    const bool valid = g < groups && r < rows;
+    const int rc = valid ? r : rows - 1;
+    const float a = smem[rc * 16 + lane_col];  // A[l % 16][row of l]
+    const float av = valid ? a : 0.f;
+    const float zr = (kZero && kRowScale) ? static_cast<float>(p.zero[k0 + rc]) : 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      float b = ByteToFloat(Word(w[u], t >> 2), t & 3);
+      if (kZero) b = b - (zc[t] + zr);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b, acc[t], 0, 0, 0);
+    }
+  }
+}
+
 template <bool kVec, bool kZero, bool kRowScale>
 __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
   __shared__ float smem[16 * kWideMaxRows];  // A stage [row][16]; reused for the wave sums
@@ -460,29 +497,18 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
 
   const int groups = (rows + 3) >> 2;
   const int8_t* wbase = p.q + k0 * p.n;
-  for (int g0 = wave; g0 < groups; g0 += kWideWaves * kWideUnroll) {
-    uint4 w[kWideUnroll];
-    float av[kWideUnroll];
-    float zr[kWideUnroll];
-#pragma unroll
-    for (int u = 0; u < kWideUnroll; ++u) {
-      const int g = g0 + u * kWideWaves;
-      const int r = g * 4 + lane_row;
-      const bool valid = g < groups && r < rows;
-      const int rc = valid ? r : rows - 1;
-      w[u] = LoadRow16<kVec>(wbase + static_cast<int64_t>(rc) * p.n, col, p.n, valid);
-      const float a = smem[rc * 16 + lane_col];  // A[l % 16][row of l]
-      av[u] = valid ? a : 0.f;
-      zr[u] = (kZero && kRowScale) ? static_cast<float>(p.zero[k0 + rc]) : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < kWideUnroll; ++u) {
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        float b = ByteToFloat(Word(w[u], t >> 2), t & 3);
-        if (kZero) b = b - (zc[t] + zr[u]);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], b, acc[t], 0, 0, 0);
-      }
+  // Two register sets in turn: the next step's rows are requested before this step's
+  // MFMAs, so a load has a whole step of matrix work to arrive in.
+  constexpr int kStride = kWideWaves * kWideUnroll;
+  uint4 wa[kWideUnroll], wb[kWideUnroll];
+  WideLoad<kVec>(p, wbase, col, rows, groups, wave, lane_row, wa);
+  for (int g0 = wave; g0 < groups; g0 += 2 * kStride) {
+    const bool second = g0 + kStride < groups;  // uniform across the wave
+    if (second) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + kStride, lane_row, wb);
+    WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0, lane_row, lane_col, zc, wa, acc);
+    if (second) {
+      if (g0 + 2 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 2 * kStride, lane_row, wa);
+      WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0 + kStride, lane_row, lane_col, zc, wb, acc);
     }
   }
   __syncthreads();  // A stage done; smem becomes [wave][16][kWideTile]
@@ -617,7 +643,9 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     rows = (k + splits - 1) / splits;
     rows = (rows + step_rows - 1) / step_rows * step_rows;
   } else {
-    splits = std::max<int64_t>((cus + tiles - 1) / tiles, (k + kWideMaxRows - 1) / kWideMaxRows);
+    // About 1.75 workgroups per CU (measured best for 4096 x 14336 at m = 16), and no split
+    // longer than the A stage.
+    splits = std::max<int64_t>((7 * cus / 4 + tiles - 1) / tiles, (k + kWideMaxRows - 1) / kWideMaxRows);
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, (k + 255) / 256));
     rows = (k + splits - 1) / splits;
     rows = std::min<int64_t>((rows + 15) / 16 * 16, kWideMaxRows);
