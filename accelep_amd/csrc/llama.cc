@@ -4,11 +4,13 @@
 // The call sequence per layer is the reference's: RMSNorm, q/k/v projections, RoPE on q and
 // k, KV append, causal attention, o projection + residual, RMSNorm, gate/up, SiLU*up, down
 // projection + residual; then the final RMSNorm of the last row and the LM head. What
-// differs is where things live and how many passes there are (9 kernels per layer where the
-// reference makes 15 device calls):
+// differs is where things live and how many passes there are (a decode step takes 7
+// kernels per layer where the reference makes 15 device calls):
 //  * q/k/v and gate/up are one matmul each over concatenated weights, storing into the
 //    separate outputs (a column-split store); RoPE of q and k and both KV appends are one
 //    kernel;
+//  * for a one-row (decode) forward the RMSNorms and SiLU*up run inside the next int8 GEMV
+//    (GemvPrologue), with the same bits as the separate passes a prompt uses;
 //  * the residual adds run in the o and down projections' stores (c = acc + hidden, in
 //    place), which gives the bits of the reference's MatMul + ResidualAdd pair;
 //  * linear layers are int8 [in, out] with a per-output-column scale (the int8 GEMV for a
