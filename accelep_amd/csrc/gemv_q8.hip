@@ -473,7 +473,7 @@ __device__ __forceinline__ void WideStep(const GemvArgs& p, const float* smem, i
 
 template <bool kVec, bool kZero, bool kRowScale>
 __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
-  __shared__ float smem[16 * kWideMaxRows];  // A stage [row][16]; reused for the wave sums
+  __shared__ __align__(16) float smem[16 * kWideMaxRows];  // A stage [row][16]; reused for the wave sums
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -483,15 +483,31 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
   const int64_t k0 = static_cast<int64_t>(split) * p.rows_per_split;
   const int rows = static_cast<int>(min(p.rows_per_split, p.k - k0));
 
-  for (int idx = tid; idx < rows * 16; idx += kWideThreads) {
-    const int r = idx >> 4;
-    const int mm = idx & 15;
-    float v = 0.f;
-    if (mm < p.m) {
-      v = p.a[mm * p.k + k0 + r];
-      if (kRowScale) v = __fmul_rn(v, p.scale[k0 + r]);
+  // A stage: smem[r * 16 + mm] = A[mm][k0 + r] (times the row's scale when per-row), 0 for
+  // mm >= m. Thread r reads its row's 16 values down A's columns (consecutive threads,
+  // consecutive addresses) and issues all of them before storing any, so the stage costs one
+  // memory round trip per 256 rows instead of one per element.
+  for (int r0 = 0; r0 < rows; r0 += kWideThreads) {
+    const int r = r0 + tid;
+    const int rc = r < rows ? r : rows - 1;
+    float v[16];
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm) {
+      const int64_t mc = mm < p.m ? mm : p.m - 1;  // a valid row; zeroed below
+      v[mm] = p.a[mc * p.k + k0 + rc];
     }
-    smem[idx] = v;
+    const float rs = kRowScale ? p.scale[k0 + rc] : 1.f;
+    if (r < rows) {
+#pragma unroll
+      for (int mm = 0; mm < 16; mm += 4) {
+        float4 q;
+        q.x = mm + 0 < p.m ? (kRowScale ? __fmul_rn(v[mm + 0], rs) : v[mm + 0]) : 0.f;
+        q.y = mm + 1 < p.m ? (kRowScale ? __fmul_rn(v[mm + 1], rs) : v[mm + 1]) : 0.f;
+        q.z = mm + 2 < p.m ? (kRowScale ? __fmul_rn(v[mm + 2], rs) : v[mm + 2]) : 0.f;
+        q.w = mm + 3 < p.m ? (kRowScale ? __fmul_rn(v[mm + 3], rs) : v[mm + 3]) : 0.f;
+        *reinterpret_cast<float4*>(&smem[r * 16 + mm]) = q;
+      }
+    }
   }
   __syncthreads();
 
@@ -506,18 +522,22 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
 
   const int groups = (rows + 3) >> 2;
   const int8_t* wbase = p.q + k0 * p.n;
-  // Two register sets in turn: the next step's rows are requested before this step's
-  // MFMAs, so a load has a whole step of matrix work to arrive in.
+  // Three register sets in turn: the rows of step s + 2 are requested before the MFMAs of
+  // step s, so a load has two steps of matrix work (about 2 us) to arrive in.
   constexpr int kStride = kWideWaves * kWideUnroll;
-  uint4 wa[kWideUnroll], wb[kWideUnroll];
+  uint4 wa[kWideUnroll], wb[kWideUnroll], wc[kWideUnroll];
   WideLoad<kVec>(p, wbase, col, rows, groups, wave, lane_row, wa);
-  for (int g0 = wave; g0 < groups; g0 += 2 * kStride) {
-    const bool second = g0 + kStride < groups;  // uniform across the wave
-    if (second) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + kStride, lane_row, wb);
+  if (wave + kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, wave + kStride, lane_row, wb);
+  for (int g0 = wave; g0 < groups; g0 += 3 * kStride) {  // every test below is uniform across the wave
+    if (g0 + 2 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 2 * kStride, lane_row, wc);
     WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0, lane_row, lane_col, zc, wa, acc);
-    if (second) {
-      if (g0 + 2 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 2 * kStride, lane_row, wa);
+    if (g0 + kStride < groups) {
+      if (g0 + 3 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 3 * kStride, lane_row, wa);
       WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0 + kStride, lane_row, lane_col, zc, wb, acc);
+    }
+    if (g0 + 2 * kStride < groups) {
+      if (g0 + 4 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 4 * kStride, lane_row, wb);
+      WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0 + 2 * kStride, lane_row, lane_col, zc, wc, acc);
     }
   }
   __syncthreads();  // A stage done; smem becomes [wave][16][kWideTile]
