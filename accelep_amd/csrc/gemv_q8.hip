@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int tile = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
+  const int tile = blockIdx.x;
   if (tile >= p.tiles) return;
   const int split = blockIdx.y;
   const int64_t k0 = static_cast<int64_t>(split) * p.rows_per_split;
@@ -522,23 +522,17 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
 
   const int groups = (rows + 3) >> 2;
   const int8_t* wbase = p.q + k0 * p.n;
-  // Three register sets in turn: the rows of step s + 2 are requested before the MFMAs of
-  // step s, so a load has two steps of matrix work (about 2 us) to arrive in.
+  // The next step's rows are requested before this step's MFMAs (one set in flight while
+  // one is multiplied).
   constexpr int kStride = kWideWaves * kWideUnroll;
-  uint4 wa[kWideUnroll], wb[kWideUnroll], wc[kWideUnroll];
-  WideLoad<kVec>(p, wbase, col, rows, groups, wave, lane_row, wa);
-  if (wave + kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, wave + kStride, lane_row, wb);
-  for (int g0 = wave; g0 < groups; g0 += 3 * kStride) {  // every test below is uniform across the wave
-    if (g0 + 2 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 2 * kStride, lane_row, wc);
-    WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0, lane_row, lane_col, zc, wa, acc);
-    if (g0 + kStride < groups) {
-      if (g0 + 3 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 3 * kStride, lane_row, wa);
-      WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0 + kStride, lane_row, lane_col, zc, wb, acc);
-    }
-    if (g0 + 2 * kStride < groups) {
-      if (g0 + 4 * kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + 4 * kStride, lane_row, wb);
-      WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0 + 2 * kStride, lane_row, lane_col, zc, wc, acc);
-    }
+  uint4 wn[kWideUnroll];
+  WideLoad<kVec>(p, wbase, col, rows, groups, wave, lane_row, wn);
+  for (int g0 = wave; g0 < groups; g0 += kStride) {
+    uint4 w[kWideUnroll];
+#pragma unroll
+    for (int u = 0; u < kWideUnroll; ++u) w[u] = wn[u];
+    if (g0 + kStride < groups) WideLoad<kVec>(p, wbase, col, rows, groups, g0 + kStride, lane_row, wn);
+    WideStep<kZero, kRowScale>(p, smem, k0, rows, groups, g0, lane_row, lane_col, zc, w, acc);
   }
   __syncthreads();  // A stage done; smem becomes [wave][16][kWideTile]
   // Lane l holds m = 4*(l/16) + r, column 16*(l%16) + t.
@@ -555,18 +549,19 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
 }
 
 // ---- split-K reduction ----------------------------------------------------------------------
+// One thread per output column of a row (blockIdx.y strides over rows): no index division.
 __global__ void SplitReduceKernel(const float* partials, int32_t splits, int64_t m, int64_t n, float* c,
                                   int32_t mode, const float* scale, int64_t const_index, Epilogue epi) {
+  const int64_t j = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (j >= n) return;
   const int64_t total = m * n;
-  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
-       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t i = idx / n;
-    const int64_t j = idx - i * n;
+  float cs = 1.f;
+  if (scale != nullptr && mode == kScalePerCol) cs = scale[j];
+  if (scale != nullptr && mode == kScaleConst) cs = scale[const_index];
+  for (int64_t i = blockIdx.y; i < m; i += gridDim.y) {
+    const int64_t idx = i * n + j;
     float s = partials[idx];
     for (int sp = 1; sp < splits; ++sp) s = s + partials[static_cast<int64_t>(sp) * total + idx];
-    float cs = 1.f;
-    if (scale != nullptr && mode == kScalePerCol) cs = scale[j];
-    if (scale != nullptr && mode == kScaleConst) cs = scale[const_index];
     StoreC(c, i, j, n, epi, ApplyEpilogue(__fmul_rn(s, cs), i, j, n, epi));
   }
 }
@@ -615,11 +610,11 @@ void LaunchTileColumns(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipSt
 
 void LaunchSplitReduce(const float* partials, int32_t splits, int64_t m, int64_t n, float* c, int32_t mode,
                        const float* scale, int64_t const_index, const Epilogue& epi, hipStream_t stream) {
-  const int64_t total = m * n;
-  int64_t grid = (total + 255) / 256;
-  if (grid > 65536) grid = 65536;
-  hipLaunchKernelGGL(SplitReduceKernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, partials, splits, m, n,
-                     c, mode, scale, const_index, epi);
+  const int64_t gx = (n + 255) / 256;
+  const int64_t gy = std::min<int64_t>(m, 65535);
+  if (gx > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "split reduction grid too large");
+  hipLaunchKernelGGL(SplitReduceKernel, dim3(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy)), dim3(256), 0, stream,
+                     partials, splits, m, n, c, mode, scale, const_index, epi);
   Check(hipGetLastError(), "SplitReduceKernel launch");
 }
 
