@@ -541,11 +541,25 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
   __syncthreads();
   const int64_t out_col = static_cast<int64_t>(tile) * kWideTile + tid;
   if (out_col >= p.n) return;
-  for (int mm = 0; mm < p.m; ++mm) {
+  // All 16 rows' wave sums are read at once (one LDS round trip), then stored.
+  float sums[16];
+#pragma unroll
+  for (int mm = 0; mm < 16; ++mm) {
     float s = smem[mm * kWideTile + tid];
+#pragma unroll
     for (int wv = 1; wv < kWideWaves; ++wv) s = s + smem[(wv * 16 + mm) * kWideTile + tid];
-    Emit(p, split, mm, out_col, s);
+    sums[mm] = s;
   }
+  if (p.splits > 1) {
+    float* dst = p.partials + static_cast<int64_t>(split) * p.m * p.n + out_col;
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm)
+      if (mm < p.m) dst[mm * p.n] = sums[mm];
+    return;  // SplitReduceKernel applies the scale and the epilogue
+  }
+#pragma unroll
+  for (int mm = 0; mm < 16; ++mm)
+    if (mm < p.m) Emit(p, split, mm, out_col, sums[mm]);
 }
 
 // ---- split-K reduction ----------------------------------------------------------------------
