@@ -33,28 +33,24 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
 
-// The fields a workgroup needs to issue its first loads come first, so they arrive in one
-// scalar load at the start of the kernel.
 struct GemvArgs {
+  const float* a;
+  const int8_t* q;
+  const float* scale;
+  const int8_t* zero;
+  int32_t mode;
+  int64_t const_index;
+  float* c;
+  int64_t m, k, n;
+  int32_t tiles;
+  int32_t tiles_per_xcd;
+  int32_t splits;
+  int64_t rows_per_split;
+  float* partials;  // [splits][m][n] when splits > 1
   // Column-tiled copy of W (narrow kernel): 8-column tile t, row r at tiled + (t*kp + r)*8
   // (kp = k rounded up to even), columns past n and the pad row zero. nullptr: read W in
   // its [k, n] layout.
   const int8_t* tiled;
-  const float* a;
-  int64_t k;
-  int64_t rows_per_split;
-  int32_t tiles;
-  int32_t tiles_per_xcd;
-  int64_t m;
-  const float* scale;
-  int32_t mode;
-  int32_t splits;
-  int64_t const_index;
-  int64_t n;
-  const int8_t* q;
-  const int8_t* zero;
-  float* c;
-  float* partials;  // [splits][m][n] when splits > 1
   Epilogue epi;
   GemvPrologue pro;  // narrow m = 1 kernel with kAOp != 0
 };
@@ -318,11 +314,8 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // Workgroups past the last tile (fewer than kXcds) redo the last tile and store nothing:
-  // no early exit, so the first loads wait on no branch over a kernel argument.
-  const int tile_id = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
-  const bool live = tile_id < p.tiles;
-  const int tile = live ? tile_id : p.tiles - 1;
+  const int tile = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
+  if (tile >= p.tiles) return;
   const int split = blockIdx.y;
   const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
   const int64_t ke = min(p.k, kb + p.rows_per_split);
@@ -382,11 +375,9 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
   // the loads, which would make each load wait for the one before it.
   constexpr int kTailUnroll = S::kUnroll / 2;
   static_assert(S::kUnroll % kTailUnroll == 0, "tail steps");
-  // b0 is the batch's first row (uniform, so the tests below are scalar branches); this
-  // lane's rows start at b0 + 2 * tid.
-  for (int b0 = static_cast<int>(kb); kAOp == kAOpNone && b0 < ke32; b0 += static_cast<int>(S::kBatchRows)) {
-    const int r0 = b0 + 2 * tid;
-    if (b0 + static_cast<int>(S::kBatchRows) <= ke32) {
+  for (int r0 = static_cast<int>(kb) + 2 * tid; kAOp == kAOpNone && r0 - 2 * tid < ke32;
+       r0 += static_cast<int>(S::kBatchRows)) {
+    if (r0 - 2 * tid + static_cast<int>(S::kBatchRows) <= ke32) {
       NarrowBatch<M, S::kUnroll> bx;
       LoadNarrowBatch<M, S::kUnroll, kZero, kRowScale, kPairA, false>(p, arow, r0, ke32, kw32, tbase, bx);
       __builtin_amdgcn_sched_barrier(0);
@@ -395,7 +386,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
 #pragma unroll 1
       for (int u = 0; u < S::kUnroll; u += kTailUnroll) {
         const int rt = r0 + u * static_cast<int>(S::kStepRows);
-        if (b0 + u * static_cast<int>(S::kStepRows) >= ke32) break;  // the rest of the batch lies past ke
+        if (rt - 2 * tid >= ke32) break;  // the rest of the batch lies past ke (workgroup-uniform)
         NarrowBatch<M, kTailUnroll> bt;
         LoadNarrowBatch<M, kTailUnroll, kZero, kRowScale, kPairA, true>(p, arow, rt, ke32, kw32, tbase, bt);
         __builtin_amdgcn_sched_barrier(0);
@@ -414,7 +405,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
     const int mm = tid / kNarrowTile;
     const int c = tid % kNarrowTile;
     const int64_t col = col0 + c;
-    if (live && mm < p.m && col < p.n) {
+    if (mm < p.m && col < p.n) {
       float s = red[0][mm][c];
       for (int wv = 1; wv < S::kWaves; ++wv) s = s + red[wv][mm][c];
       if (p.splits > 1) {
