@@ -239,6 +239,28 @@ def test_gemm_int8_panels(m, k, n):
         np.testing.assert_allclose(got, case["a"] @ w, rtol=1e-5, atol=1e-5)
 
 
+def test_gemm_c4_shape_with_fused_rmsnorm():
+    """The prefill product at full size, X[2048, 4096] @ int8 W[4096, 14336] per-column scale
+    with the RMSNormalization of the output rows fused: 40 sampled rows (first, last, random)
+    meet the gamma_K bound against float64, and the fused RMS rows equal the oracle's RMSNorm
+    of the stored product rows."""
+    m, k, n = 2048, 4096, 14336
+    case = c3_case(m, k, n, 4242)
+    r = np.random.default_rng(4243)
+    gamma_w = (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+    g_d = dev(gamma_w)
+    out = dev(np.zeros((m, n), np.float32))
+    e = Epilogue(alpha=1.0, beta=1.0, rms_weight=g_d.ptr, rms_eps=1e-5, rms_out=out.ptr)
+    got = matmul_quantized(case, e)
+    y = out.numpy()
+    rows = np.unique(np.concatenate([[0, 1, 127, 128, m - 1], r.choice(m, 35, replace=False)]))
+    w = dequant_host(case["bq"], k, n)
+    assert_gamma_bound(got[rows], case["a"][rows], w)
+    want = oracle().rmsnorm(np.ascontiguousarray(got[rows]), gamma_w, rows.size, n, 1e-5)
+    np.testing.assert_allclose(y[rows], want, rtol=1e-6, atol=1e-6)
+    assert np.isfinite(y).all()
+
+
 def test_staged_weight_follows_rewrites():
     """The GEMV reads a staged column-tiled copy of W; rewriting W (host copy, or W used as a
     kernel output) must be seen by the next call."""
