@@ -288,6 +288,167 @@ __global__ __launch_bounds__(64) void AttentionCombineKernel(const float* partia
   }
 }
 
+
+// ---- prompt rows, head_dim 64, fast mode: online softmax over key stages ------------------
+// One workgroup per (16 query rows, head); its four waves take a quarter of the keys each and
+// the quarters are combined at the end. Lane l of a wave owns query row l / 4 and dims
+// [16 (l % 4), +16): a score is 16 FMAs plus two lane exchanges. Each wave stages 16 keys
+// of K and V in its own LDS slice (coalesced loads), then for 8 keys at a time takes the
+// scores, their max, one rescale of the running sum and output, and the 8 weighted V rows
+// (online softmax). K and V are read once per 16 query rows instead of once per row. The
+// summation order differs from the reference's sequential loops (rounding only), so this
+// path serves the fast mode; the per-row kernel above keeps the reference's score bits.
+constexpr int kFlashRows = 16;
+constexpr int kFlashWaves = 4;
+constexpr int kFlashStage = 16;  // keys per LDS stage
+constexpr int kFlashDim = 64;
+
+__global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const float* q, const float* k,
+                                                                      const float* v, float* out, int64_t seq,
+                                                                      int64_t position_arg, int64_t heads,
+                                                                      int64_t kv_heads, const int32_t* position_dev) {
+  __shared__ __align__(16) float ks[kFlashWaves][kFlashStage][kFlashDim];
+  __shared__ __align__(16) float vs[kFlashWaves][kFlashStage][kFlashDim];
+  __shared__ float part_m[kFlashWaves][kFlashRows];
+  __shared__ float part_l[kFlashWaves][kFlashRows];
+  __shared__ __align__(16) float part_acc[kFlashWaves][kFlashRows][kFlashDim];
+  const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r = lane >> 2;   // query row in the block
+  const int qd = lane & 3;   // dim quarter
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * kFlashRows;
+  const int64_t h = blockIdx.y;
+  const int64_t kv = h / (heads / kv_heads);
+  const int64_t row = s0 + r;
+  const bool live = row < seq;
+  const int64_t last_key = position + (live ? row : -1);  // keys 0 .. last_key (causal)
+  const float scale = __fdiv_rn(1.f, __fsqrt_rn(static_cast<float>(kFlashDim)));
+
+  float qv[16];
+  {
+    const float* qrow = q + ((live ? row : 0) * heads + h) * kFlashDim + 16 * qd;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(qrow + i);
+      qv[i] = x.x;
+      qv[i + 1] = x.y;
+      qv[i + 2] = x.z;
+      qv[i + 3] = x.w;
+    }
+  }
+  // Keys of the block: 0 .. position + min(s0 + 16, seq) - 1, cut into four ranges.
+  const int64_t nkeys = position + min<int64_t>(s0 + kFlashRows, seq);
+  const int64_t per = ((nkeys + kFlashWaves - 1) / kFlashWaves + kFlashStage - 1) / kFlashStage * kFlashStage;
+  const int64_t kbeg = min<int64_t>(wave * per, nkeys);
+  const int64_t kend = min<int64_t>(kbeg + per, nkeys);
+  const int64_t kv_stride = kv_heads * kFlashDim;
+
+  float m = -INFINITY;
+  float l = 0.f;
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+
+  for (int64_t t0 = kbeg; t0 < kend; t0 += kFlashStage) {  // uniform across the wave
+    // Stage keys t0 .. t0 + 15 (rows past the range read key kend - 1; they are masked).
+#pragma unroll
+    for (int i = 0; i < kFlashStage * kFlashDim / 4 / 64; ++i) {
+      const int f = i * 64 + lane;
+      const int key = f >> 4;
+      const int part = f & 15;
+      const int64_t t = min<int64_t>(t0 + key, kend - 1);
+      const float4 kx = *reinterpret_cast<const float4*>(k + t * kv_stride + kv * kFlashDim + part * 4);
+      const float4 vx = *reinterpret_cast<const float4*>(v + t * kv_stride + kv * kFlashDim + part * 4);
+      *reinterpret_cast<float4*>(&ks[wave][key][part * 4]) = kx;
+      *reinterpret_cast<float4*>(&vs[wave][key][part * 4]) = vx;
+    }
+    // The stage is this wave's alone: a wave-level fence and barrier order its writes
+    // before its reads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int g = 0; g < kFlashStage; g += 8) {
+      float sc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float* kr = &ks[wave][g + j][16 * qd];
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(kr + i);
+          dot = __builtin_fmaf(qv[i], x.x, dot);
+          dot = __builtin_fmaf(qv[i + 1], x.y, dot);
+          dot = __builtin_fmaf(qv[i + 2], x.z, dot);
+          dot = __builtin_fmaf(qv[i + 3], x.w, dot);
+        }
+        dot = dot + __shfl_xor(dot, 1);
+        dot = dot + __shfl_xor(dot, 2);
+        const int64_t t = t0 + g + j;
+        sc[j] = (t < kend && t <= last_key) ? __fmul_rn(dot, scale) : -INFINITY;
+      }
+      float mb = sc[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) mb = fmaxf(mb, sc[j]);
+      const float m_new = fmaxf(m, mb);
+      if (m_new != -INFINITY) {  // else nothing of this row so far
+        const float corr = m == -INFINITY ? 0.f : expf(m - m_new);
+        l = l * corr;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = acc[i] * corr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = sc[j] == -INFINITY ? 0.f : expf(sc[j] - m_new);
+          l = l + p;
+          const float* vr = &vs[wave][g + j][16 * qd];
+#pragma unroll
+          for (int i = 0; i < 16; i += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(vr + i);
+            acc[i] = __builtin_fmaf(p, x.x, acc[i]);
+            acc[i + 1] = __builtin_fmaf(p, x.y, acc[i + 1]);
+            acc[i + 2] = __builtin_fmaf(p, x.z, acc[i + 2]);
+            acc[i + 3] = __builtin_fmaf(p, x.w, acc[i + 3]);
+          }
+        }
+        m = m_new;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // the stage is read before the next one overwrites it
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  if (qd == 0) {
+    part_m[wave][r] = m;
+    part_l[wave][r] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i += 4)
+    *reinterpret_cast<float4*>(&part_acc[wave][r][16 * qd + i]) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+  __syncthreads();
+  if (wave == 0 && live) {
+    float big = part_m[0][r];
+    for (int w = 1; w < kFlashWaves; ++w) big = fmaxf(big, part_m[w][r]);
+    float wts[kFlashWaves];
+    float total = 0.f;
+    for (int w = 0; w < kFlashWaves; ++w) {
+      wts[w] = part_m[w][r] == -INFINITY ? 0.f : expf(part_m[w][r] - big);
+      total = total + wts[w] * part_l[w][r];
+    }
+    float* orow = out + (row * heads + h) * kFlashDim + 16 * qd;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      float o[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < kFlashWaves; ++w)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = o[e] + wts[w] * part_acc[w][r][16 * qd + i + e];
+      *reinterpret_cast<float4*>(orow + i) = make_float4(o[0] / total, o[1] / total, o[2] / total, o[3] / total);
+    }
+  }
+}
+
 constexpr int64_t kSplitMaxSeq = 4;
 
 }  // namespace
@@ -304,7 +465,7 @@ size_t AttentionWorkBytes(int64_t seq, int64_t heads, int64_t max_position, int6
 
 void LaunchAttention(const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position,
                      int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream, const int32_t* position_dev,
-                     int64_t max_position, float* work, size_t work_bytes) {
+                     int64_t max_position, float* work, size_t work_bytes, bool fast) {
   if (seq <= 0 || heads <= 0) return;
   if (head_dim <= 0 || head_dim > 256) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention head_dim must be in 1..256");
   const int64_t blocks = seq * heads;
@@ -344,6 +505,15 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
     hipLaunchKernelGGL(AttentionCombineKernel, dim3(static_cast<uint32_t>(blocks)), dim3(64), 0, stream, scratch, out,
                        chunks, head_dim);
     Check(hipGetLastError(), "AttentionCombineKernel launch");
+    return;
+  }
+  if (fast && head_dim == kFlashDim && aligned && (reinterpret_cast<uintptr_t>(q) % 16 == 0) &&
+      (reinterpret_cast<uintptr_t>(out) % 16 == 0)) {
+    const int64_t qblocks = (seq + kFlashRows - 1) / kFlashRows;
+    if (qblocks > 0x7fffffff || heads > 65535) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
+    hipLaunchKernelGGL(AttentionFlashKernel, dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(heads)),
+                       dim3(kFlashWaves * 64), 0, stream, q, k, v, out, seq, position, heads, kv_heads, position_dev);
+    Check(hipGetLastError(), "AttentionFlashKernel launch");
     return;
   }
   float* spill = rows > kLdsScores ? scratch : nullptr;

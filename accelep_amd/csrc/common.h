@@ -169,10 +169,13 @@ void LaunchAdvance(int32_t* state, hipStream_t stream);
 // max_position: with position_dev, the largest position the device word may hold. work /
 // work_bytes: caller-owned scratch (at least AttentionWorkBytes); null uses the library
 // workspace.
+// fast: prompt rows (seq > 4) with head_dim 64 may use the online-softmax kernel, whose sums
+// run in another order than the reference's (rounding only); otherwise the scores keep the
+// reference's bits.
 void LaunchAttention(const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position,
                      int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
                      const int32_t* position_dev = nullptr, int64_t max_position = 0, float* work = nullptr,
-                     size_t work_bytes = 0);
+                     size_t work_bytes = 0, bool fast = false);
 // Scratch bytes LaunchAttention needs for these sizes (0 when none).
 size_t AttentionWorkBytes(int64_t seq, int64_t heads, int64_t max_position, int64_t head_dim);
 // rng_inout is a device word holding the xorshift32 state; index_dev offsets `chosen`.

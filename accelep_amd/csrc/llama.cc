@@ -251,7 +251,7 @@ struct Model {
       LaunchRopeAppend(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc, rope_cos.as<float>(),
                        rope_sin.as<float>(), seq, cfg.heads, cfg.kv_heads, hd, pos, s, state);
       LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s, state,
-                      cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes);
+                      cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes, !Ctx().exact_products);
       Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, residual);
       ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
       ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
