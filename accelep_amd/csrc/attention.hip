@@ -303,6 +303,23 @@ constexpr int kFlashWaves = 4;
 constexpr int kFlashStage = 16;  // keys per LDS stage
 constexpr int kFlashDim = 64;
 
+constexpr int kFlashStageLoads = kFlashStage * kFlashDim / 4 / 64;  // 16-byte pieces of K (and of V) per lane
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Lane l brings float4 (f & 15) of key t0 + (f >> 4), f = i * 64 + l, of K and V; keys past
+// the range read key kend - 1 (masked at use).
+__device__ __forceinline__ void FlashLoadStage(const float* k, const float* v, int64_t t0, int64_t kend,
+                                               int64_t kv_stride, int64_t kv, int lane,
+                                               f4 (&kx)[kFlashStageLoads], f4 (&vx)[kFlashStageLoads]) {
+#pragma unroll
+  for (int i = 0; i < kFlashStageLoads; ++i) {
+    const int f = i * 64 + lane;
+    const int64_t t = min<int64_t>(t0 + (f >> 4), kend - 1);
+    kx[i] = *reinterpret_cast<const f4*>(k + t * kv_stride + kv * kFlashDim + (f & 15) * 4);
+    vx[i] = *reinterpret_cast<const f4*>(v + t * kv_stride + kv * kFlashDim + (f & 15) * 4);
+  }
+}
+
 __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const float* q, const float* k,
                                                                       const float* v, float* out, int64_t seq,
                                                                       int64_t position_arg, int64_t heads,
@@ -351,19 +368,17 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
 
+  // The next stage's loads are issued before the current stage is multiplied.
+  f4 kx[kFlashStageLoads], vx[kFlashStageLoads];
+  if (kbeg < kend) FlashLoadStage(k, v, kbeg, kend, kv_stride, kv, lane, kx, vx);
   for (int64_t t0 = kbeg; t0 < kend; t0 += kFlashStage) {  // uniform across the wave
-    // Stage keys t0 .. t0 + 15 (rows past the range read key kend - 1; they are masked).
 #pragma unroll
-    for (int i = 0; i < kFlashStage * kFlashDim / 4 / 64; ++i) {
+    for (int i = 0; i < kFlashStageLoads; ++i) {
       const int f = i * 64 + lane;
-      const int key = f >> 4;
-      const int part = f & 15;
-      const int64_t t = min<int64_t>(t0 + key, kend - 1);
-      const float4 kx = *reinterpret_cast<const float4*>(k + t * kv_stride + kv * kFlashDim + part * 4);
-      const float4 vx = *reinterpret_cast<const float4*>(v + t * kv_stride + kv * kFlashDim + part * 4);
-      *reinterpret_cast<float4*>(&ks[wave][key][part * 4]) = kx;
-      *reinterpret_cast<float4*>(&vs[wave][key][part * 4]) = vx;
+      *reinterpret_cast<f4*>(&ks[wave][f >> 4][(f & 15) * 4]) = kx[i];
+      *reinterpret_cast<f4*>(&vs[wave][f >> 4][(f & 15) * 4]) = vx[i];
     }
+    if (t0 + kFlashStage < kend) FlashLoadStage(k, v, t0 + kFlashStage, kend, kv_stride, kv, lane, kx, vx);
     // The stage is this wave's alone: a wave-level fence and barrier order its writes
     // before its reads.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -430,9 +445,11 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
   __syncthreads();
   if (wave == 0 && live) {
     float big = part_m[0][r];
+#pragma unroll
     for (int w = 1; w < kFlashWaves; ++w) big = fmaxf(big, part_m[w][r]);
     float wts[kFlashWaves];
     float total = 0.f;
+#pragma unroll
     for (int w = 0; w < kFlashWaves; ++w) {
       wts[w] = part_m[w][r] == -INFINITY ? 0.f : expf(part_m[w][r] - big);
       total = total + wts[w] * part_l[w][r];
@@ -441,6 +458,7 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
       float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
       for (int w = 0; w < kFlashWaves; ++w)
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = o[e] + wts[w] * part_acc[w][r][16 * qd + i + e];
