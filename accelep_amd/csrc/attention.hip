@@ -467,6 +467,188 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
   }
 }
 
+// ---- decode row, head_dim 64: RoPE, KV append, chunked attention and combine in one kernel --
+// One workgroup per (head, 64-position chunk), as AttentionChunkKernel, for the single query
+// row of a decode step. Each workgroup rotates its head's q itself (RopeAppendKernel's
+// arithmetic); the workgroup of the chunk holding the new position rotates the new k, uses
+// the new k and v from LDS for that position, and, for the first query head of the kv
+// group, stores them into the cache rows. No workgroup reads the cache row being written.
+// The chunk's (m, l, acc) go to `partial`; the last workgroup of a head to finish (counted in
+// `arrivals[h]`) adds the chunks in chunk order as AttentionCombineKernel does, writes the
+// output row and sets the count back to zero for the next launch. Chunks past the position
+// exit at once. The scores, the chunk sums and the combine are those of the three-kernel
+// path, bit for bit.
+constexpr int kStepDim = 64;
+
+__global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
+    const float* q_raw, const float* k_raw, const float* v_raw, float* k_cache, float* v_cache, const float* cos_t,
+    const float* sin_t, float* out, int64_t position_arg, const int32_t* position_dev, int64_t heads,
+    int64_t kv_heads, int64_t chunks_max, float* partial, uint32_t* arrivals) {
+  __shared__ __align__(16) float qs[kStepDim];
+  __shared__ __align__(16) float knew[kStepDim];
+  __shared__ __align__(16) float vnew[kStepDim];
+  __shared__ float es[kChunk];
+  __shared__ float acc_part[kSplitThreads / (kStepDim / 4) * kStepDim];
+  __shared__ float red[2];
+  __shared__ float wts[kMaxChunks];
+  __shared__ float lsum[kMaxChunks];
+  __shared__ int is_last;
+  const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
+  const int64_t h = blockIdx.x;
+  const int64_t c = blockIdx.y;
+  const int64_t group = heads / kv_heads;
+  const int64_t kv = h / group;
+  const int64_t total = position + 1;
+  const int64_t live = (total + kChunk - 1) / kChunk;
+  if (c >= live) return;  // uniform over the workgroup
+  const int64_t t0 = c * kChunk;
+  const int64_t n = min<int64_t>(kChunk, total - t0);
+  const bool tail = t0 + n == total;  // this chunk holds the new position
+  const int tid = threadIdx.x;
+  const int64_t kv_row = kv_heads * kStepDim;
+
+  // Loads that do not depend on the rotation are issued first: the key row of this lane
+  // (wave 0) and the value rows of this thread's (position group, column quad).
+  constexpr int kCols = 4;
+  constexpr int kGroups = kSplitThreads / (kStepDim / kCols);  // 16
+  const int cc = tid % (kStepDim / kCols);
+  const int g = tid / (kStepDim / kCols);
+  float4 kx[kStepDim / 4];
+  const bool score_lane = tid < n && t0 + tid != position;
+  if (score_lane) {
+    const float4* kr = reinterpret_cast<const float4*>(k_cache + (t0 + tid) * kv_row + kv * kStepDim);
+#pragma unroll
+    for (int j = 0; j < kStepDim / 4; ++j) kx[j] = kr[j];
+  }
+  float4 vx[kChunk / kGroups];
+#pragma unroll
+  for (int i = 0; i < kChunk / kGroups; ++i) {
+    const int64_t t = g + i * kGroups;
+    if (t < n && t0 + t != position)
+      vx[i] = *reinterpret_cast<const float4*>(v_cache + (t0 + t) * kv_row + kv * kStepDim + cc * kCols);
+  }
+
+  // RoPE (RopeAppendKernel's arithmetic) of q, and in the tail chunk of the new k; new v.
+  constexpr int kHalf = kStepDim / 2;
+  const float* cs = cos_t + position * kStepDim;
+  const float* sn = sin_t + position * kStepDim;
+  if (tid < kHalf || (tail && tid < 2 * kHalf)) {
+    const int i = tid % kHalf;
+    const float* src = tid < kHalf ? q_raw + h * kStepDim : k_raw + kv * kStepDim;
+    float* dst = tid < kHalf ? qs : knew;
+    const float x0 = src[i];
+    const float x1 = src[kHalf + i];
+    dst[i] = __fsub_rn(__fmul_rn(x0, cs[i]), __fmul_rn(x1, sn[i]));
+    dst[kHalf + i] = __fadd_rn(__fmul_rn(x1, cs[kHalf + i]), __fmul_rn(x0, sn[kHalf + i]));
+  } else if (tail && tid >= 64 && tid < 64 + kStepDim) {
+    vnew[tid - 64] = v_raw[kv * kStepDim + (tid - 64)];
+  }
+  __syncthreads();
+  if (tail && h % group == 0 && tid < kStepDim) {
+    k_cache[position * kv_row + kv * kStepDim + tid] = knew[tid];
+    v_cache[position * kv_row + kv * kStepDim + tid] = vnew[tid];
+  }
+
+  // Scores: d ascending, each product rounded before its add (Dot<16>).
+  const float scale = __fdiv_rn(1.f, __fsqrt_rn(static_cast<float>(kStepDim)));
+  if (tid < n) {
+    if (!score_lane) {
+#pragma unroll
+      for (int j = 0; j < kStepDim / 4; ++j) kx[j] = reinterpret_cast<const float4*>(knew)[j];
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < kStepDim / 4; ++j) {
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 0], kx[j].x));
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 1], kx[j].y));
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 2], kx[j].z));
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 3], kx[j].w));
+    }
+    es[tid] = __fmul_rn(dot, scale);
+  }
+  __syncthreads();
+  if (tid < 64) {  // wave 0: chunk max, exps, their sum
+    const float x = tid < n ? es[tid] : -INFINITY;
+    float m = x;
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float e = tid < n ? expf(__fsub_rn(x, m)) : 0.f;
+    if (tid < n) es[tid] = e;
+    float l = e;
+    for (int off = 32; off > 0; off >>= 1) l = __fadd_rn(l, __shfl_xor(l, off));
+    if (tid == 0) {
+      red[0] = m;
+      red[1] = l;
+    }
+  }
+  __syncthreads();
+  // acc[d] over the chunk: thread (g, cc) adds positions g, g + 16, ... in order.
+  float acc[kCols] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kChunk / kGroups; ++i) {
+    const int64_t t = g + i * kGroups;
+    if (t < n) {
+      const float e = es[t];
+      const float4 x4 = t0 + t == position ? reinterpret_cast<const float4*>(vnew)[cc] : vx[i];
+      acc[0] = __fadd_rn(acc[0], __fmul_rn(e, x4.x));
+      acc[1] = __fadd_rn(acc[1], __fmul_rn(e, x4.y));
+      acc[2] = __fadd_rn(acc[2], __fmul_rn(e, x4.z));
+      acc[3] = __fadd_rn(acc[3], __fmul_rn(e, x4.w));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) acc_part[g * kStepDim + cc * kCols + j] = acc[j];
+  __syncthreads();
+  // The chunk's partial goes out with device-scope (agent) stores, which are written through
+  // to the level every XCD reads; each thread waits until its stores are done before the
+  // barrier, and only then is the chunk counted. The workgroup that brings the count to
+  // `live` reads the partials with device-scope loads. No cache-wide writeback or
+  // invalidate is needed for these few hundred bytes.
+  float* mine = partial + (h * chunks_max + c) * (2 + kStepDim);
+  if (tid < kStepDim) {
+    float o = acc_part[tid];
+    for (int gg = 1; gg < kGroups; ++gg) o = __fadd_rn(o, acc_part[gg * kStepDim + tid]);
+    __hip_atomic_store(&mine[2 + tid], o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid == 0) {
+    __hip_atomic_store(&mine[0], red[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&mine[1], red[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) is_last = atomicAdd(&arrivals[h], 1u) == static_cast<uint32_t>(live - 1);
+  __syncthreads();
+  if (!is_last) return;
+  const float* p = partial + h * chunks_max * (2 + kStepDim);
+  const auto load = [](const float* x) { return __hip_atomic_load(x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  if (tid < 64) {
+    float big = -INFINITY;
+    for (int64_t ch = tid; ch < live; ch += 64) {
+      wts[ch] = load(&p[ch * (2 + kStepDim)]);
+      lsum[ch] = load(&p[ch * (2 + kStepDim) + 1]);
+      big = fmaxf(big, wts[ch]);
+    }
+    for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+    for (int64_t ch = tid; ch < live; ch += 64) wts[ch] = wts[ch] == -INFINITY ? 0.f : expf(__fsub_rn(wts[ch], big));
+  }
+  __syncthreads();
+  if (tid < kStepDim) {
+    float l = 0.f;
+    for (int64_t ch = 0; ch < live; ++ch) l = __fadd_rn(l, __fmul_rn(wts[ch], lsum[ch]));
+    float o = 0.f;
+    int64_t ch = 0;
+    for (; ch + 8 <= live; ch += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = load(&p[(ch + u) * (2 + kStepDim) + 2 + tid]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o = __fadd_rn(o, __fmul_rn(wts[ch + u], x[u]));
+    }
+    for (; ch < live; ++ch) o = __fadd_rn(o, __fmul_rn(wts[ch], load(&p[ch * (2 + kStepDim) + 2 + tid])));
+    out[h * kStepDim + tid] = __fdiv_rn(o, l);
+  }
+  if (tid == 0) atomicExch(&arrivals[h], 0u);
+}
+
 constexpr int64_t kSplitMaxSeq = 4;
 
 }  // namespace
@@ -548,6 +730,28 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
   }
 #undef ACCEL_ATTN
   Check(hipGetLastError(), "AttentionKernel launch");
+}
+
+
+bool LaunchDecodeAttention(const float* q, const float* k, const float* v, float* k_cache, float* v_cache,
+                           const float* cos_table, const float* sin_table, float* out, int64_t position,
+                           int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
+                           const int32_t* position_dev, int64_t max_position, float* work, size_t work_bytes,
+                           uint32_t* arrivals) {
+  if (head_dim != kStepDim || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || arrivals == nullptr ||
+      work == nullptr)
+    return false;
+  const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!aligned(k_cache) || !aligned(v_cache)) return false;
+  const int64_t top = position_dev != nullptr ? max_position : position;
+  const int64_t chunks = (top + 1 + kChunk - 1) / kChunk;
+  if (chunks > kMaxChunks || heads > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention context is too long for a decode step");
+  if (work_bytes < AttentionWorkBytes(1, heads, top, head_dim)) Fail(ACCEL_HIP_INVALID_ARGUMENT, "attention scratch is too small");
+  hipLaunchKernelGGL(DecodeAttentionKernel, dim3(static_cast<uint32_t>(heads), static_cast<uint32_t>(chunks)),
+                     dim3(kSplitThreads), 0, stream, q, k, v, k_cache, v_cache, cos_table, sin_table, out, position,
+                     position_dev, heads, kv_heads, chunks, work, arrivals);
+  Check(hipGetLastError(), "DecodeAttentionKernel launch");
+  return true;
 }
 
 }  // namespace accel_hip

@@ -176,6 +176,17 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
                      int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
                      const int32_t* position_dev = nullptr, int64_t max_position = 0, float* work = nullptr,
                      size_t work_bytes = 0, bool fast = false);
+// A decode row (seq 1) with head_dim 64: RoPE of q and k, the KV append and the attention
+// (LaunchRopeAppend + LaunchAttention) in one kernel, with the same output bits and the same
+// cache rows. `work` holds at least AttentionWorkBytes(1, heads, max position, 64) bytes;
+// `arrivals` is heads zeroed uint32 words, left zero again by each launch (launches that
+// share it must not overlap). Returns false, launching nothing, when the sizes or the
+// alignment do not fit (head_dim != 64, caches not 16-byte aligned).
+bool LaunchDecodeAttention(const float* q, const float* k, const float* v, float* k_cache, float* v_cache,
+                           const float* cos_table, const float* sin_table, float* out, int64_t position,
+                           int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
+                           const int32_t* position_dev, int64_t max_position, float* work, size_t work_bytes,
+                           uint32_t* arrivals);
 // Scratch bytes LaunchAttention needs for these sizes (0 when none).
 size_t AttentionWorkBytes(int64_t seq, int64_t heads, int64_t max_position, int64_t head_dim);
 // rng_inout is a device word holding the xorshift32 state; index_dev offsets `chosen`.

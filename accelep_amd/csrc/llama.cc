@@ -4,11 +4,11 @@
 // The call sequence per layer is the reference's: RMSNorm, q/k/v projections, RoPE on q and
 // k, KV append, causal attention, o projection + residual, RMSNorm, gate/up, SiLU*up, down
 // projection + residual; then the final RMSNorm of the last row and the LM head. What
-// differs is where things live and how many passes there are (a decode step takes 7
+// differs is where things live and how many passes there are (a decode step takes 5
 // kernels per layer where the reference makes 15 device calls):
 //  * q/k/v and gate/up are one matmul each over concatenated weights, storing into the
 //    separate outputs (a column-split store); RoPE of q and k and both KV appends are one
-//    kernel;
+//    kernel, and for a decode row (head_dim 64) that kernel is also the attention;
 //  * for a one-row (decode) forward the RMSNorms and SiLU*up run inside the next int8 GEMV
 //    (GemvPrologue), with the same bits as the separate passes a prompt uses;
 //  * the residual adds run in the o and down projections' stores (c = acc + hidden, in
@@ -125,10 +125,11 @@ struct Model {
   bool decode_graph_exact = false;
   uint64_t decode_graph_epoch = 0;
   bool decode_warm = false;
-  bool fuse_inputs = true;  // decode rows: RMSNorm and SiLU*up inside the next GEMV
+  bool fuse_inputs = true;  // decode rows: RMSNorm and SiLU*up inside the next GEMV, one attention kernel
   // Attention partials of a decode step ([heads][context / 64 chunks][2 + head_dim]): owned
   // here so a captured step never points into a workspace that later grows.
   DevBuf attn_work;
+  DevBuf attn_arrivals;  // uint32 per head, zero between decode attention launches
 
   void DropDecodeGraph() {
     if (decode_graph != nullptr) accel_hip_graph_destroy(decode_graph);
@@ -248,10 +249,17 @@ struct Model {
       float* kc = k_cache[static_cast<size_t>(li)].as<float>();
       float* vc = v_cache[static_cast<size_t>(li)].as<float>();
       ApplyNormed(l.qkv, hidden.as<float>(), l.attn_norm, query.as<float>(), seq, qkv);
-      LaunchRopeAppend(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc, rope_cos.as<float>(),
-                       rope_sin.as<float>(), seq, cfg.heads, cfg.kv_heads, hd, pos, s, state);
-      LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s, state,
-                      cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes, !Ctx().exact_products);
+      if (seq != 1 || !fuse_inputs || !LaunchDecodeAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
+                                             rope_cos.as<float>(), rope_sin.as<float>(), mixed.as<float>(), pos,
+                                             cfg.heads, cfg.kv_heads, hd, s, state, cfg.context - 1,
+                                             attn_work.as<float>(), attn_work.buffer().bytes,
+                                             attn_arrivals.as<uint32_t>())) {
+        LaunchRopeAppend(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc, rope_cos.as<float>(),
+                         rope_sin.as<float>(), seq, cfg.heads, cfg.kv_heads, hd, pos, s, state);
+        LaunchAttention(query.as<float>(), kc, vc, mixed.as<float>(), seq, pos, cfg.heads, cfg.kv_heads, hd, s,
+                        state, cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes,
+                        !Ctx().exact_products);
+      }
       Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, residual);
       ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
       ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
@@ -539,6 +547,7 @@ ACCEL_LLAMA_API AccelLlama* accel_llama_create(const AccelLlamaConfig* config) {
     m->prompt_ids = DevBuf(ctx * sizeof(int32_t));
     m->words = DevBuf(64);
     m->attn_work = DevBuf(AttentionWorkBytes(1, config->heads, config->context - 1, dim));
+    m->attn_arrivals = DevBuf(static_cast<size_t>(config->heads) * sizeof(uint32_t));
     for (int32_t l = 0; l < config->layers; ++l) {
       m->k_cache.emplace_back(k_n * f);
       m->v_cache.emplace_back(k_n * f);

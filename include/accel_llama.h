@@ -77,7 +77,8 @@ ACCEL_LLAMA_API int accel_llama_logit_max_abs(AccelLlama* model, const float* re
 /* Uncounted read of the logit row (no reference counterpart; for tests). */
 ACCEL_LLAMA_API int accel_llama_logits(AccelLlama* model, float* out, int32_t count);
 /* No reference counterpart (a test seam): enable 0 runs the RMSNorms and SiLU*up of a
- * one-row (decode) forward as separate kernels instead of inside the next int8 GEMV. Both
+ * one-row (decode) forward as separate kernels instead of inside the next int8 GEMV, and
+ * its RoPE + KV append, attention and chunk combine as three kernels instead of one. Both
  * forms store the same bits. Default 1. */
 ACCEL_LLAMA_API int accel_llama_set_fused_inputs(AccelLlama* model, int32_t enable);
 ACCEL_LLAMA_API void accel_llama_reset(AccelLlama* model);
