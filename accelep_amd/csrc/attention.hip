@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void AttentionKernel(const float* q, cons
     scores[t] = sc;
     local_max = fmaxf(local_max, sc);
   }
-  for (int off = 32; off > 0; off >>= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, off));
+  local_max = WaveButterfly(local_max, [](float a, float b) { return fmaxf(a, b); });
   if ((tid & 63) == 0) red[tid >> 6] = local_max;
   __syncthreads();
   float top = red[0];
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void AttentionKernel(const float* q, cons
     scores[t] = e;
     local_sum = __fadd_rn(local_sum, e);
   }
-  for (int off = 32; off > 0; off >>= 1) local_sum = __fadd_rn(local_sum, __shfl_xor(local_sum, off));
+  local_sum = WaveButterfly(local_sum, [](float a, float b) { return __fadd_rn(a, b); });
   if ((tid & 63) == 0) red[tid >> 6] = local_sum;
   __syncthreads();
   float sum = red[0];
@@ -199,11 +199,11 @@ __global__ __launch_bounds__(kSplitThreads) void AttentionChunkKernel(const floa
   if (tid < 64) {  // wave 0: chunk max, exps, their sum
     const float x = tid < n ? es[tid] : -INFINITY;
     float m = x;
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = WaveButterfly(m, [](float a, float b) { return fmaxf(a, b); });
     const float e = tid < n ? expf(__fsub_rn(x, m)) : 0.f;
     if (tid < n) es[tid] = e;
     float l = e;
-    for (int off = 32; off > 0; off >>= 1) l = __fadd_rn(l, __shfl_xor(l, off));
+    l = WaveButterfly(l, [](float a, float b) { return __fadd_rn(a, b); });
     if (tid == 0) {
       red[0] = m;
       red[1] = l;
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64) void AttentionCombineKernel(const float* partia
     lsum[c] = p[c * stride + 1];
     big = fmaxf(big, wts[c]);
   }
-  for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+  big = WaveButterfly(big, [](float a, float b) { return fmaxf(a, b); });
   __syncthreads();
   for (int64_t c = tid; c < chunks; c += 64) wts[c] = wts[c] == -INFINITY ? 0.f : expf(__fsub_rn(wts[c], big));
   __syncthreads();
@@ -399,8 +399,8 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
           dot = __builtin_fmaf(qv[i + 2], x.z, dot);
           dot = __builtin_fmaf(qv[i + 3], x.w, dot);
         }
-        dot = dot + __shfl_xor(dot, 1);
-        dot = dot + __shfl_xor(dot, 2);
+        dot = dot + XorLane<1>(dot);
+        dot = dot + XorLane<2>(dot);
         const int64_t t = t0 + g + j;
         sc[j] = (t < kend && t <= last_key) ? __fmul_rn(dot, scale) : -INFINITY;
       }
@@ -570,11 +570,11 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   if (tid < 64) {  // wave 0: chunk max, exps, their sum
     const float x = tid < n ? es[tid] : -INFINITY;
     float m = x;
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = WaveButterfly(m, [](float a, float b) { return fmaxf(a, b); });
     const float e = tid < n ? expf(__fsub_rn(x, m)) : 0.f;
     if (tid < n) es[tid] = e;
     float l = e;
-    for (int off = 32; off > 0; off >>= 1) l = __fadd_rn(l, __shfl_xor(l, off));
+    l = WaveButterfly(l, [](float a, float b) { return __fadd_rn(a, b); });
     if (tid == 0) {
       red[0] = m;
       red[1] = l;
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
       lsum[ch] = load(&p[ch * (2 + kStepDim) + 1]);
       big = fmaxf(big, wts[ch]);
     }
-    for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+    big = WaveButterfly(big, [](float a, float b) { return fmaxf(a, b); });
     for (int64_t ch = tid; ch < live; ch += 64) wts[ch] = wts[ch] == -INFINITY ? 0.f : expf(__fsub_rn(wts[ch], big));
   }
   __syncthreads();

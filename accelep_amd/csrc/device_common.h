@@ -47,6 +47,56 @@ __device__ __forceinline__ void StoreC(float* c, int64_t i, int64_t j, int64_t n
   }
 }
 
+// Lane exchange without LDS: the value of lane l ^ kOff (kOff in 1, 2, 4, 8, 16, 32), as
+// __shfl_xor returns it, from VALU lane moves instead of an LDS permute round trip. Across
+// wave halves and 16-lane rows, v_permlane32_swap / v_permlane16_swap of x with itself leaves
+// the partner half (row) in one of its two results; inside a row, DPP: row_ror:8 is xor 8,
+// row_shr:4 into banks 1 and 3 plus row_shl:4 into banks 0 and 2 is xor 4, and quad_perm
+// gives xor 2 and xor 1.
+template <int kOff>
+__device__ __forceinline__ unsigned XorLaneBits(unsigned x) {
+  static_assert(kOff == 1 || kOff == 2 || kOff == 4 || kOff == 8 || kOff == 16 || kOff == 32, "lane xor offset");
+  if constexpr (kOff == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+  } else if constexpr (kOff == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+  } else if constexpr (kOff == 8) {
+    return static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x128, 0xf, 0xf, false));
+  } else if constexpr (kOff == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xf, 0xa, false);
+    return static_cast<unsigned>(__builtin_amdgcn_update_dpp(up, static_cast<int>(x), 0x104, 0xf, 0x5, false));
+  } else if constexpr (kOff == 2) {
+    return static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4e, 0xf, 0xf, false));
+  } else {
+    return static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xb1, 0xf, 0xf, false));
+  }
+}
+template <int kOff, typename T>
+__device__ __forceinline__ T XorLane(T x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte lane values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, XorLaneBits<kOff>(__builtin_bit_cast(unsigned, x)));
+  } else {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+    const unsigned lo = XorLaneBits<kOff>(static_cast<unsigned>(b));
+    const unsigned hi = XorLaneBits<kOff>(static_cast<unsigned>(b >> 32));
+    return __builtin_bit_cast(T, (static_cast<unsigned long long>(hi) << 32) | lo);
+  }
+}
+// x = op(x, x of lane l ^ off) for off = 32, 16, 8, 4, 2, 1: the butterfly of a
+// `for (off = 32; off > 0; off >>= 1)` loop over __shfl_xor, with the same operands.
+template <typename T, typename Op>
+__device__ __forceinline__ T WaveButterfly(T x, Op op) {
+  x = op(x, XorLane<32>(x));
+  x = op(x, XorLane<16>(x));
+  x = op(x, XorLane<8>(x));
+  x = op(x, XorLane<4>(x));
+  x = op(x, XorLane<2>(x));
+  return op(x, XorLane<1>(x));
+}
+
 // Signed byte b of a dword to float, exact.
 __device__ __forceinline__ float ByteToFloat(uint32_t word, int b) {
   return static_cast<float>(static_cast<int32_t>(word << (24 - 8 * b)) >> 24);

@@ -62,7 +62,7 @@ __global__ void RmsNormKernel(const float* x, const float* w, float* y, int64_t 
     const double v = static_cast<double>(in[i]);
     ss += v * v;
   }
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  ss = WaveButterfly(ss, [](double a, double b) { return a + b; });
   if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
   __syncthreads();
   double total = 0.0;

@@ -233,27 +233,44 @@ __device__ __forceinline__ void ComputeNarrowBatch(const NarrowBatch<M, U>& b, i
   }
 }
 
+__device__ __forceinline__ unsigned FloatBits(float x) { return __builtin_bit_cast(unsigned, x); }
+__device__ __forceinline__ float BitsFloat(unsigned x) { return __builtin_bit_cast(float, x); }
+// x from lane l ^ 8 (row_ror:8 inside each 16-lane row), l + 7 - 2 (l % 8) (row_half_mirror),
+// l ^ 2 and l ^ 1 (quad_perm).
+template <int kCtrl>
+__device__ __forceinline__ float Dpp(float x) {
+  return BitsFloat(static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(FloatBits(x)), kCtrl, 0xf, 0xf,
+                                                                     false)));
+}
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppQuadXor2 = 0x4e;  // quad_perm [2, 3, 0, 1]
+constexpr int kDppQuadXor1 = 0xb1;  // quad_perm [1, 0, 3, 2]
+
 // Sums one value per column over the 64 lanes of a wave: three halving exchanges leave lane l
-// with column (l >> 3) & 7 summed over its 8-lane group, three more finish the sum.
+// with column (l >> 3) & 7 summed over its 8-lane group, three more finish the sum. The
+// exchanges are VALU lane moves (v_permlane32_swap between wave halves, v_permlane16_swap
+// between 16-lane rows, DPP inside a row), not LDS round trips. With A = column i and
+// B = column i + 4, the 32-lane swap leaves [A.lo, B.lo] and [A.hi, B.hi], whose sum holds
+// column i in the low half and column i + 4 in the high half; the 16-lane swap does the same
+// between rows 0/1 and 2/3.
 __device__ __forceinline__ float WaveColumnSum8(const float (&v8)[kNarrowTile], int lane) {
-  const bool h1 = lane & 32, h2 = lane & 16, h3 = lane & 8;
   float v4[4], v2[2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float send = h1 ? v8[i] : v8[i + 4];
-    const float keep = h1 ? v8[i + 4] : v8[i];
-    v4[i] = keep + __shfl_xor(send, 32);
+    const auto r = __builtin_amdgcn_permlane32_swap(FloatBits(v8[i]), FloatBits(v8[i + 4]), false, false);
+    v4[i] = BitsFloat(r[0]) + BitsFloat(r[1]);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const float send = h2 ? v4[i] : v4[i + 2];
-    const float keep = h2 ? v4[i + 2] : v4[i];
-    v2[i] = keep + __shfl_xor(send, 16);
+    const auto r = __builtin_amdgcn_permlane16_swap(FloatBits(v4[i]), FloatBits(v4[i + 2]), false, false);
+    v2[i] = BitsFloat(r[0]) + BitsFloat(r[1]);
   }
-  float v = (h3 ? v2[1] : v2[0]) + __shfl_xor(h3 ? v2[0] : v2[1], 8);
-  v = v + __shfl_xor(v, 4);
-  v = v + __shfl_xor(v, 2);
-  v = v + __shfl_xor(v, 1);
+  const bool h3 = lane & 8;
+  float v = (h3 ? v2[1] : v2[0]) + Dpp<kDppRowRor8>(h3 ? v2[0] : v2[1]);
+  v = v + Dpp<kDppRowHalfMirror>(v);
+  v = v + Dpp<kDppQuadXor2>(v);
+  v = v + Dpp<kDppQuadXor1>(v);
   return v;
 }
 
@@ -283,7 +300,7 @@ __device__ __forceinline__ void StageInputRow(const GemvArgs& p, float* a_stage,
       const double v = static_cast<double>(p.a[i]);
       ss += v * v;
     }
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = WaveButterfly(ss, [](double a, double b) { return a + b; });
     if ((tid & 63) == 0) part[tid >> 6] = ss;
     __syncthreads();
     double total = 0.0;

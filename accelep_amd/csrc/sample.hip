@@ -33,7 +33,7 @@ __device__ __forceinline__ uint32_t XorShift32(uint32_t x) {
 
 template <class T>
 __device__ T BlockSum(T v, T* scratch) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  v = WaveButterfly(v, [](T a, T b) { return a + b; });
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -76,12 +76,12 @@ __device__ __forceinline__ Best Better(Best a, Best b) {
 }
 
 __device__ Best BlockArgmax(Best b, float* sv, int64_t* si) {
-  for (int off = 32; off > 0; off >>= 1) {
-    Best o;
-    o.v = __shfl_xor(b.v, off);
-    o.i = __shfl_xor(b.i, off);
-    b = Better(b, o);
-  }
+  b = Better(b, Best{XorLane<32>(b.v), XorLane<32>(b.i)});
+  b = Better(b, Best{XorLane<16>(b.v), XorLane<16>(b.i)});
+  b = Better(b, Best{XorLane<8>(b.v), XorLane<8>(b.i)});
+  b = Better(b, Best{XorLane<4>(b.v), XorLane<4>(b.i)});
+  b = Better(b, Best{XorLane<2>(b.v), XorLane<2>(b.i)});
+  b = Better(b, Best{XorLane<1>(b.v), XorLane<1>(b.i)});
   __syncthreads();
   if ((threadIdx.x & 63) == 0) {
     sv[threadIdx.x >> 6] = b.v;

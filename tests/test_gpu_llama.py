@@ -118,14 +118,14 @@ def test_llama_full_size_matches_reference():
         eng.close()
 
 
-@pytest.mark.parametrize("count", [9, 64, 65, 150])
+@pytest.mark.parametrize("count", [9, 64, 65, 150, 8250])
 def test_decode_row_fused_inputs_match_separate_passes(count):
     """A one-row forward folds the RMSNorms and SiLU*up into the next int8 GEMV and runs RoPE,
     the KV append, the chunked attention and its combine as one kernel; the logits must
     carry exactly the bits of the separate-kernel forward. The prompt lengths put the new
     position inside the first 64-position chunk, at its last slot, at the first slot of the
-    second, and in a third chunk."""
-    cfg = dict(llama_config("smol3"), layers=2, context=160)
+    second, in a third chunk, and in the 129th."""
+    cfg = dict(llama_config("smol3"), layers=2, context=max(160, count + 16))
     w, q = llama_weights(cfg, 103)
     prompt = np.random.default_rng(5).integers(0, cfg["vocab"], size=count).astype(np.int32)
     eng = Engine(cfg, w, q)
