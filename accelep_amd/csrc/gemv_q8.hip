@@ -331,8 +331,11 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int tile = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
-  if (tile >= p.tiles) return;
+  // A workgroup past the last tile (the grid is a multiple of the XCD count) recomputes the
+  // last tile and stores nothing: no branch on the arguments before the loads are issued.
+  const int tile_raw = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
+  const bool tile_live = tile_raw < p.tiles;
+  const int tile = tile_live ? tile_raw : p.tiles - 1;
   const int split = blockIdx.y;
   const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
   const int64_t ke = min(p.k, kb + p.rows_per_split);
@@ -418,7 +421,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
     if ((lane & 7) == 0) red[wave][mm][lane >> 3] = v;
   }
   __syncthreads();
-  if (tid < M * kNarrowTile) {
+  if (tile_live && tid < M * kNarrowTile) {
     const int mm = tid / kNarrowTile;
     const int c = tid % kNarrowTile;
     const int64_t col = col0 + c;
@@ -431,6 +434,82 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
         const float cs = p.mode == kScalePerRow ? 1.f : col_scale;
         StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(s, cs), mm, col, p.n, p.epi));
       }
+    }
+  }
+}
+
+// The m = 1 product on staged tiles with k <= 4096 (one batch), no zero points and no per-row
+// scale: the headline shape and the decode GEMVs without an input prologue. The arithmetic is
+// GemvNarrowKernel<1>'s (the same load, compute and reduction helpers), so both kernels store
+// the same bits. What differs is the entry and the exit. The pointers and sizes come first
+// among the arguments and nothing branches on an argument before the weight loads are
+// issued (the general kernel reads its fields from one argument struct, and the compiler
+// spreads those reads over three or four dependent rounds ahead of the first weight load).
+// The epilogue's arguments, bias and residual values are read while the weight loads are in
+// flight instead of after the sums, so the last workgroup's store waits for no memory.
+template <int kSteps, bool kClamp, bool kPlain>
+__global__ __launch_bounds__(NarrowShape<1>::kThreads)
+__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOpNone>()))) void GemvM1Kernel(
+    const int8_t* tiled, const float* a, const float* scale, float* c, int32_t k, int32_t n, int32_t tiles,
+    int32_t tiles_per_xcd, int32_t scale_index_mul, int32_t const_index, Epilogue epi) {
+  using S = NarrowShape<1>;
+  static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
+  __shared__ float red[S::kWaves][kNarrowTile];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tile_raw = (blockIdx.x % kXcds) * tiles_per_xcd + blockIdx.x / kXcds;
+  const bool tile_live = tile_raw < tiles;
+  const int tile = tile_live ? tile_raw : tiles - 1;
+  const int8_t* tbase = tiled + static_cast<int64_t>(tile) * k * kNarrowTile;  // k is even
+  const int col = tile * kNarrowTile + (tid & 7);
+  const int colc = col < n ? col : n - 1;
+  // Per-column scale: index col (scale_index_mul 1); whole tensor: const_index (mul 0).
+  const float col_scale = scale[scale_index_mul * colc + const_index];
+  const float* const arow[1] = {a};
+  const GemvArgs unused{};
+  NarrowBatch<1, kSteps> b;
+  LoadNarrowBatch<1, kSteps, false, false, true, kClamp>(unused, arow, 2 * tid, k, k, tbase, b);
+  __builtin_amdgcn_sched_barrier(0);
+  float bias_v = 0.f;
+  float res_v = 0.f;
+  if (!kPlain) {
+    if (epi.bias != nullptr) bias_v = epi.bias[BiasIndex(epi, 0, colc)];
+    if (epi.residual != nullptr) res_v = epi.residual[colc];
+    asm volatile("" ::"s"(epi.alpha), "s"(epi.beta), "s"(epi.activation), "s"(epi.split[0]), "s"(epi.split[1]),
+                 "s"(epi.c2), "s"(epi.c3));
+  }
+  float acc[1][kNarrowTile];
+  float zc[kNarrowTile];
+#pragma unroll
+  for (int cc = 0; cc < kNarrowTile; ++cc) {
+    acc[0][cc] = 0.f;
+    zc[cc] = 0.f;
+  }
+  ComputeNarrowBatch<1, kSteps, false, false, kClamp>(b, 2 * tid, k, zc, acc);
+  const float v = WaveColumnSum8(acc[0], lane);
+  if ((lane & 7) == 0) red[wave][lane >> 3] = v;
+  __syncthreads();
+  if (tile_live && tid < kNarrowTile && col < n) {
+    float sum = red[0][tid];
+#pragma unroll
+    for (int wv = 1; wv < S::kWaves; ++wv) sum = sum + red[wv][tid];
+    const float x = __fmul_rn(sum, col_scale);
+    if (kPlain) {
+      c[col] = x;
+    } else {
+      // ApplyEpilogue's steps and roundings, with the bias and residual already loaded.
+      float y = __fmul_rn(epi.alpha, x);
+      if (epi.bias != nullptr) y = __fadd_rn(y, __fmul_rn(epi.beta, bias_v));
+      if (epi.activation == ACCEL_HIP_ACT_RELU) {
+        if (y < 0.f) y = 0.f;
+      } else if (epi.activation == ACCEL_HIP_ACT_GELU) {
+        const float half = __fmul_rn(0.5f, y);
+        const float arg = __fmul_rn(y, 0.7071067811865476f);
+        y = __fmul_rn(half, __fadd_rn(1.f, erff(arg)));
+      }
+      if (epi.residual != nullptr) y = __fadd_rn(y, res_v);
+      StoreC(c, 0, col, n, epi, y);
     }
   }
 }
@@ -730,7 +809,46 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   const dim3 grid(static_cast<uint32_t>(tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
   if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
-    if (a_op == kAOpRms) {
+    if (m == 1 && a_op == kAOpNone && !zero && !row_scale && splits == 1 && pair_a &&
+        k <= NarrowShape<1>::kBatchRows && n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
+        epi.rms_weight == nullptr) {
+      const int steps = static_cast<int>((k + NarrowShape<1>::kStepRows - 1) / NarrowShape<1>::kStepRows);
+      const bool clamp = k != steps * NarrowShape<1>::kStepRows;
+      const bool plain = epi.Identity() && epi.split[0] == 0;
+      const int32_t mul = b.mode == kScalePerCol ? 1 : 0;
+      const int32_t cidx = b.mode == kScalePerCol ? 0 : static_cast<int32_t>(b.const_index);
+      const dim3 block(NarrowShape<1>::kThreads);
+#define ACCEL_GEMV_M1(ST, CL)                                                                                          \
+  do {                                                                                                                 \
+    if (plain)                                                                                                         \
+      hipLaunchKernelGGL((GemvM1Kernel<ST, CL, true>), grid, block, 0, stream, b.tiled, a, b.scale, c,                \
+                         static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),              \
+                         static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi);                                        \
+    else                                                                                                               \
+      hipLaunchKernelGGL((GemvM1Kernel<ST, CL, false>), grid, block, 0, stream, b.tiled, a, b.scale, c,               \
+                         static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),              \
+                         static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi);                                        \
+  } while (0)
+      switch (steps * 2 + (clamp ? 1 : 0)) {
+        case 2: ACCEL_GEMV_M1(1, false); break;
+        case 3: ACCEL_GEMV_M1(1, true); break;
+        case 4: ACCEL_GEMV_M1(2, false); break;
+        case 5: ACCEL_GEMV_M1(2, true); break;
+        case 6: ACCEL_GEMV_M1(3, false); break;
+        case 7: ACCEL_GEMV_M1(3, true); break;
+        case 8: ACCEL_GEMV_M1(4, false); break;
+        case 9: ACCEL_GEMV_M1(4, true); break;
+        case 10: ACCEL_GEMV_M1(5, false); break;
+        case 11: ACCEL_GEMV_M1(5, true); break;
+        case 12: ACCEL_GEMV_M1(6, false); break;
+        case 13: ACCEL_GEMV_M1(6, true); break;
+        case 14: ACCEL_GEMV_M1(7, false); break;
+        case 15: ACCEL_GEMV_M1(7, true); break;
+        case 16: ACCEL_GEMV_M1(8, false); break;
+        default: ACCEL_GEMV_M1(8, true); break;
+      }
+#undef ACCEL_GEMV_M1
+    } else if (a_op == kAOpRms) {
       // The staged row in LDS is 16-byte aligned and k is whole, so pairs load as one.
       if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpRms>), grid,
                                          dim3(NarrowShape<1>::kThreads), 0, stream, args);
