@@ -446,15 +446,18 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
 // issued (the general kernel reads its fields from one argument struct, and the compiler
 // spreads those reads over three or four dependent rounds ahead of the first weight load).
 // The epilogue's arguments, bias and residual values are read while the weight loads are in
-// flight instead of after the sums, so the last workgroup's store waits for no memory.
-template <int kSteps, bool kClamp, bool kPlain>
+// flight instead of after the sums, so the last workgroup's store waits for no memory. With
+// an input prologue (kAOp) the weight loads are issued first, the transformed row is staged
+// in LDS (StageInputRow) while they are in flight, and A is read from there.
+template <int kSteps, bool kClamp, bool kPlain, int kAOp>
 __global__ __launch_bounds__(NarrowShape<1>::kThreads)
-__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOpNone>()))) void GemvM1Kernel(
+__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) void GemvM1Kernel(
     const int8_t* tiled, const float* a, const float* scale, float* c, int32_t k, int32_t n, int32_t tiles,
-    int32_t tiles_per_xcd, int32_t scale_index_mul, int32_t const_index, Epilogue epi) {
+    int32_t tiles_per_xcd, int32_t scale_index_mul, int32_t const_index, Epilogue epi, GemvPrologue pro) {
   using S = NarrowShape<1>;
   static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
   __shared__ float red[S::kWaves][kNarrowTile];
+  __shared__ __align__(16) float a_stage[kAOp != kAOpNone ? kGemvPrologueMaxK : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -466,10 +469,24 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOpNone>()))
   const int colc = col < n ? col : n - 1;
   // Per-column scale: index col (scale_index_mul 1); whole tensor: const_index (mul 0).
   const float col_scale = scale[scale_index_mul * colc + const_index];
-  const float* const arow[1] = {a};
   const GemvArgs unused{};
   NarrowBatch<1, kSteps> b;
-  LoadNarrowBatch<1, kSteps, false, false, true, kClamp>(unused, arow, 2 * tid, k, k, tbase, b);
+  if (kAOp == kAOpNone) {
+    const float* const arow[1] = {a};
+    LoadNarrowBatch<1, kSteps, false, false, true, kClamp>(unused, arow, 2 * tid, k, k, tbase, b);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    __shared__ double part[S::kWaves];
+    GemvArgs staged{};
+    staged.a = a;
+    staged.k = k;
+    staged.pro = pro;
+    StageInputRow<kAOp, S::kThreads>(staged, a_stage, part);
+    const float* const srow[1] = {a_stage};
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) LoadNarrowAAt<1, kSteps, false, false, true, kClamp>(u, unused, srow, 2 * tid, k, b);
+  }
   __builtin_amdgcn_sched_barrier(0);
   float bias_v = 0.f;
   float res_v = 0.f;
@@ -809,25 +826,27 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   const dim3 grid(static_cast<uint32_t>(tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
   if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
-    if (m == 1 && a_op == kAOpNone && !zero && !row_scale && splits == 1 && pair_a &&
-        k <= NarrowShape<1>::kBatchRows && n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
-        epi.rms_weight == nullptr) {
+    // The prologue row lives in LDS (16-byte aligned), so only an even k is needed there.
+    const bool m1_pairs = a_op == kAOpNone ? pair_a : k % 2 == 0;
+    if (m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
+        n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) && epi.rms_weight == nullptr) {
       const int steps = static_cast<int>((k + NarrowShape<1>::kStepRows - 1) / NarrowShape<1>::kStepRows);
       const bool clamp = k != steps * NarrowShape<1>::kStepRows;
-      const bool plain = epi.Identity() && epi.split[0] == 0;
+      const bool plain = epi.Identity() && epi.split[0] == 0 && a_op == kAOpNone;
+      const GemvPrologue pro = prologue != nullptr ? *prologue : GemvPrologue{};
       const int32_t mul = b.mode == kScalePerCol ? 1 : 0;
       const int32_t cidx = b.mode == kScalePerCol ? 0 : static_cast<int32_t>(b.const_index);
       const dim3 block(NarrowShape<1>::kThreads);
-#define ACCEL_GEMV_M1(ST, CL)                                                                                          \
-  do {                                                                                                                 \
-    if (plain)                                                                                                         \
-      hipLaunchKernelGGL((GemvM1Kernel<ST, CL, true>), grid, block, 0, stream, b.tiled, a, b.scale, c,                \
-                         static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),              \
-                         static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi);                                        \
-    else                                                                                                               \
-      hipLaunchKernelGGL((GemvM1Kernel<ST, CL, false>), grid, block, 0, stream, b.tiled, a, b.scale, c,               \
-                         static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),              \
-                         static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi);                                        \
+#define ACCEL_GEMV_M1_K(ST, CL, PL, OP)                                                                        \
+  hipLaunchKernelGGL((GemvM1Kernel<ST, CL, PL, OP>), grid, block, 0, stream, b.tiled, a, b.scale, c,            \
+                     static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),            \
+                     static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi, pro)
+#define ACCEL_GEMV_M1(ST, CL)                                                               \
+  do {                                                                                      \
+    if (a_op == kAOpRms) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRms);                           \
+    else if (a_op == kAOpSiluUp) ACCEL_GEMV_M1_K(ST, CL, false, kAOpSiluUp);                \
+    else if (plain) ACCEL_GEMV_M1_K(ST, CL, true, kAOpNone);                                \
+    else ACCEL_GEMV_M1_K(ST, CL, false, kAOpNone);                                          \
   } while (0)
       switch (steps * 2 + (clamp ? 1 : 0)) {
         case 2: ACCEL_GEMV_M1(1, false); break;
@@ -848,6 +867,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
         default: ACCEL_GEMV_M1(8, true); break;
       }
 #undef ACCEL_GEMV_M1
+#undef ACCEL_GEMV_M1_K
     } else if (a_op == kAOpRms) {
       // The staged row in LDS is 16-byte aligned and k is whole, so pairs load as one.
       if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpRms>), grid,
