@@ -482,8 +482,8 @@ constexpr int kStepDim = 64;
 
 __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
     const float* q_raw, const float* k_raw, const float* v_raw, float* k_cache, float* v_cache, const float* cos_t,
-    const float* sin_t, float* out, int64_t position_arg, const int32_t* position_dev, int64_t heads,
-    int64_t kv_heads, int64_t chunks_max, float* partial, uint32_t* arrivals) {
+    const float* sin_t, float* out, int32_t position_arg, const int32_t* position_dev, int32_t group,
+    int32_t kv_heads, int32_t chunks_max, float* partial, uint32_t* arrivals) {
   __shared__ __align__(16) float qs[kStepDim];
   __shared__ __align__(16) float knew[kStepDim];
   __shared__ __align__(16) float vnew[kStepDim];
@@ -493,19 +493,24 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   __shared__ float wts[kMaxChunks];
   __shared__ float lsum[kMaxChunks];
   __shared__ int is_last;
-  const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
-  const int64_t h = blockIdx.x;
-  const int64_t c = blockIdx.y;
-  const int64_t group = heads / kv_heads;
-  const int64_t kv = h / group;
-  const int64_t total = position + 1;
-  const int64_t live = (total + kChunk - 1) / kChunk;
+  // 32-bit indexes (the launcher checks that the caches and partials fit them): no 64-bit
+  // division or multiply stands between the position read and the first loads. The pointer
+  // arguments are read in the same round as the position's address (the compiler would read
+  // them after the position and the live-chunk test).
+  asm volatile("" ::"s"(k_cache), "s"(v_cache), "s"(q_raw), "s"(k_raw), "s"(v_raw), "s"(cos_t), "s"(sin_t),
+               "s"(position_arg), "s"(group), "s"(kv_heads), "s"(chunks_max));
+  const int position = position_dev != nullptr ? *position_dev : position_arg;
+  const int h = blockIdx.x;
+  const int c = blockIdx.y;
+  const int kv = h / group;  // group = heads / kv_heads
+  const int total = position + 1;
+  const int live = (total + kChunk - 1) / kChunk;
   if (c >= live) return;  // uniform over the workgroup
-  const int64_t t0 = c * kChunk;
-  const int64_t n = min<int64_t>(kChunk, total - t0);
+  const int t0 = c * kChunk;
+  const int n = min(kChunk, total - t0);
   const bool tail = t0 + n == total;  // this chunk holds the new position
   const int tid = threadIdx.x;
-  const int64_t kv_row = kv_heads * kStepDim;
+  const int kv_row = kv_heads * kStepDim;
 
   // Loads that do not depend on the rotation are issued first: the key row of this lane
   // (wave 0) and the value rows of this thread's (position group, column quad).
@@ -523,7 +528,7 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   float4 vx[kChunk / kGroups];
 #pragma unroll
   for (int i = 0; i < kChunk / kGroups; ++i) {
-    const int64_t t = g + i * kGroups;
+    const int t = g + i * kGroups;
     if (t < n && t0 + t != position)
       vx[i] = *reinterpret_cast<const float4*>(v_cache + (t0 + t) * kv_row + kv * kStepDim + cc * kCols);
   }
@@ -544,7 +549,7 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
     vnew[tid - 64] = v_raw[kv * kStepDim + (tid - 64)];
   }
   __syncthreads();
-  if (tail && h % group == 0 && tid < kStepDim) {
+  if (tail && h == kv * group && tid < kStepDim) {
     k_cache[position * kv_row + kv * kStepDim + tid] = knew[tid];
     v_cache[position * kv_row + kv * kStepDim + tid] = vnew[tid];
   }
@@ -585,7 +590,7 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   float acc[kCols] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < kChunk / kGroups; ++i) {
-    const int64_t t = g + i * kGroups;
+    const int t = g + i * kGroups;
     if (t < n) {
       const float e = es[t];
       const float4 x4 = t0 + t == position ? reinterpret_cast<const float4*>(vnew)[cc] : vx[i];
@@ -622,20 +627,20 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   const auto load = [](const float* x) { return __hip_atomic_load(x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   if (tid < 64) {
     float big = -INFINITY;
-    for (int64_t ch = tid; ch < live; ch += 64) {
+    for (int ch = tid; ch < live; ch += 64) {
       wts[ch] = load(&p[ch * (2 + kStepDim)]);
       lsum[ch] = load(&p[ch * (2 + kStepDim) + 1]);
       big = fmaxf(big, wts[ch]);
     }
     big = WaveButterfly(big, [](float a, float b) { return fmaxf(a, b); });
-    for (int64_t ch = tid; ch < live; ch += 64) wts[ch] = wts[ch] == -INFINITY ? 0.f : expf(__fsub_rn(wts[ch], big));
+    for (int ch = tid; ch < live; ch += 64) wts[ch] = wts[ch] == -INFINITY ? 0.f : expf(__fsub_rn(wts[ch], big));
   }
   __syncthreads();
   if (tid < kStepDim) {
     float l = 0.f;
-    for (int64_t ch = 0; ch < live; ++ch) l = __fadd_rn(l, __fmul_rn(wts[ch], lsum[ch]));
+    for (int ch = 0; ch < live; ++ch) l = __fadd_rn(l, __fmul_rn(wts[ch], lsum[ch]));
     float o = 0.f;
-    int64_t ch = 0;
+    int ch = 0;
     for (; ch + 8 <= live; ch += 8) {
       float x[8];
 #pragma unroll
@@ -745,11 +750,14 @@ bool LaunchDecodeAttention(const float* q, const float* k, const float* v, float
   if (!aligned(k_cache) || !aligned(v_cache)) return false;
   const int64_t top = position_dev != nullptr ? max_position : position;
   const int64_t chunks = (top + 1 + kChunk - 1) / kChunk;
-  if (chunks > kMaxChunks || heads > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention context is too long for a decode step");
+  if (chunks > kMaxChunks || heads > 65535 || chunks * kChunk * kv_heads * kStepDim > 0x7fffffff ||
+      heads * chunks * (2 + kStepDim) > 0x7fffffff)
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention context is too long for a decode step");
   if (work_bytes < AttentionWorkBytes(1, heads, top, head_dim)) Fail(ACCEL_HIP_INVALID_ARGUMENT, "attention scratch is too small");
   hipLaunchKernelGGL(DecodeAttentionKernel, dim3(static_cast<uint32_t>(heads), static_cast<uint32_t>(chunks)),
-                     dim3(kSplitThreads), 0, stream, q, k, v, k_cache, v_cache, cos_table, sin_table, out, position,
-                     position_dev, heads, kv_heads, chunks, work, arrivals);
+                     dim3(kSplitThreads), 0, stream, q, k, v, k_cache, v_cache, cos_table, sin_table, out,
+                     static_cast<int32_t>(position), position_dev, static_cast<int32_t>(heads / kv_heads),
+                     static_cast<int32_t>(kv_heads), static_cast<int32_t>(chunks), work, arrivals);
   Check(hipGetLastError(), "DecodeAttentionKernel launch");
   return true;
 }
