@@ -175,6 +175,7 @@ struct Model {
   }
 
   // One row through an int8 weight on the GEMV, with the input transform done inside it.
+  static constexpr int64_t kFusedNormMaxOut = 8192;
   bool Fusable(const Linear& w, int64_t m) const {
     return fuse_inputs && m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
   }
@@ -188,8 +189,10 @@ struct Model {
     LaunchGemvQ8(x, v, c, 1, w.in, w.out, e, ctx.stream, &pro);
   }
   // c = RMSNorm(x; norm) @ W: one kernel for a decode row, else the norm pass into `normed`.
+  // A wide product (the LM head: 6144 workgroups) takes the separate pass too, rather than
+  // every workgroup reading and normalizing the row again.
   void ApplyNormed(const Linear& w, const float* x, const DevBuf& norm, float* c, int64_t m, const Epilogue& e) {
-    if (Fusable(w, m)) {
+    if (Fusable(w, m) && w.out <= kFusedNormMaxOut) {
       GemvPrologue pro;
       pro.rms_weight = norm.as<float>();
       pro.rms_eps = cfg.eps;
