@@ -106,20 +106,35 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* logits, in
   const int tid = threadIdx.x;
 
   if (!(temperature > 0.f)) {
-    // 8 loads in flight per thread; Better is a total order (larger value, then smaller
-    // id), so the order in which candidates meet does not change the winner.
-    constexpr int kUnroll = 8;
+    // Better is a total order (larger value, then smaller id), so the order in which
+    // candidates meet does not change the winner. The row is read as 16-byte pieces, twelve
+    // in flight per thread: a 49152-id row is one round of loads.
+    constexpr int kVec = 12;
     Best b{0.f, -1};
-    int64_t i = tid;
-    for (; i + (kUnroll - 1) * kThreads < vocab; i += kUnroll * kThreads) {
-      float v[kUnroll];
+    const int64_t nvec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 ? vocab / 4 : 0;
+    const float4* l4 = reinterpret_cast<const float4*>(logits);
+    int64_t j = tid;
+    for (; j + (kVec - 1) * kThreads < nvec; j += kVec * kThreads) {
+      float4 v[kVec];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) v[u] = logits[i + u * kThreads];
+      for (int u = 0; u < kVec; ++u) v[u] = l4[j + u * kThreads];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        if (!isnan(v[u])) b = Better(b, Best{v[u], i + u * kThreads});
+      for (int u = 0; u < kVec; ++u) {
+        const int64_t i0 = 4 * (j + u * kThreads);
+        if (!isnan(v[u].x)) b = Better(b, Best{v[u].x, i0});
+        if (!isnan(v[u].y)) b = Better(b, Best{v[u].y, i0 + 1});
+        if (!isnan(v[u].z)) b = Better(b, Best{v[u].z, i0 + 2});
+        if (!isnan(v[u].w)) b = Better(b, Best{v[u].w, i0 + 3});
+      }
     }
-    for (; i < vocab; i += kThreads) {
+    for (; j < nvec; j += kThreads) {
+      const float4 v = l4[j];
+      if (!isnan(v.x)) b = Better(b, Best{v.x, 4 * j});
+      if (!isnan(v.y)) b = Better(b, Best{v.y, 4 * j + 1});
+      if (!isnan(v.z)) b = Better(b, Best{v.z, 4 * j + 2});
+      if (!isnan(v.w)) b = Better(b, Best{v.w, 4 * j + 3});
+    }
+    for (int64_t i = 4 * nvec + tid; i < vocab; i += kThreads) {
       const float v = logits[i];
       if (!isnan(v)) b = Better(b, Best{v, i});
     }
