@@ -228,6 +228,63 @@ def test_gemv_unaligned_a(m):
     assert_gamma_bound(c.numpy(), case["a"], dequant_host(case["bq"], k, n))
 
 
+def _gemv_m1_pair(case, epi=None):
+    """C from an 8-byte aligned A (the m = 1 entry kernel, for an even k <= 4096 without zero
+    points) and from the same A at a 4-byte offset (the general narrow kernel, single A loads)."""
+    k, n = case["k"], case["n"]
+    plane, keep = plane_from_spec(case["bq"])
+    a_al = dev(case["a"])
+    a_un = dev(np.concatenate([np.zeros(1, np.float32), case["a"].ravel()]))
+    out = []
+    for a_ptr in (a_al.ptr, a_un.at(1)):
+        c = dev(np.full((1, n), 3.0, np.float32))
+        if epi is None:
+            check(lib().accel_hip_matmul_quantized(a_ptr, None, None, C.byref(plane), c.ptr, 1, k, n))
+        else:
+            check(lib().accel_hip_matmul_quantized_fused(a_ptr, None, None, C.byref(plane), c.ptr, 1, k, n,
+                                                         C.byref(epi)))
+        out.append(c.numpy())
+    return out
+
+
+@pytest.mark.parametrize("k,n,axis", [(2, 3, 1), (510, 49, 1), (576, 1001, 1), (1000, 64, 1), (1536, 576, 1),
+                                      (4094, 17, 1), (4096, 264, -1)])
+def test_gemv_m1_entry_kernel_matches_general_kernel(k, n, axis):
+    """m = 1 with an even k <= 4096: the entry kernel issues only the 512-row steps k needs
+    (k = 510, 1000 and 4094 end inside a step) and must store the general kernel's bits;
+    n off a multiple of 8 leaves a partial last tile; axis -1 is one scale for the tensor."""
+    case = c3_case(1, k, n, 3 * k + n, axis=max(axis, 0) if axis >= 0 else 1)
+    if axis < 0:
+        case["bq"]["scale"] = np.array([0.0042], np.float32)
+        case["bq"]["axis"] = -1
+    entry, general = _gemv_m1_pair(case)
+    same_bits(entry, general)
+    assert_gamma_bound(entry, case["a"], dequant_host(case["bq"], k, n))
+
+
+def test_gemv_m1_entry_kernel_epilogues():
+    """alpha, beta * bias, Relu / exact Gelu and the residual on the m = 1 entry kernel, whose
+    epilogue inputs are loaded before the sums: the general kernel's bits and the composed
+    oracle's values."""
+    o = oracle()
+    r = np.random.default_rng(48)
+    k, n = 576, 203
+    case = c3_case(1, k, n, 49)
+    bias = r.standard_normal(n).astype(np.float32)
+    resid = r.standard_normal((1, n)).astype(np.float32)
+    bias_d = dev(bias)
+    res_d = dev(resid)
+    w = dequant_host(case["bq"], k, n)
+    base = o.reference_matmul(case["a"], w)
+    for act in (0, 1, 2):
+        e = Epilogue(alpha=1.5, beta=0.5, bias=bias_d.ptr, bias_rank=1, activation=act, residual=res_d.ptr)
+        e.bias_shape[0] = n
+        entry, general = _gemv_m1_pair(case, e)
+        same_bits(entry, general)
+        want = o.gemm_epilogue(base, 1.5, bias, [n], 0.5, act) + resid
+        np.testing.assert_allclose(entry, want, rtol=2e-5, atol=2e-5)
+
+
 @pytest.mark.parametrize("m,k,n", [(512, 576, 1536), (64, 4096, 1024), (100, 200, 300), (2048, 576, 192)])
 def test_gemm_int8_panels(m, k, n):
     """m > 16: fp32 MFMA GEMM with the int8 panel dequantized in LDS."""
