@@ -291,11 +291,9 @@ __global__ __launch_bounds__(64) void AttentionCombineKernel(const float* partia
 
 // ---- prompt rows, head_dim 64, fast mode: online softmax over key stages ------------------
 // One workgroup per (16 query rows, head); its four waves take a quarter of the keys each and
-// the quarters are combined at the end. Lane l of a wave owns query row l / 4 and dims
-// [16 (l % 4), +16): a score is 16 FMAs plus two lane exchanges. Each wave stages 16 keys
-// of K and V in its own LDS slice (coalesced loads), then for 8 keys at a time takes the
-// scores, their max, one rescale of the running sum and output, and the 8 weighted V rows
-// (online softmax). K and V are read once per 16 query rows instead of once per row. The
+// the quarters are combined at the end. Each wave stages 16 keys of K and V in its own LDS
+// slice (coalesced loads; the next stage's loads are issued while the current one is
+// multiplied), so K and V are read once per 16 query rows instead of once per row. The
 // summation order differs from the reference's sequential loops (rounding only), so this
 // path serves the fast mode; the per-row kernel above keeps the reference's score bits.
 constexpr int kFlashRows = 16;
@@ -320,42 +318,50 @@ __device__ __forceinline__ void FlashLoadStage(const float* k, const float* v, i
   }
 }
 
-__global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const float* q, const float* k,
-                                                                      const float* v, float* out, int64_t seq,
-                                                                      int64_t position_arg, int64_t heads,
-                                                                      int64_t kv_heads, const int32_t* position_dev) {
-  __shared__ __align__(16) float ks[kFlashWaves][kFlashStage][kFlashDim];
-  __shared__ __align__(16) float vs[kFlashWaves][kFlashStage][kFlashDim];
+// Both products run on v_mfma_f32_16x16x4f32. Per stage a wave forms S^T = K Q^T (16 keys x 16
+// rows, 16 MFMAs over the 64 dims) and O^T += V^T P^T (64 dims x 16 rows, 16 MFMAs). Lane l
+// serves row j = l % 16 and key group g = l / 16: the S^T tile leaves it the scores of keys
+// 4g .. 4g + 3 for row j, which is exactly its operand of P^T when the k slot g of step s is
+// key 4g + s, and the O^T tiles hold row j too, so the softmax rescale needs no lane exchange.
+// A row's max and sum meet over the four key groups through two lane swaps.
+constexpr int kMfmaPad = kFlashDim + 4;  // LDS row stride: the 16 key rows fall on distinct banks
+
+typedef float mv4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashMfmaKernel(
+    const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position_arg, int64_t heads,
+    int64_t kv_heads, const int32_t* position_dev) {
+  __shared__ __align__(16) float ks[kFlashWaves][kFlashStage][kMfmaPad];
+  __shared__ __align__(16) float vs[kFlashWaves][kFlashStage][kMfmaPad];
   __shared__ float part_m[kFlashWaves][kFlashRows];
   __shared__ float part_l[kFlashWaves][kFlashRows];
-  __shared__ __align__(16) float part_acc[kFlashWaves][kFlashRows][kFlashDim];
   const int64_t position = position_dev != nullptr ? *position_dev : position_arg;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int r = lane >> 2;   // query row in the block
-  const int qd = lane & 3;   // dim quarter
+  const int j = lane & 15;  // query row of the block
+  const int g = lane >> 4;  // key group / dim group
   const int64_t s0 = static_cast<int64_t>(blockIdx.x) * kFlashRows;
   const int64_t h = blockIdx.y;
   const int64_t kv = h / (heads / kv_heads);
-  const int64_t row = s0 + r;
+  const int64_t row = s0 + j;
   const bool live = row < seq;
   const int64_t last_key = position + (live ? row : -1);  // keys 0 .. last_key (causal)
   const float scale = __fdiv_rn(1.f, __fsqrt_rn(static_cast<float>(kFlashDim)));
 
-  float qv[16];
+  // B operand of S^T: q[row j][16 g + s], s = 0 .. 15.
+  float qb[16];
   {
-    const float* qrow = q + ((live ? row : 0) * heads + h) * kFlashDim + 16 * qd;
+    const float* qrow = q + ((live ? row : 0) * heads + h) * kFlashDim + 16 * g;
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
       const float4 x = *reinterpret_cast<const float4*>(qrow + i);
-      qv[i] = x.x;
-      qv[i + 1] = x.y;
-      qv[i + 2] = x.z;
-      qv[i + 3] = x.w;
+      qb[i] = x.x;
+      qb[i + 1] = x.y;
+      qb[i + 2] = x.z;
+      qb[i + 3] = x.w;
     }
   }
-  // Keys of the block: 0 .. position + min(s0 + 16, seq) - 1, cut into four ranges.
   const int64_t nkeys = position + min<int64_t>(s0 + kFlashRows, seq);
   const int64_t per = ((nkeys + kFlashWaves - 1) / kFlashWaves + kFlashStage - 1) / kFlashStage * kFlashStage;
   const int64_t kbeg = min<int64_t>(wave * per, nkeys);
@@ -363,12 +369,11 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
   const int64_t kv_stride = kv_heads * kFlashDim;
 
   float m = -INFINITY;
-  float l = 0.f;
-  float acc[16];
+  float l = 0.f;  // this lane's share (its key groups) of row j's sum
+  mv4 acc_o[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int t = 0; t < 4; ++t) acc_o[t] = mv4{0.f, 0.f, 0.f, 0.f};
 
-  // The next stage's loads are issued before the current stage is multiplied.
   f4 kx[kFlashStageLoads], vx[kFlashStageLoads];
   if (kbeg < kend) FlashLoadStage(k, v, kbeg, kend, kv_stride, kv, lane, kx, vx);
   for (int64_t t0 = kbeg; t0 < kend; t0 += kFlashStage) {  // uniform across the wave
@@ -379,90 +384,96 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashKernel(const f
       *reinterpret_cast<f4*>(&vs[wave][f >> 4][(f & 15) * 4]) = vx[i];
     }
     if (t0 + kFlashStage < kend) FlashLoadStage(k, v, t0 + kFlashStage, kend, kv_stride, kv, lane, kx, vx);
-    // The stage is this wave's alone: a wave-level fence and barrier order its writes
-    // before its reads.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // S^T[key i][row j]: A = K[key l % 16][16 g + s], B = q[row][16 g + s].
+    float kr[16];
 #pragma unroll
-    for (int g = 0; g < kFlashStage; g += 8) {
-      float sc[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float* kr = &ks[wave][g + j][16 * qd];
-        float dot = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-          const float4 x = *reinterpret_cast<const float4*>(kr + i);
-          dot = __builtin_fmaf(qv[i], x.x, dot);
-          dot = __builtin_fmaf(qv[i + 1], x.y, dot);
-          dot = __builtin_fmaf(qv[i + 2], x.z, dot);
-          dot = __builtin_fmaf(qv[i + 3], x.w, dot);
-        }
-        dot = dot + XorLane<1>(dot);
-        dot = dot + XorLane<2>(dot);
-        const int64_t t = t0 + g + j;
-        sc[j] = (t < kend && t <= last_key) ? __fmul_rn(dot, scale) : -INFINITY;
-      }
-      float mb = sc[0];
-#pragma unroll
-      for (int j = 1; j < 8; ++j) mb = fmaxf(mb, sc[j]);
-      const float m_new = fmaxf(m, mb);
-      if (m_new != -INFINITY) {  // else nothing of this row so far
-        const float corr = m == -INFINITY ? 0.f : expf(m - m_new);
-        l = l * corr;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = acc[i] * corr;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float p = sc[j] == -INFINITY ? 0.f : expf(sc[j] - m_new);
-          l = l + p;
-          const float* vr = &vs[wave][g + j][16 * qd];
-#pragma unroll
-          for (int i = 0; i < 16; i += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(vr + i);
-            acc[i] = __builtin_fmaf(p, x.x, acc[i]);
-            acc[i + 1] = __builtin_fmaf(p, x.y, acc[i + 1]);
-            acc[i + 2] = __builtin_fmaf(p, x.z, acc[i + 2]);
-            acc[i + 3] = __builtin_fmaf(p, x.w, acc[i + 3]);
-          }
-        }
-        m = m_new;
-      }
+    for (int i = 0; i < 16; i += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(&ks[wave][j][16 * g + i]);
+      kr[i] = x.x;
+      kr[i + 1] = x.y;
+      kr[i + 2] = x.z;
+      kr[i + 3] = x.w;
     }
+    mv4 st = mv4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s], qb[s], st, 0, 0, 0);
+    // Lane (j, g) holds the scores of keys t0 + 4 g + r, r = 0 .. 3, for row j.
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = t0 + 4 * g + r;
+      sc[r] = (t < kend && t <= last_key) ? __fmul_rn(st[r], scale) : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, XorLane<16>(mx));
+    mx = fmaxf(mx, XorLane<32>(mx));
+    const float m_new = fmaxf(m, mx);
+    const bool none = m_new == -INFINITY;  // nothing of this row so far
+    const float corr = (m == -INFINITY || none) ? (none ? 1.f : 0.f) : expf(m - m_new);
+    float pr[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = sc[r] == -INFINITY ? 0.f : expf(sc[r] - m_new);
+      psum = psum + pr[r];
+    }
+    l = l * corr + psum;
+    m = none ? m : m_new;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc_o[t] = acc_o[t] * corr;
+    // O^T[dim 16 t + i][row j] += V^T[dim][key 4 g + s] P^T[key 4 g + s][row j].
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc_o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[wave][4 * g + s][16 * t + j], pr[s], acc_o[t], 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();  // the stage is read before the next one overwrites it
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-
-  if (qd == 0) {
-    part_m[wave][r] = m;
-    part_l[wave][r] = l;
+  // Row j's sum over the four key groups; then the quarters meet in LDS. acc_o[t][r] is
+  // O^T[dim 16 t + 4 g + r][row j]; the wave's stage rows hold its 16 x 64 block.
+  l = l + XorLane<16>(l);
+  l = l + XorLane<32>(l);
+  float* part_acc = &ks[wave][0][0];  // [16 rows][kMfmaPad]: this wave's stage, no longer read
+  if (g == 0) {
+    part_m[wave][j] = m;
+    part_l[wave][j] = l;
   }
 #pragma unroll
-  for (int i = 0; i < 16; i += 4)
-    *reinterpret_cast<float4*>(&part_acc[wave][r][16 * qd + i]) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+  for (int t = 0; t < 4; ++t)
+    *reinterpret_cast<float4*>(&part_acc[j * kMfmaPad + 16 * t + 4 * g]) =
+        make_float4(acc_o[t][0], acc_o[t][1], acc_o[t][2], acc_o[t][3]);
   __syncthreads();
   if (wave == 0 && live) {
-    float big = part_m[0][r];
+    float big = part_m[0][j];
 #pragma unroll
-    for (int w = 1; w < kFlashWaves; ++w) big = fmaxf(big, part_m[w][r]);
+    for (int w = 1; w < kFlashWaves; ++w) big = fmaxf(big, part_m[w][j]);
     float wts[kFlashWaves];
     float total = 0.f;
 #pragma unroll
     for (int w = 0; w < kFlashWaves; ++w) {
-      wts[w] = part_m[w][r] == -INFINITY ? 0.f : expf(part_m[w][r] - big);
-      total = total + wts[w] * part_l[w][r];
+      wts[w] = part_m[w][j] == -INFINITY ? 0.f : expf(part_m[w][j] - big);
+      total = total + wts[w] * part_l[w][j];
     }
-    float* orow = out + (row * heads + h) * kFlashDim + 16 * qd;
+    float* orow = out + (row * heads + h) * kFlashDim;
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) {
+    for (int t = 0; t < 4; ++t) {
       float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < kFlashWaves; ++w)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = o[e] + wts[w] * part_acc[w][r][16 * qd + i + e];
-      *reinterpret_cast<float4*>(orow + i) = make_float4(o[0] / total, o[1] / total, o[2] / total, o[3] / total);
+      for (int w = 0; w < kFlashWaves; ++w) {
+        const float4 x = *reinterpret_cast<const float4*>(&ks[w][0][0] + j * kMfmaPad + 16 * t + 4 * g);
+        o[0] = o[0] + wts[w] * x.x;
+        o[1] = o[1] + wts[w] * x.y;
+        o[2] = o[2] + wts[w] * x.z;
+        o[3] = o[3] + wts[w] * x.w;
+      }
+      *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) =
+          make_float4(o[0] / total, o[1] / total, o[2] / total, o[3] / total);
     }
   }
 }
@@ -716,9 +727,9 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
       (reinterpret_cast<uintptr_t>(out) % 16 == 0)) {
     const int64_t qblocks = (seq + kFlashRows - 1) / kFlashRows;
     if (qblocks > 0x7fffffff || heads > 65535) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
-    hipLaunchKernelGGL(AttentionFlashKernel, dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(heads)),
+    hipLaunchKernelGGL(AttentionFlashMfmaKernel, dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(heads)),
                        dim3(kFlashWaves * 64), 0, stream, q, k, v, out, seq, position, heads, kv_heads, position_dev);
-    Check(hipGetLastError(), "AttentionFlashKernel launch");
+    Check(hipGetLastError(), "AttentionFlashMfmaKernel launch");
     return;
   }
   float* spill = rows > kLdsScores ? scratch : nullptr;
