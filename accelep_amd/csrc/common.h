@@ -115,11 +115,16 @@ struct Epilogue {
 // A transform the m = 1 GEMV applies to its input row before the product, inside each
 // workgroup (the row is at most kGemvPrologueMaxK long):
 //  * rms_weight: a = fl(float(double(x) * inv) * w), inv = 1/sqrt(sum(double(x)^2)/k + eps),
-//    the sum taken exactly as RmsNormKernel takes it (same bits as the separate pass);
+//    the sum taken exactly as RmsNormKernel takes it (same bits as the separate pass); or,
+//    with rms_after, a = fl(x * w) and the sums times float(inv) at the store;
 //  * silu_up: a = fl(fl(x / fl(1 + expf(-x))) * up), SiluMulKernel's formula.
 struct GemvPrologue {
   const float* rms_weight = nullptr;
   float rms_eps = 0.f;
+  // With rms_weight: multiply the sums by 1/rms at the store instead of normalizing the row
+  // first (a = fl(x * w) enters the product at once; rounding differs, so fast mode only).
+  // Used where the m = 1 entry kernel runs (even k <= 4096, x and w 8-byte aligned).
+  bool rms_after = false;
   const float* silu_up = nullptr;
 };
 constexpr int64_t kGemvPrologueMaxK = 4096;

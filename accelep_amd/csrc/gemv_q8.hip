@@ -287,6 +287,10 @@ constexpr int NarrowMinWaves() {
 constexpr int kAOpNone = 0;
 constexpr int kAOpRms = 1;
 constexpr int kAOpSiluUp = 2;
+// RMSNorm applied after the product (GemvPrologue::rms_after): A = fl(x * w) feeds the FMAs
+// at once and the row's sum of squares is reduced beside them; each output is scaled by
+// 1/rms at the store. Rounding differs from the normalize-first order (fast mode only).
+constexpr int kAOpRmsAfter = 3;
 
 // Writes the transformed input row (kAOp) into a_stage; every thread of the workgroup takes
 // part and the row is complete when this returns.
@@ -471,9 +475,31 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   const float col_scale = scale[scale_index_mul * colc + const_index];
   const GemvArgs unused{};
   NarrowBatch<1, kSteps> b;
+  double ss = 0.0;  // kAOpRmsAfter: this lane's share of sum(double(x)^2)
   if (kAOp == kAOpNone) {
     const float* const arow[1] = {a};
     LoadNarrowBatch<1, kSteps, false, false, true, kClamp>(unused, arow, 2 * tid, k, k, tbase, b);
+  } else if (kAOp == kAOpRmsAfter) {
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    float2 xv[kSteps], wv[kSteps];
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+      const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole
+      xv[u] = *reinterpret_cast<const float2*>(a + rp);
+      wv[u] = *reinterpret_cast<const float2*>(pro.rms_weight + rp);
+    }
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+      b.a[u][0][0] = __fmul_rn(xv[u].x, wv[u].x);
+      b.a[u][0][1] = __fmul_rn(xv[u].y, wv[u].y);
+      if (!kClamp || r < k) {
+        ss += static_cast<double>(xv[u].x) * static_cast<double>(xv[u].x);
+        ss += static_cast<double>(xv[u].y) * static_cast<double>(xv[u].y);
+      }
+    }
   } else {
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
@@ -506,11 +532,23 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   ComputeNarrowBatch<1, kSteps, false, false, kClamp>(b, 2 * tid, k, zc, acc);
   const float v = WaveColumnSum8(acc[0], lane);
   if ((lane & 7) == 0) red[wave][lane >> 3] = v;
+  __shared__ double ss_part[S::kWaves];
+  if (kAOp == kAOpRmsAfter) {
+    const double w_ss = WaveButterfly(ss, [](double x, double y) { return x + y; });
+    if (lane == 0) ss_part[wave] = w_ss;
+  }
   __syncthreads();
   if (tile_live && tid < kNarrowTile && col < n) {
     float sum = red[0][tid];
 #pragma unroll
     for (int wv = 1; wv < S::kWaves; ++wv) sum = sum + red[wv][tid];
+    if (kAOp == kAOpRmsAfter) {
+      double total = ss_part[0];
+#pragma unroll
+      for (int wv = 1; wv < S::kWaves; ++wv) total += ss_part[wv];
+      const double inv = 1.0 / sqrt(total / static_cast<double>(k) + static_cast<double>(pro.rms_eps));
+      sum = __fmul_rn(sum, static_cast<float>(inv));
+    }
     const float x = __fmul_rn(sum, col_scale);
     if (kPlain) {
       c[col] = x;
@@ -758,10 +796,11 @@ void LaunchNarrow(const GemvArgs& args, dim3 grid, bool zero, bool row_scale, bo
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
                   hipStream_t stream, const GemvPrologue* prologue) {
   if (m < 1 || m > 16 || k < 1 || n < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV shape out of range");
-  const int a_op = prologue == nullptr ? kAOpNone
-                   : prologue->rms_weight != nullptr ? kAOpRms
-                   : prologue->silu_up != nullptr    ? kAOpSiluUp
-                                                     : kAOpNone;
+  int a_op = prologue == nullptr                                        ? kAOpNone
+                   : prologue->rms_weight != nullptr && prologue->rms_after ? kAOpRmsAfter
+                   : prologue->rms_weight != nullptr                       ? kAOpRms
+                   : prologue->silu_up != nullptr                          ? kAOpSiluUp
+                                                                           : kAOpNone;
   static_assert(kGemvPrologueMaxK <= NarrowShape<1>::kBatchRows, "prologue rows fit one batch");
   if (a_op != kAOpNone && (m != 1 || b.tiled == nullptr || b.zero != nullptr || b.mode == kScalePerRow ||
                            k > kGemvPrologueMaxK))
@@ -826,10 +865,17 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   const dim3 grid(static_cast<uint32_t>(tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
   if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
-    // The prologue row lives in LDS (16-byte aligned), so only an even k is needed there.
-    const bool m1_pairs = a_op == kAOpNone ? pair_a : k % 2 == 0;
-    if (m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
-        n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) && epi.rms_weight == nullptr) {
+    // The staged prologue row lives in LDS (16-byte aligned), so only an even k is needed
+    // there; the norm-after form reads x and the norm weight in pairs from memory.
+    const bool m1_pairs = a_op == kAOpNone ? pair_a
+                          : a_op == kAOpRmsAfter
+                              ? pair_a && reinterpret_cast<uintptr_t>(prologue->rms_weight) % 8 == 0
+                              : k % 2 == 0;
+    const bool m1 = m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
+                    n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
+                    epi.rms_weight == nullptr;
+    if (!m1 && a_op == kAOpRmsAfter) a_op = kAOpRms;  // the general kernel normalizes first
+    if (m1) {
       const int steps = static_cast<int>((k + NarrowShape<1>::kStepRows - 1) / NarrowShape<1>::kStepRows);
       const bool clamp = k != steps * NarrowShape<1>::kStepRows;
       const bool plain = epi.Identity() && epi.split[0] == 0 && a_op == kAOpNone;
@@ -844,6 +890,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
 #define ACCEL_GEMV_M1(ST, CL)                                                               \
   do {                                                                                      \
     if (a_op == kAOpRms) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRms);                           \
+    else if (a_op == kAOpRmsAfter) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRmsAfter);            \
     else if (a_op == kAOpSiluUp) ACCEL_GEMV_M1_K(ST, CL, false, kAOpSiluUp);                \
     else if (plain) ACCEL_GEMV_M1_K(ST, CL, true, kAOpNone);                                \
     else ACCEL_GEMV_M1_K(ST, CL, false, kAOpNone);                                          \

@@ -125,7 +125,9 @@ struct Model {
   bool decode_graph_exact = false;
   uint64_t decode_graph_epoch = 0;
   bool decode_warm = false;
-  bool fuse_inputs = true;  // decode rows: RMSNorm and SiLU*up inside the next GEMV, one attention kernel
+  // Decode-row fusions (accel_llama_set_fused_inputs): bit 0, RMSNorm and SiLU*up inside the
+  // next GEMV; bit 1, RoPE + KV append + attention + combine as one kernel.
+  int32_t fuse = 3;
   // Attention partials of a decode step ([heads][context / 64 chunks][2 + head_dim]): owned
   // here so a captured step never points into a workspace that later grows.
   DevBuf attn_work;
@@ -177,7 +179,7 @@ struct Model {
   // One row through an int8 weight on the GEMV, with the input transform done inside it.
   static constexpr int64_t kFusedNormMaxOut = 8192;
   bool Fusable(const Linear& w, int64_t m) const {
-    return fuse_inputs && m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
+    return (fuse & 1) != 0 && m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
   }
   void ApplyPrologue(const Linear& w, const float* x, float* c, const Epilogue& e, const GemvPrologue& pro) {
     Context& ctx = Ctx();
@@ -196,6 +198,7 @@ struct Model {
       GemvPrologue pro;
       pro.rms_weight = norm.as<float>();
       pro.rms_eps = cfg.eps;
+      pro.rms_after = true;
       ApplyPrologue(w, x, c, e, pro);
       return;
     }
@@ -252,7 +255,7 @@ struct Model {
       float* kc = k_cache[static_cast<size_t>(li)].as<float>();
       float* vc = v_cache[static_cast<size_t>(li)].as<float>();
       ApplyNormed(l.qkv, hidden.as<float>(), l.attn_norm, query.as<float>(), seq, qkv);
-      if (seq != 1 || !fuse_inputs || !LaunchDecodeAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
+      if (seq != 1 || (fuse & 2) == 0 || !LaunchDecodeAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
                                              rope_cos.as<float>(), rope_sin.as<float>(), mixed.as<float>(), pos,
                                              cfg.heads, cfg.kv_heads, hd, s, state, cfg.context - 1,
                                              attn_work.as<float>(), attn_work.buffer().bytes,
@@ -704,9 +707,10 @@ ACCEL_LLAMA_API int accel_llama_set_fused_inputs(AccelLlama* handle, int32_t ena
     return 1;
   }
   return Run([&] {
+    if (enable < 0 || enable > 3) Fail(ACCEL_HIP_INVALID_ARGUMENT, "fused inputs: enable must be 0 .. 3");
     std::lock_guard<std::mutex> lock(m->mu);
-    if (m->fuse_inputs != (enable != 0)) m->DropDecodeGraph();  // the graph holds the other kernels
-    m->fuse_inputs = enable != 0;
+    if (m->fuse != enable) m->DropDecodeGraph();  // the graph holds the other kernels
+    m->fuse = enable;
   });
 }
 

@@ -118,29 +118,37 @@ def test_llama_full_size_matches_reference():
         eng.close()
 
 
+def _decode_row_logits(eng, cfg, prompt, fuse):
+    """Last-row logits after a prompt forward of prompt[:-1] and a one-row forward of the last id."""
+    assert eng.L.accel_llama_set_fused_inputs(eng.h, fuse) == 0
+    head, last = np.ascontiguousarray(prompt[:-1]), np.ascontiguousarray(prompt[-1:])
+    assert eng.L.accel_llama_forward_ids(eng.h, head.ctypes.data_as(I32P), head.size, 1) == 0
+    assert eng.L.accel_llama_forward_ids(eng.h, last.ctypes.data_as(I32P), 1, 0) == 0
+    row = np.zeros(cfg["vocab"], np.float32)
+    assert eng.L.accel_llama_logits(eng.h, row.ctypes.data_as(F32P), row.size) == 0
+    return row
+
+
 @pytest.mark.parametrize("count", [9, 64, 65, 150, 8250])
-def test_decode_row_fused_inputs_match_separate_passes(count):
-    """A one-row forward folds the RMSNorms and SiLU*up into the next int8 GEMV and runs RoPE,
-    the KV append, the chunked attention and its combine as one kernel; the logits must
-    carry exactly the bits of the separate-kernel forward. The prompt lengths put the new
-    position inside the first 64-position chunk, at its last slot, at the first slot of the
-    second, in a third chunk, and in the 129th."""
+def test_decode_row_fused_kernels_match_separate_passes(count):
+    """A one-row forward runs RoPE, the KV append, the chunked attention and its combine as one
+    kernel: the logits must carry exactly the bits of the three-kernel forward. With the
+    RMSNorms and SiLU*up inside the GEMVs as well (the norm applied to the sums) they agree to
+    rounding and pick the same id. The prompt lengths put the new position inside the first
+    64-position chunk, at its last slot, at the first slot of the second, in a third chunk,
+    and in the 129th."""
     cfg = dict(llama_config("smol3"), layers=2, context=max(160, count + 16))
     w, q = llama_weights(cfg, 103)
     prompt = np.random.default_rng(5).integers(0, cfg["vocab"], size=count).astype(np.int32)
     eng = Engine(cfg, w, q)
     try:
-        rows = {}
-        for fused in (1, 0):
-            assert eng.L.accel_llama_set_fused_inputs(eng.h, fused) == 0
-            head, last = np.ascontiguousarray(prompt[:-1]), np.ascontiguousarray(prompt[-1:])
-            assert eng.L.accel_llama_forward_ids(eng.h, head.ctypes.data_as(I32P), head.size, 1) == 0
-            assert eng.L.accel_llama_forward_ids(eng.h, last.ctypes.data_as(I32P), 1, 0) == 0
-            row = np.zeros(cfg["vocab"], np.float32)
-            assert eng.L.accel_llama_logits(eng.h, row.ctypes.data_as(F32P), row.size) == 0
-            rows[fused] = row
-        assert np.isfinite(rows[1]).all()
-        np.testing.assert_array_equal(rows[1].view(np.uint32), rows[0].view(np.uint32))
+        rows = {fuse: _decode_row_logits(eng, cfg, prompt, fuse) for fuse in (0, 2, 3)}
+        assert np.isfinite(rows[3]).all()
+        np.testing.assert_array_equal(rows[2].view(np.uint32), rows[0].view(np.uint32))
+        np.testing.assert_allclose(rows[3], rows[0], rtol=1e-4, atol=1e-4)
+        assert int(np.argmax(rows[3])) == int(np.argmax(rows[0]))
+        assert eng.L.accel_llama_set_fused_inputs(eng.h, 4) == 1
+        assert b"enable must be 0 .. 3" in eng.L.accel_llama_last_error()
     finally:
         eng.close()
 
