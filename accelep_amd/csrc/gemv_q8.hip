@@ -461,7 +461,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   using S = NarrowShape<1>;
   static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
   __shared__ float red[S::kWaves][kNarrowTile];
-  __shared__ __align__(16) float a_stage[kAOp != kAOpNone ? kGemvPrologueMaxK : 1];
+  __shared__ __align__(16) float a_stage[kAOp == kAOpRms ? kGemvPrologueMaxK : 1];  // the staged row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -479,25 +479,33 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   if (kAOp == kAOpNone) {
     const float* const arow[1] = {a};
     LoadNarrowBatch<1, kSteps, false, false, true, kClamp>(unused, arow, 2 * tid, k, k, tbase, b);
-  } else if (kAOp == kAOpRmsAfter) {
+  } else if (kAOp == kAOpRmsAfter || kAOp == kAOpSiluUp) {
+    // Elementwise inputs: each lane forms its own A pairs from x and the second operand (the
+    // norm weight, or up for SiLU*up), with no LDS stage and no barrier.
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    const float* second = kAOp == kAOpRmsAfter ? pro.rms_weight : pro.silu_up;
     float2 xv[kSteps], wv[kSteps];
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) {
       const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
       const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole
       xv[u] = *reinterpret_cast<const float2*>(a + rp);
-      wv[u] = *reinterpret_cast<const float2*>(pro.rms_weight + rp);
+      wv[u] = *reinterpret_cast<const float2*>(second + rp);
     }
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) {
       const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
-      b.a[u][0][0] = __fmul_rn(xv[u].x, wv[u].x);
-      b.a[u][0][1] = __fmul_rn(xv[u].y, wv[u].y);
-      if (!kClamp || r < k) {
-        ss += static_cast<double>(xv[u].x) * static_cast<double>(xv[u].x);
-        ss += static_cast<double>(xv[u].y) * static_cast<double>(xv[u].y);
+      if (kAOp == kAOpRmsAfter) {
+        b.a[u][0][0] = __fmul_rn(xv[u].x, wv[u].x);
+        b.a[u][0][1] = __fmul_rn(xv[u].y, wv[u].y);
+        if (!kClamp || r < k) {
+          ss += static_cast<double>(xv[u].x) * static_cast<double>(xv[u].x);
+          ss += static_cast<double>(xv[u].y) * static_cast<double>(xv[u].y);
+        }
+      } else {  // SiluMulKernel's formula
+        b.a[u][0][0] = __fmul_rn(__fdiv_rn(xv[u].x, __fadd_rn(1.f, expf(-xv[u].x))), wv[u].x);
+        b.a[u][0][1] = __fmul_rn(__fdiv_rn(xv[u].y, __fadd_rn(1.f, expf(-xv[u].y))), wv[u].y);
       }
     }
   } else {
@@ -870,7 +878,8 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     const bool m1_pairs = a_op == kAOpNone ? pair_a
                           : a_op == kAOpRmsAfter
                               ? pair_a && reinterpret_cast<uintptr_t>(prologue->rms_weight) % 8 == 0
-                              : k % 2 == 0;
+                          : a_op == kAOpSiluUp ? pair_a && reinterpret_cast<uintptr_t>(prologue->silu_up) % 8 == 0
+                                               : k % 2 == 0;
     const bool m1 = m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
                     n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
                     epi.rms_weight == nullptr;
