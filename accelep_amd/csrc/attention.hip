@@ -490,6 +490,7 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashMfmaKernel(
 // exit at once. The scores, the chunk sums and the combine are those of the three-kernel
 // path, bit for bit.
 constexpr int kStepDim = 64;
+constexpr int kStepFastChunks = 16;
 
 __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
     const float* q_raw, const float* k_raw, const float* v_raw, float* k_cache, float* v_cache, const float* cos_t,
@@ -523,8 +524,21 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   const int tid = threadIdx.x;
   const int kv_row = kv_heads * kStepDim;
 
-  // Loads that do not depend on the rotation are issued first: the key row of this lane
-  // (wave 0) and the value rows of this thread's (position group, column quad).
+  // The rotation's inputs are loaded first (every thread, from valid addresses), then the key
+  // row of this lane (wave 0) and the value rows of this thread's (position group, column
+  // quad). Loads complete in issue order; the rotation runs in waves 1 and 2, which load no
+  // key rows, so it waits only for its own values and the four value rows, not for the keys.
+  constexpr int kHalf = kStepDim / 2;
+  const int ri = tid % kHalf;
+  const bool rot_q = (tid >> 5) == 2;  // tid 64 .. 95: q; 96 .. 127: the new k
+  const float* rsrc = rot_q ? q_raw + h * kStepDim : k_raw + kv * kStepDim;
+  const float rx0 = rsrc[ri];
+  const float rx1 = rsrc[kHalf + ri];
+  const float rc0 = cos_t[position * kStepDim + ri];
+  const float rc1 = cos_t[position * kStepDim + kHalf + ri];
+  const float rs0 = sin_t[position * kStepDim + ri];
+  const float rs1 = sin_t[position * kStepDim + kHalf + ri];
+  const float rv = v_raw[kv * kStepDim + (tid & (kStepDim - 1))];
   constexpr int kCols = 4;
   constexpr int kGroups = kSplitThreads / (kStepDim / kCols);  // 16
   const int cc = tid % (kStepDim / kCols);
@@ -536,28 +550,22 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
 #pragma unroll
     for (int j = 0; j < kStepDim / 4; ++j) kx[j] = kr[j];
   }
+  // Value rows past the chunk's end read its last row and the new position reads the stale
+  // cache row: both are replaced at use, so the loads need no branches.
   float4 vx[kChunk / kGroups];
 #pragma unroll
   for (int i = 0; i < kChunk / kGroups; ++i) {
-    const int t = g + i * kGroups;
-    if (t < n && t0 + t != position)
-      vx[i] = *reinterpret_cast<const float4*>(v_cache + (t0 + t) * kv_row + kv * kStepDim + cc * kCols);
+    const int t = min(g + i * kGroups, n - 1);
+    vx[i] = *reinterpret_cast<const float4*>(v_cache + (t0 + t) * kv_row + kv * kStepDim + cc * kCols);
   }
 
   // RoPE (RopeAppendKernel's arithmetic) of q, and in the tail chunk of the new k; new v.
-  constexpr int kHalf = kStepDim / 2;
-  const float* cs = cos_t + position * kStepDim;
-  const float* sn = sin_t + position * kStepDim;
-  if (tid < kHalf || (tail && tid < 2 * kHalf)) {
-    const int i = tid % kHalf;
-    const float* src = tid < kHalf ? q_raw + h * kStepDim : k_raw + kv * kStepDim;
-    float* dst = tid < kHalf ? qs : knew;
-    const float x0 = src[i];
-    const float x1 = src[kHalf + i];
-    dst[i] = __fsub_rn(__fmul_rn(x0, cs[i]), __fmul_rn(x1, sn[i]));
-    dst[kHalf + i] = __fadd_rn(__fmul_rn(x1, cs[kHalf + i]), __fmul_rn(x0, sn[kHalf + i]));
-  } else if (tail && tid >= 64 && tid < 64 + kStepDim) {
-    vnew[tid - 64] = v_raw[kv * kStepDim + (tid - 64)];
+  if (rot_q || (tail && (tid >> 5) == 3)) {
+    float* dst = rot_q ? qs : knew;
+    dst[ri] = __fsub_rn(__fmul_rn(rx0, rc0), __fmul_rn(rx1, rs0));
+    dst[kHalf + ri] = __fadd_rn(__fmul_rn(rx1, rc1), __fmul_rn(rx0, rs1));
+  } else if (tail && (tid >> 6) == 2) {
+    vnew[tid - 128] = rv;
   }
   __syncthreads();
   if (tail && h == kv * group && tid < kStepDim) {
@@ -598,18 +606,27 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   }
   __syncthreads();
   // acc[d] over the chunk: thread (g, cc) adds positions g, g + 16, ... in order.
+  // Branch-free: a position past n adds e * x = 0 * 0, which leaves the sum's bits unchanged
+  // (the sum starts at +0 and never becomes -0).
   float acc[kCols] = {0.f, 0.f, 0.f, 0.f};
+  const float4 vn4 = reinterpret_cast<const float4*>(vnew)[cc];
+  float ev[kChunk / kGroups];
+#pragma unroll
+  for (int i = 0; i < kChunk / kGroups; ++i) ev[i] = es[min(g + i * kGroups, kChunk - 1)];
 #pragma unroll
   for (int i = 0; i < kChunk / kGroups; ++i) {
     const int t = g + i * kGroups;
-    if (t < n) {
-      const float e = es[t];
-      const float4 x4 = t0 + t == position ? reinterpret_cast<const float4*>(vnew)[cc] : vx[i];
-      acc[0] = __fadd_rn(acc[0], __fmul_rn(e, x4.x));
-      acc[1] = __fadd_rn(acc[1], __fmul_rn(e, x4.y));
-      acc[2] = __fadd_rn(acc[2], __fmul_rn(e, x4.z));
-      acc[3] = __fadd_rn(acc[3], __fmul_rn(e, x4.w));
-    }
+    const bool in = t < n;
+    const bool fresh = t0 + t == position;
+    const float e = in ? ev[i] : 0.f;
+    const float x0 = in ? (fresh ? vn4.x : vx[i].x) : 0.f;
+    const float x1 = in ? (fresh ? vn4.y : vx[i].y) : 0.f;
+    const float x2 = in ? (fresh ? vn4.z : vx[i].z) : 0.f;
+    const float x3 = in ? (fresh ? vn4.w : vx[i].w) : 0.f;
+    acc[0] = __fadd_rn(acc[0], __fmul_rn(e, x0));
+    acc[1] = __fadd_rn(acc[1], __fmul_rn(e, x1));
+    acc[2] = __fadd_rn(acc[2], __fmul_rn(e, x2));
+    acc[3] = __fadd_rn(acc[3], __fmul_rn(e, x3));
   }
 #pragma unroll
   for (int j = 0; j < kCols; ++j) acc_part[g * kStepDim + cc * kCols + j] = acc[j];
@@ -636,6 +653,38 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   if (!is_last) return;
   const float* p = partial + h * chunks_max * (2 + kStepDim);
   const auto load = [](const float* x) { return __hip_atomic_load(x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  if (live <= kStepFastChunks) {
+    // Up to 16 chunks (1024 positions): wave 0 issues every load of the combine at once (lane
+    // c: chunk c's m and l; lane d: column d of each chunk), then combines: one memory round
+    // trip instead of one for (m, l) and more for the columns. Same arithmetic and order.
+    if (tid < 64) {
+      const int chl = min(tid, live - 1);
+      float mc = load(&p[chl * (2 + kStepDim)]);
+      const float lc = load(&p[chl * (2 + kStepDim) + 1]);
+      float xs[kStepFastChunks];
+#pragma unroll
+      for (int ch = 0; ch < kStepFastChunks; ++ch) xs[ch] = load(&p[min(ch, live - 1) * (2 + kStepDim) + 2 + tid]);
+      if (tid >= live) mc = -INFINITY;
+      const float big = WaveButterfly(mc, [](float a, float b) { return fmaxf(a, b); });
+      wts[tid] = mc == -INFINITY ? 0.f : expf(__fsub_rn(mc, big));
+      lsum[tid] = lc;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float l = 0.f;
+      float o = 0.f;
+#pragma unroll
+      for (int ch = 0; ch < kStepFastChunks; ++ch) {
+        if (ch < live) {
+          l = __fadd_rn(l, __fmul_rn(wts[ch], lsum[ch]));
+          o = __fadd_rn(o, __fmul_rn(wts[ch], xs[ch]));
+        }
+      }
+      out[h * kStepDim + tid] = __fdiv_rn(o, l);
+      if (tid == 0) atomicExch(&arrivals[h], 0u);
+    }
+    return;
+  }
   if (tid < 64) {
     float big = -INFINITY;
     for (int ch = tid; ch < live; ch += 64) {
