@@ -38,8 +38,9 @@ Context& Ctx();
 // Ensures workspace >= bytes; returns the context.
 Context& Scratch(size_t bytes);
 // Library-owned device temporaries, one per purpose, grown on demand (the stream is
-// drained before a buffer is replaced). Distinct from the split-K workspace.
-enum TempSlot { kTempDequantA = 0, kTempDequantB = 1, kTempFlags = 2, kTempCount = 3 };
+// drained before a buffer is replaced; a new buffer starts zeroed). Distinct from the
+// split-K workspace. kTempArrivals holds counters that every kernel using them leaves zero.
+enum TempSlot { kTempDequantA = 0, kTempDequantB = 1, kTempFlags = 2, kTempArrivals = 3, kTempCount = 4 };
 void* Temp(TempSlot slot, size_t bytes);
 
 // Stats of include/accel/runtime.h (AcceleratorStats) and the packed-GEMM probes.
@@ -60,6 +61,7 @@ struct Q8View {
   int32_t mode = kScaleConst;
   int64_t const_index = 0;        // scale/zero index in kScaleConst mode
   const int8_t* tiled = nullptr;  // staged column-tiled copy of q (kGemvTileCols wide), or nullptr
+  const int8_t* grouped = nullptr;  // staged group-interleaved copy of q, or nullptr
 };
 
 // ---- weight staging (staging.cc) --------------------------------------------------------
@@ -84,6 +86,27 @@ void NoteDeviceWrite(const void* ptr, size_t bytes);
 bool FindAllocation(const void* ptr, uint64_t* id, const char** base, size_t* bytes);
 void DropStagedForAllocation(uint64_t id);
 void LaunchTileColumns(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
+// Group-interleaved copy for the m > 1 GEMV (k a multiple of kGemvGroupRows): the 8-column
+// tiles in groups of kGemvGroupTiles; for group G, row octet o (rows 8o .. 8o + 7) and tile
+// slot j, the 64 bytes of those rows of tile 16G + j (row-major, 8 bytes a row) sit at
+// ((G * k/8 + o) * 16 + j) * 64, so the 16 tiles' rows of one octet are 1 KB contiguous.
+// Tiles past the last column are zero.
+constexpr int64_t kGemvGroupTiles = 16;
+constexpr int64_t kGemvGroupRows = 32;
+inline size_t StagedGroupBytes(int64_t k, int64_t n) {
+  const int64_t groups = (n + kGemvTileCols * kGemvGroupTiles - 1) / (kGemvTileCols * kGemvGroupTiles);
+  return static_cast<size_t>(groups) * static_cast<size_t>(k) * static_cast<size_t>(kGemvTileCols * kGemvGroupTiles);
+}
+// The staged group-interleaved copy of the [k, n] int8 matrix at q (k % kGemvGroupRows == 0),
+// built on first use; nullptr when q is not inside a live allocation of this library.
+const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);
+void LaunchTileGroups(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
+// Whether LaunchGemvQ8 takes an m-row product with this k from the group-interleaved copy
+// (the caller stages that copy instead of the 8-column tiles).
+constexpr int64_t kGemvGroupMinM = 3;
+inline bool GemvWantsGroups(int64_t m, int64_t k) {
+  return m >= kGemvGroupMinM && m <= 16 && k % kGemvGroupRows == 0;
+}
 
 struct Epilogue {
   float alpha = 1.f;
@@ -129,7 +152,9 @@ struct GemvPrologue {
 };
 constexpr int64_t kGemvPrologueMaxK = 4096;
 
-// C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV). A prologue needs m == 1,
+// C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV). With b.grouped (and no zero
+// points or per-row scale, k % 32 == 0, A 8-byte aligned) the split-bf16 MFMA kernel runs;
+// with b.tiled the 8-column tile kernels; otherwise W is read in place. A prologue needs m == 1,
 // staged tiles, a per-column or whole-tensor scale without zero points and k <=
 // kGemvPrologueMaxK.
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,

@@ -136,6 +136,7 @@ void* Temp(TempSlot slot, size_t bytes) {
     buffers[slot] = nullptr;
     const size_t grown = std::max<size_t>(bytes, std::max<size_t>(sizes[slot] * 2, 256));
     Check(hipMalloc(&buffers[slot], grown), "hipMalloc(temp)");
+    Check(hipMemset(buffers[slot], 0, grown), "hipMemset(temp)");
     sizes[slot] = grown;
   }
   return buffers[slot];

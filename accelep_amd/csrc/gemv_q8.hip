@@ -3,7 +3,7 @@
 //
 // Bound: HBM. Algorithmic bytes per call = k*n (int8 W) + 4*n (scale) + 4*m*k (A) + 4*m*n (C).
 //
-// Both kernels stream W with 16-byte loads and convert the bytes to fp32 exactly. Per-column
+// Every kernel streams W with 16-byte loads and converts the bytes exactly. Per-column
 // (or whole-tensor) scale multiplies each finished sum once; a per-row scale is folded into
 // A; zero points are subtracted from the exact integer before the product. Every sum runs
 // in a fixed order, so results are deterministic.
@@ -18,11 +18,16 @@
 //  * the 8 column sums of the 64 lanes are reduce-scattered with lane shuffles, the waves'
 //    sums added through LDS;
 //  * tiles go to XCDs in contiguous runs (workgroup i runs on XCD i % 8).
-// Wide kernel (4 < m <= 16): W in place, 256-column tiles, 16 lanes per 256-byte row segment,
-// 4 rows per wave load feed v_mfma_f32_16x16x4_f32 as its K = 4; A staged in LDS.
-// Split-K (only where the tile count cannot fill the GPU): each split writes its partial
-// sums to the workspace and a second kernel adds them in split order (no inter-workgroup
-// synchronization inside a kernel).
+// Split-bf16 kernel (2 < m <= 16, k a multiple of 32, no zero points or per-row scale): a
+// group-interleaved staged copy of the tiles, exact products on v_mfma_f32_16x16x32_bf16
+// with each activation split into three bf16 parts, split-K summed in split order by the
+// last workgroup of each column group to arrive (no second kernel).
+// Wide kernel (the other 4 < m <= 16 cases): W in place, 256-column tiles, 16 lanes per
+// 256-byte row segment, 4 rows per wave load feed v_mfma_f32_16x16x4_f32 as its K = 4; A
+// staged in LDS.
+// Split-K of the narrow and wide kernels (only where the tile count cannot fill the GPU):
+// each split writes its partial sums to the workspace and a second kernel adds them in
+// split order.
 #include "device_common.h"
 
 namespace accel_hip {
@@ -51,6 +56,10 @@ struct GemvArgs {
   // (kp = k rounded up to even), columns past n and the pad row zero. nullptr: read W in
   // its [k, n] layout.
   const int8_t* tiled;
+  // Group-interleaved copy of W (split-bf16 kernel; StagedGroupBytes' layout), and its
+  // per-group arrival counters (zero between launches).
+  const int8_t* grouped;
+  uint32_t* arrivals;
   Epilogue epi;
   GemvPrologue pro;  // narrow m = 1 kernel with kAOp != 0
 };
@@ -712,6 +721,215 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
     if (mm < p.m) Emit(p, split, mm, out_col, sums[mm]);
 }
 
+// ---- split-bf16 MFMA kernel: 1 < m <= 16, group-interleaved tiles, k a multiple of 32 ---------
+// The products run on v_mfma_f32_16x16x32_bf16 (A: 16 rows x 32 k, B: 32 k x 16 columns)
+// without rounding either operand:
+//  * every weight byte is an integer in [-128, 127], which bf16 holds exactly;
+//  * every activation x is split as x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi),
+//    lo = bf16(x - hi - mid); both differences are exact in fp32 and the three parts carry all
+//    24 significand bits of x (for |x| >= 2^-110; below that the last part may lose bits), so
+//    three MFMAs multiply by x exactly and only the fp32 accumulation rounds.
+// A workgroup (4 waves) owns one group of 16 staged tiles (128 columns) over one split of K.
+// Lane l takes tile slot l % 16 as the B column of its MFMAs and, for the 8 columns c of that
+// tile, the operand of the c-th MFMA. A 32-row block is read as 4 loads of 16 bytes per lane:
+// load h of lane group g = l / 16 holds rows 8h + 2g and 8h + 2g + 1 of the tile, so one load
+// of the wave is the 1 KB octet of all 16 tiles; A lane (row l % 16, group g) loads the same
+// rows of A, so the k slots agree. The waves take interleaved blocks, and their sums are added
+// through LDS in wave order. With splits, each workgroup stores its partial sums and the last
+// one of a group to arrive adds them in split order and applies the scale and the epilogue.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kSplitWaves = 4;
+constexpr int kSplitThreads = kSplitWaves * 64;
+constexpr int kSplitTiles = static_cast<int>(kGemvGroupTiles);      // tiles of a group (128 columns)
+constexpr int kSplitBlockRows = static_cast<int>(kGemvGroupRows);  // K of one MFMA
+constexpr int kSplitBatch = 2;  // blocks a wave loads before using any
+constexpr int kSplitGroupBytes = kSplitTiles * kNarrowTile;  // bytes of one row of a group
+
+// Two floats to one word of two bf16 (round to nearest even; exact for the values used here).
+__device__ __forceinline__ uint32_t PackBf16(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
+}
+__device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+__global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p) {
+  __shared__ float red[kSplitWaves][32][65];  // [wave][4 * column + row of the MFMA tile][lane]
+  __shared__ bool is_last;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int slot = lane & 15;  // B column slot (tile) and A row
+  const int g = lane >> 4;     // k group
+  const int group = blockIdx.x;
+  const int split = blockIdx.y;
+  const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
+  const int64_t ke = min(p.k, kb + p.rows_per_split);
+  const int blocks = static_cast<int>((ke - kb) / kSplitBlockRows);
+  const int8_t* tb = p.grouped + (static_cast<int64_t>(group) * p.k + kb) * kSplitGroupBytes + 64 * slot + 16 * g;
+  const bool row_live = slot < p.m;
+  const float* ab = p.a + static_cast<int64_t>(row_live ? slot : p.m - 1) * p.k + kb + 2 * g;
+
+  v4f acc[kNarrowTile];
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int b0 = wave; b0 < blocks; b0 += kSplitWaves * kSplitBatch) {
+    u32x4 w[kSplitBatch][4];
+    f32x2 x[kSplitBatch][4];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const int blk = b0 + u * kSplitWaves;
+      const int bc = blk < blocks ? blk : blocks - 1;  // a valid block; its A is zeroed below
+      const u32x4* wb = reinterpret_cast<const u32x4*>(tb + static_cast<int64_t>(bc) * (kSplitBlockRows * kSplitGroupBytes));
+      const f32x2* xb = reinterpret_cast<const f32x2*>(ab + static_cast<int64_t>(bc) * kSplitBlockRows);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        w[u][h] = __builtin_nontemporal_load(wb + 64 * h);  // octet h: rows 8h + 2g, 8h + 2g + 1
+        x[u][h] = xb[4 * h];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any is used
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const bool live = row_live && b0 + u * kSplitWaves < blocks;
+      u32x4 ah, am, al;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float x0 = live ? x[u][h][0] : 0.f;
+        const float x1 = live ? x[u][h][1] : 0.f;
+        ah[h] = PackBf16(x0, x1);
+        const float r0 = x0 - Bf16Low(ah[h]);
+        const float r1 = x1 - Bf16High(ah[h]);
+        am[h] = PackBf16(r0, r1);
+        al[h] = PackBf16(r0 - Bf16Low(am[h]), r1 - Bf16High(am[h]));
+      }
+      // Column c of the tile: row 8h + 2g in byte c of words 0..1 of load h, row 8h + 2g + 1
+      // in words 2..3.
+      u32x4 bw[kNarrowTile];
+#pragma unroll
+      for (int c = 0; c < kNarrowTile; ++c)
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          bw[c][h] = PackBf16(ByteToFloat(w[u][h][c >> 2], c & 3), ByteToFloat(w[u][h][2 + (c >> 2)], c & 3));
+#pragma unroll
+      for (int c = 0; c < kNarrowTile; ++c)
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), __builtin_bit_cast(bf16x8, bw[c]),
+                                                         acc[c], 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < kNarrowTile; ++c)
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), __builtin_bit_cast(bf16x8, bw[c]),
+                                                         acc[c], 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < kNarrowTile; ++c)
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), __builtin_bit_cast(bf16x8, bw[c]),
+                                                         acc[c], 0, 0, 0);
+    }
+  }
+
+  // Element r of MFMA c in lane l: row 4 * (l / 16) + r, column 8 * (16 * group + l % 16) + c.
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * c + r][lane] = acc[c][r];
+  __syncthreads();
+  // Thread: one column of the group, rows 8 * (tid / 128) .. + 7.
+  const int cc = tid & (kSplitGroupBytes - 1);
+  const int jt = cc >> 3;
+  const int c = cc & 7;
+  const int64_t col = static_cast<int64_t>(group * kSplitTiles + jt) * kNarrowTile + c;
+  const int m0 = (tid >> 7) * 8;
+  const int mend = min(p.m, static_cast<int64_t>(m0 + 8));
+  float sum[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int mm = m0 + i;
+    const int ln = 16 * (mm >> 2) + jt;
+    const int ri = 4 * c + (mm & 3);
+    float s = red[0][ri][ln];
+#pragma unroll
+    for (int wv = 1; wv < kSplitWaves; ++wv) s = s + red[wv][ri][ln];
+    sum[i] = s;
+  }
+  const bool live_col = col < p.n;
+  if (p.splits > 1) {
+    // Partial sums out (agent scope: the last workgroup, on any XCD, reads them), then the
+    // arrival count of the group.
+    float* part = p.partials + col;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (live_col && m0 + i < mend)
+        __hip_atomic_store(&part[(static_cast<int64_t>(split) * p.m + m0 + i) * p.n], sum[i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) is_last = atomicAdd(&p.arrivals[group], 1u) == static_cast<uint32_t>(p.splits - 1);
+    __syncthreads();
+    if (!is_last) return;
+    if (tid == 0) atomicExch(&p.arrivals[group], 0u);  // ready for the next launch
+    if (!live_col || m0 >= mend) return;
+    // The splits' sums in split order; kChunk splits of all 8 rows are requested at once
+    // (clamped to valid rows and splits; the extra values are not used).
+    constexpr int kChunk = 4;
+    for (int sp0 = 0; sp0 < p.splits; sp0 += kChunk) {
+      float v[kChunk][8];
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int64_t sp = min(sp0 + t, p.splits - 1);
+          const int64_t mm = min(m0 + i, mend - 1);
+          v[t][i] = __hip_atomic_load(&part[(sp * p.m + mm) * p.n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (sp0 + t < p.splits) sum[i] = sp0 + t == 0 ? v[t][i] : sum[i] + v[t][i];
+    }
+  }
+  if (!live_col) return;
+  const float cs = ColScale(p, col);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int mm = m0 + i;
+    if (mm >= mend) break;
+    StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(sum[i], cs), mm, col, p.n, p.epi));
+  }
+}
+
+// dst (group-interleaved, see StagedGroupBytes) from q [k, n]: one thread writes the 16 bytes
+// of one row pair of one tile; consecutive threads write consecutive 16-byte pieces.
+__global__ void TileGroupsKernel(const int8_t* q, int64_t k, int64_t n, int8_t* dst, int64_t groups) {
+  const int64_t pieces = groups * k * kSplitTiles / 2;
+  const bool vec = (n % 8 == 0) && (reinterpret_cast<uintptr_t>(q) % 8 == 0);
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < pieces;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t pair = idx & 3;
+    const int64_t j = (idx >> 2) % kSplitTiles;
+    const int64_t go = (idx >> 2) / kSplitTiles;  // G * k/8 + o
+    const int64_t o = go % (k / 8);
+    const int64_t grp = go / (k / 8);
+    const int64_t col = (grp * kSplitTiles + j) * kNarrowTile;
+    uint32_t w[4] = {0, 0, 0, 0};
+    for (int h = 0; h < 2; ++h) {
+      const int64_t r = 8 * o + 2 * pair + h;
+      if (vec && col + 7 < n) {
+        const uint2 v = *reinterpret_cast<const uint2*>(q + r * n + col);
+        w[2 * h] = v.x;
+        w[2 * h + 1] = v.y;
+      } else {
+        for (int b = 0; b < 8; ++b)
+          if (col + b < n)
+            w[2 * h + (b >> 2)] |= static_cast<uint32_t>(static_cast<uint8_t>(q[r * n + col + b])) << (8 * (b & 3));
+      }
+    }
+    *reinterpret_cast<uint4*>(dst + idx * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // ---- split-K reduction ----------------------------------------------------------------------
 // One thread per output column of a row (blockIdx.y strides over rows): no index division.
 __global__ void SplitReduceKernel(const float* partials, int32_t splits, int64_t m, int64_t n, float* c,
@@ -772,6 +990,16 @@ void LaunchTileColumns(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipSt
   Check(hipGetLastError(), "TileColumnsKernel launch");
 }
 
+void LaunchTileGroups(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream) {
+  if (k % kGemvGroupRows != 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "group tiles need k % 32 == 0");
+  const int64_t groups = (n + kSplitGroupBytes - 1) / kSplitGroupBytes;
+  const int64_t pieces = groups * k * kSplitTiles / 2;
+  int64_t grid = (pieces + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(TileGroupsKernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, q, k, n, dst, groups);
+  Check(hipGetLastError(), "TileGroupsKernel launch");
+}
+
 void LaunchSplitReduce(const float* partials, int32_t splits, int64_t m, int64_t n, float* c, int32_t mode,
                        const float* scale, int64_t const_index, const Epilogue& epi, hipStream_t stream) {
   const int64_t gx = (n + 255) / 256;
@@ -817,12 +1045,26 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // The narrow kernel reads the staged column tiles (and indexes rows in 32 bits); without
   // them the wide kernel, which reads W in place, takes any m <= 16.
-  const bool narrow = m <= 4 && b.tiled != nullptr && k < (int64_t(1) << 28);
-  const int64_t tile_cols = narrow ? kNarrowTile : kWideTile;
+  const bool zero = b.zero != nullptr;
+  const bool row_scale = b.mode == kScalePerRow;
+  // The split-bf16 MFMA kernel: group-interleaved copy, whole 32-row blocks, A 8-byte aligned.
+  const bool split_bf16 = m > 1 && b.grouped != nullptr && !zero && !row_scale && a_op == kAOpNone &&
+                          k % kSplitBlockRows == 0 && k < (int64_t(1) << 28) &&
+                          reinterpret_cast<uintptr_t>(a) % 8 == 0 && (b.mode == kScalePerCol || b.mode == kScaleConst);
+  const bool narrow = !split_bf16 && m <= 4 && b.tiled != nullptr && k < (int64_t(1) << 28);
+  const int64_t tile_cols = narrow || split_bf16 ? kNarrowTile : kWideTile;
   const int64_t tiles = (n + tile_cols - 1) / tile_cols;
   int64_t splits = 1;
   int64_t rows = k;
-  if (narrow) {
+  if (split_bf16) {
+    // About 1.75 workgroups per CU: K split into 4 for 4096 x 14336 (measured best there;
+    // twice the splits costs more in partial sums and arrivals than it gains in parallelism).
+    const int64_t target = 7 * cus / 4;
+    const int64_t groups = (tiles + kSplitTiles - 1) / kSplitTiles;
+    const int64_t blocks = k / kSplitBlockRows;
+    splits = std::max<int64_t>(1, std::min<int64_t>((target + groups - 1) / groups, blocks / (kSplitWaves * kSplitBatch)));
+    rows = (blocks + splits - 1) / splits * kSplitBlockRows;
+  } else if (narrow) {
     // One workgroup per tile over all of K, unless the tiles leave the CUs short of work on a
     // K of several batches: then K is split so that about four workgroups run per CU.
     const int64_t step_rows = m == 1 ? NarrowShape<1>::kStepRows : NarrowShape<2>::kStepRows;
@@ -842,6 +1084,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   splits = (k + rows - 1) / rows;
   if (a_op != kAOpNone && splits != 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV input prologue needs one split");
   const int64_t tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
+  if (split_bf16 && (tiles + kSplitTiles - 1) / kSplitTiles > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV too large");
   if (tiles_per_xcd * kXcds > 0x7fffffff || splits > 65535) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV grid too large");
 
   GemvArgs args;
@@ -867,11 +1110,16 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   }
   static_assert(kNarrowTile == kGemvTileCols, "staged tiles must match the narrow kernel tile");
   args.tiled = narrow ? b.tiled : nullptr;
+  args.grouped = split_bf16 ? b.grouped : nullptr;
+  args.arrivals = nullptr;
   if (prologue != nullptr) args.pro = *prologue;
-  const bool zero = b.zero != nullptr;
-  const bool row_scale = b.mode == kScalePerRow;
   const dim3 grid(static_cast<uint32_t>(tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
-  if (narrow) {
+  if (split_bf16) {
+    const int64_t groups = (tiles + kSplitTiles - 1) / kSplitTiles;
+    if (splits > 1) args.arrivals = static_cast<uint32_t*>(Temp(kTempArrivals, static_cast<size_t>(groups) * 4));
+    const dim3 sgrid(static_cast<uint32_t>(groups), static_cast<uint32_t>(splits));
+    hipLaunchKernelGGL(GemvSplitBf16Kernel, sgrid, dim3(kSplitThreads), 0, stream, args);
+  } else if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
     // The staged prologue row lives in LDS (16-byte aligned), so only an even k is needed
     // there; the norm-after form reads x and the norm weight in pairs from memory.
@@ -957,7 +1205,8 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     }
   }
   Check(hipGetLastError(), "GEMV launch");
-  if (splits > 1) LaunchSplitReduce(args.partials, args.splits, m, n, c, b.mode, b.scale, b.const_index, epi, stream);
+  if (splits > 1 && !split_bf16)
+    LaunchSplitReduce(args.partials, args.splits, m, n, c, b.mode, b.scale, b.const_index, epi, stream);
 }
 
 }  // namespace accel_hip

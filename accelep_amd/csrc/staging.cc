@@ -4,7 +4,8 @@
 // (src/ep.cc:843-900, src/runtime.cc:326-327). Read in that layout, a workgroup that owns a
 // few columns walks k rows 14 KB apart, which HBM serves at well under half its streaming
 // rate. On its first use by the GEMV, the matrix is copied once into 8-column tiles, each
-// tile's k x 8 bytes contiguous; later calls read the copy. The original bytes stay as
+// tile's k x 8 bytes contiguous (the m > 1 MFMA GEMV takes a group-interleaved form of the
+// same tiles instead); later calls read the copy. The original bytes stay as
 // they are, so every counted copy and every other kernel still sees the EP's layout.
 //
 // A copy is keyed by (allocation id, byte offset, k, n) and dropped when its allocation is
@@ -23,11 +24,16 @@
 namespace accel_hip {
 namespace {
 
+enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1 };
+
 struct Key {
   uint64_t id;
   size_t offset;
   int64_t k, n;
-  bool operator<(const Key& o) const { return std::tie(id, offset, k, n) < std::tie(o.id, o.offset, o.k, o.n); }
+  int layout;
+  bool operator<(const Key& o) const {
+    return std::tie(id, offset, k, n, layout) < std::tie(o.id, o.offset, o.k, o.n, o.layout);
+  }
 };
 
 struct Entry {
@@ -62,9 +68,7 @@ void EvictFor(size_t bytes) {
   }
 }
 
-}  // namespace
-
-const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream) {
+const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStream_t stream) {
   if (k <= 0 || n <= 0) return nullptr;
   uint64_t id = 0;
   const char* base = nullptr;
@@ -74,21 +78,33 @@ const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream
   const size_t need = static_cast<size_t>(k) * static_cast<size_t>(n);
   if (offset + need > alloc_bytes) return nullptr;  // the matrix must lie inside one allocation
   std::lock_guard<std::mutex> lock(g_mu);
-  const Key key{id, offset, k, n};
+  const Key key{id, offset, k, n, layout};
   auto it = g_staged.find(key);
   if (it != g_staged.end()) {
     it->second.last_use = ++g_tick;
     return it->second.data;
   }
-  const size_t bytes = StagedTileBytes(k, n);
+  const size_t bytes = layout == kLayoutGroups ? StagedGroupBytes(k, n) : StagedTileBytes(k, n);
   EvictFor(bytes);
   int8_t* dst = nullptr;
   if (hipMalloc(reinterpret_cast<void**>(&dst), bytes) != hipSuccess) return nullptr;  // fall back to raw
-  LaunchTileColumns(q, k, n, dst, stream);
+  if (layout == kLayoutGroups) LaunchTileGroups(q, k, n, dst, stream);
+  else LaunchTileColumns(q, k, n, dst, stream);
   g_staged.emplace(key, Entry{dst, bytes, ++g_tick});
   g_staged_bytes += bytes;
   g_any.store(true);
   return dst;
+}
+
+}  // namespace
+
+const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream) {
+  return Staged(q, k, n, kLayoutTiles, stream);
+}
+
+const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream) {
+  if (k % kGemvGroupRows != 0) return nullptr;
+  return Staged(q, k, n, kLayoutGroups, stream);
 }
 
 uint64_t StagingEpoch() { return g_epoch.load(); }
@@ -106,7 +122,7 @@ void NoteDeviceWrite(const void* ptr, size_t bytes) {
 void DropStagedForAllocation(uint64_t id) {
   if (!g_any.load()) return;
   std::lock_guard<std::mutex> lock(g_mu);
-  for (auto it = g_staged.lower_bound(Key{id, 0, INT64_MIN, INT64_MIN}); it != g_staged.end() && it->first.id == id;) {
+  for (auto it = g_staged.lower_bound(Key{id, 0, INT64_MIN, INT64_MIN, 0}); it != g_staged.end() && it->first.id == id;) {
     FreeEntry(it->second);
     it = g_staged.erase(it);
   }

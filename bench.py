@@ -321,6 +321,8 @@ def main():
     ap.add_argument("--only-llama", action="store_true", help="run only the Llama decode leg (for profiling)")
     ap.add_argument("--only-gemm", action="store_true",
                     help="run only the MFMA legs (int8 prefill GEMM + RMSNorm, fp32 MLP), for profiling")
+    ap.add_argument("--only-sweep", action="store_true",
+                    help="run only the M = 4 and M = 16 int8 GEMVs of the decode sweep (for profiling)")
     ap.add_argument("--no-graph", action="store_true", help="launch each step directly instead of from HIP graphs")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one residual add of known traffic (for profiler counter scaling)")
@@ -349,6 +351,15 @@ def main():
             out[name] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
                          "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
             log(f"{name}: {per:.4f} ms/step, {tf:.1f} TFLOP/s")
+        print(json.dumps(out), flush=True)
+        return
+    if args.only_sweep:
+        out = {}
+        for m in (4, 16):
+            per, gbs = bench_gemv(hip, m, args.steps, args.warmup, COPIES, rng)
+            out[f"gemv_m{m}"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
+                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+            log(f"gemv M={m}: {per * 1e3:.2f} us/step, {gbs:.1f} GB/s")
         print(json.dumps(out), flush=True)
         return
     if args.calibrate:

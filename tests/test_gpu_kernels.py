@@ -228,6 +228,68 @@ def test_gemv_unaligned_a(m):
     assert_gamma_bound(c.numpy(), case["a"], dequant_host(case["bq"], k, n))
 
 
+# ---- split-bf16 MFMA GEMV: 1 < m <= 16, no zero points, k a multiple of 32 --------------------
+# Each activation enters three bf16 MFMAs as hi + mid + lo (exact), each weight byte as an
+# exact bf16; only the fp32 accumulation rounds.
+
+def _split_case(m, k, n, seed, whole_scale=False, a=None, q=None):
+    r = np.random.default_rng(seed)
+    if q is None:
+        q = r.integers(-127, 128, size=k * n, dtype=np.int8)
+    scale = r.uniform(1e-3, 1e-2, size=1 if whole_scale else n).astype(np.float32)
+    if a is None:
+        a = r.standard_normal((m, k)).astype(np.float32)
+    return dict(name="split", m=m, k=k, n=n, a=a,
+                bq=dict(q=q, scale=scale, zero=None, shape=[k, n], axis=-1 if whole_scale else 1, offset=0))
+
+
+@pytest.mark.parametrize("m,k,n,whole", [
+    (2, 32, 8, False), (3, 64, 1001, False), (5, 576, 1536, False), (8, 1024, 77, True), (4, 96, 14336, False),
+    (13, 4096, 264, False), (16, 8192, 130, False), (16, 12288, 2048, True)])
+def test_gemv_split_bf16_bound(m, k, n, whole):
+    """Ragged n (tiles past the end of the last 16-tile group), one block, split K, a
+    whole-tensor scale: within 2 gamma_K of the float64 product, and for k <= 1024 also the
+    plugin tolerance."""
+    case = _split_case(m, k, n, 31 * m + k, whole_scale=whole)
+    got = matmul_quantized(case)
+    w = dequant_host(case["bq"], k, n)
+    assert_gamma_bound(got, case["a"], w)
+    if k <= 1024:
+        want = case["a"].astype(np.float64) @ w.astype(np.float64)
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("m,k,n", [(4, 576, 1536), (16, 1024, 264), (7, 4096, 136)])
+def test_gemv_split_bf16_integer_sums_exact(m, k, n):
+    """Integer A with |a| <= 16: every partial sum is an integer below 2^24, so any order of
+    summation gives the exact sum S and C = fl(S * scale) bit for bit. A row, column or k
+    slot paired wrongly anywhere changes S."""
+    r = np.random.default_rng(m * k + n)
+    a = r.integers(-16, 17, size=(m, k)).astype(np.float32)
+    case = _split_case(m, k, n, 5 + m, a=a)
+    got = matmul_quantized(case)
+    s = a.astype(np.int64) @ case["bq"]["q"].reshape(k, n).astype(np.int64)
+    assert np.abs(s).max() < 2 ** 24
+    same_bits(got, (s.astype(np.float32) * case["bq"]["scale"][None, :]).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,k,n", [(16, 4096, 1001), (3, 96, 64), (9, 1024, 520)])
+def test_gemv_split_bf16_full_precision_a(m, k, n):
+    """One nonzero weight per column, a power of two: C = fl(a * w * scale) exactly, which
+    needs all 24 significand bits of every activation (N(0, 1) values) to reach the sum;
+    dropping the mid or lo bf16 part, or pairing a k slot wrongly, changes bits."""
+    r = np.random.default_rng(k + n)
+    rows = r.integers(0, k, size=n)
+    vals = r.choice(np.array([-64, -8, -2, -1, 1, 4, 16, 64], np.int8), size=n)
+    q = np.zeros((k, n), np.int8)
+    q[rows, np.arange(n)] = vals
+    case = _split_case(m, k, n, 9 + m, q=q.ravel())
+    got = matmul_quantized(case)
+    a = case["a"]
+    prod = (a[:, rows] * vals.astype(np.float32)[None, :]).astype(np.float32)  # exact: power-of-two w
+    same_bits(got, (prod * case["bq"]["scale"][None, :]).astype(np.float32))
+
+
 def _gemv_m1_pair(case, epi=None):
     """C from an 8-byte aligned A (the m = 1 entry kernel, for an even k <= 4096 without zero
     points) and from the same A at a 4-byte offset (the general narrow kernel, single A loads)."""
