@@ -387,6 +387,7 @@ void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
   if (m < 1 || n < 1 || k < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMM shape out of range");
   Context& ctx0 = Ctx();
   const bool q8 = bq.q != nullptr;
+  if (q8 && LaunchGemmQ8Bf16(a, bq, c, m, k, n, epi, stream)) return;
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // Large tiles when they alone give about two workgroups per CU; 64x64 otherwise.
   int bm = 128, bn = 128;

@@ -1,0 +1,250 @@
+// int8-weight GEMM on the bf16 matrix cores: C[m, n] = A[m, k] @ (q[k, n] * scale) for
+// accel::MatMulQuantized with m > 16 (src/sim_device.cc:541-602), per-column or whole-tensor
+// scale, no zero points.
+//
+// Exact products on v_mfma_f32_32x32x16_bf16:
+//  * every weight byte is an integer in [-128, 127], which bf16 holds exactly;
+//  * every activation x is split as x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi),
+//    lo = bf16(x - hi - mid); both differences are exact in fp32 and the parts carry all 24
+//    significand bits (for |x| >= 2^-110), so three MFMAs per k step multiply by x exactly
+//    and only the fp32 accumulation rounds, as in the fp32-MFMA GEMM. The column scale
+//    multiplies each finished sum once.
+// Bound: MFMA. 2*m*n*k algorithmic flops per call run as 3 bf16 MFMA passes, so the
+// roofline is a third of the dense bf16 peak (2.5 PFLOP/s / 3 = 833 TFLOP/s), 5.3 times the
+// fp32-MFMA peak.
+//
+//  * Workgroup tile 128 x 128, K step 32, 256 threads = 2 x 2 waves of 64 x 64 (2 x 2 MFMA
+//    tiles of 32 x 32).
+//  * A is loaded as fp32 (float4 along k), split on its way into LDS into three bf16 planes
+//    [part][row][k]; the int8 panel is converted to bf16 and stored transposed, [column][k],
+//    so every MFMA operand (8 consecutive k of one row or column) is one 16-byte LDS read.
+//    Rows are padded to 80 bytes, which keeps those reads free of bank conflicts.
+//  * kStages register sets: chunk ch + kStages is requested while chunk ch is multiplied;
+//    the LDS planes are double buffered, one barrier per chunk.
+//  * Tiles are dealt to the 8 XCDs in contiguous runs, ordered in bands of 4 row tiles, so
+//    the workgroups resident on one XCD share A rows and W columns in its L2.
+#include "device_common.h"
+
+namespace accel_hip {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 32;
+constexpr int kThreads = 256;
+constexpr int kRowWords = kBK / 2 + 4;  // one LDS row: 32 bf16 (16 words) + 4 words of padding
+constexpr int kAPlaneWords = kBM * kRowWords;
+constexpr int kBufWords = 3 * kAPlaneWords + kBN * kRowWords;  // three A planes + the W plane
+constexpr int kStages = 3;
+constexpr int kXcds = 8;
+constexpr int kBand = 4;  // row tiles per band of the tile order
+
+struct Q8GemmArgs {
+  const float* a;
+  const int8_t* q;
+  const float* scale;
+  int32_t mode;
+  int64_t const_index;
+  float* c;
+  int64_t m, k, n;
+  int32_t tiles_m, tiles_n, tiles, tiles_per_xcd;
+  Epilogue epi;
+};
+
+// Two floats to one word of two bf16 (round to nearest even).
+__device__ __forceinline__ uint32_t PackBf16(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
+}
+__device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// The global part of one chunk, as loaded: A rows (tid / 8) + 32i, k quad tid % 8; W rows
+// 2 * (tid / 16) and + 1, column octet tid % 16.
+struct Panels {
+  float4 a[4];
+  u32x2 b[2];
+};
+
+// Rows and columns past the matrix read a clamped, valid element; their results are never
+// stored (every chunk lies inside k, which is a multiple of kBK).
+__device__ __forceinline__ void LoadPanels(const Q8GemmArgs& p, int64_t m0, int64_t n0, int64_t k0, int tid,
+                                           Panels& r) {
+  const int kq = tid & 7;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = m0 + (tid >> 3) + 32 * i;
+    const int64_t rc = row < p.m ? row : p.m - 1;
+    r.a[i] = *reinterpret_cast<const float4*>(p.a + rc * p.k + k0 + 4 * kq);
+  }
+  const int64_t col = n0 + 8 * (tid & 15);
+  const int64_t cc = col < p.n ? col : p.n - 8;
+  const int64_t kr = k0 + 2 * (tid >> 4);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) r.b[h] = *reinterpret_cast<const u32x2*>(p.q + (kr + h) * p.n + cc);
+}
+
+__device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels& r) {
+  const int kq = tid & 7;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (tid >> 3) + 32 * i;
+    const float x[4] = {r.a[i].x, r.a[i].y, r.a[i].z, r.a[i].w};
+    uint32_t part[3][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float x0 = x[2 * h];
+      const float x1 = x[2 * h + 1];
+      part[0][h] = PackBf16(x0, x1);
+      const float r0 = x0 - Bf16Low(part[0][h]);
+      const float r1 = x1 - Bf16High(part[0][h]);
+      part[1][h] = PackBf16(r0, r1);
+      part[2][h] = PackBf16(r0 - Bf16Low(part[1][h]), r1 - Bf16High(part[1][h]));
+    }
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+      *reinterpret_cast<u32x2*>(&buf[pl * kAPlaneWords + row * kRowWords + 2 * kq]) = u32x2{part[pl][0], part[pl][1]};
+  }
+  // W transposed: word kp of column row c holds rows (2kp, 2kp + 1).
+  uint32_t* wplane = buf + 3 * kAPlaneWords;
+  const int kp = tid >> 4;
+  const int oct = tid & 15;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    wplane[(8 * oct + c) * kRowWords + kp] =
+        PackBf16(ByteToFloat(r.b[0][c >> 2], c & 3), ByteToFloat(r.b[1][c >> 2], c & 3));
+}
+
+__device__ __forceinline__ void ComputeChunk(const uint32_t* buf, int lane, int wm, int wn, v16f (&acc)[2][2]) {
+  const uint32_t* wplane = buf + 3 * kAPlaneWords;
+#pragma unroll
+  for (int ks = 0; ks < kBK; ks += 16) {
+    const int word = ks / 2 + 4 * (lane >> 5);  // 8 consecutive k of this lane's row / column
+    u32x4 av[3][2];
+    u32x4 bv[2];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        av[pl][i] = *reinterpret_cast<const u32x4*>(
+            &buf[pl * kAPlaneWords + (wm * 64 + i * 32 + (lane & 31)) * kRowWords + word]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      bv[j] = *reinterpret_cast<const u32x4*>(&wplane[(wn * 64 + j * 32 + (lane & 31)) * kRowWords + word]);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[pl][i]),
+                                                              __builtin_bit_cast(bf16x8, bv[j]), acc[i][j], 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
+  __shared__ __align__(16) uint32_t lds[2 * kBufWords];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  // Contiguous runs of tiles per XCD (workgroup b runs on XCD b % 8), in bands of kBand row
+  // tiles walked column by column.
+  const int t = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
+  if (t >= p.tiles) return;
+  const int band_tiles = kBand * p.tiles_n;
+  const int band = t / band_tiles;
+  const int in_band = t % band_tiles;
+  const int rows_in_band = min(kBand, p.tiles_m - band * kBand);
+  const int tm = band * kBand + in_band % rows_in_band;
+  const int tn = in_band / rows_in_band;
+  const int64_t m0 = static_cast<int64_t>(tm) * kBM;
+  const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+  const int chunks = static_cast<int>(p.k / kBK);
+
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  Panels regs[kStages];
+#pragma unroll
+  for (int st = 0; st < kStages; ++st)
+    if (st < chunks) LoadPanels(p, m0, n0, static_cast<int64_t>(st) * kBK, tid, regs[st]);
+  StorePanels(lds, tid, regs[0]);
+  __syncthreads();
+  for (int base = 0; base < chunks; base += kStages) {
+#pragma unroll
+    for (int st = 0; st < kStages; ++st) {
+      const int ch = base + st;
+      if (ch >= chunks) break;  // workgroup-uniform
+      if (ch + kStages < chunks) LoadPanels(p, m0, n0, static_cast<int64_t>(ch + kStages) * kBK, tid, regs[st]);
+      ComputeChunk(lds + (ch & 1) * kBufWords, lane, wm, wn, acc);
+      if (ch + 1 < chunks) StorePanels(lds + ((ch + 1) & 1) * kBufWords, tid, regs[(st + 1) % kStages]);
+      __syncthreads();
+    }
+  }
+
+  // Element r of a 32 x 32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    if (col >= p.n) continue;
+    const float cs = p.scale[p.mode == kScalePerCol ? col : p.const_index];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < p.m) StoreC(p.c, row, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(acc[i][j][r], cs), row, col, p.n, p.epi));
+      }
+  }
+}
+
+}  // namespace
+
+bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
+                      hipStream_t stream) {
+  if (b.q == nullptr || b.zero != nullptr || (b.mode != kScalePerCol && b.mode != kScaleConst)) return false;
+  if (m < 1 || k < kBK || n < 8 || k % kBK != 0 || n % 8 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a) % 16 != 0 || reinterpret_cast<uintptr_t>(b.q) % 8 != 0) return false;
+  const int64_t tiles_m = (m + kBM - 1) / kBM;
+  const int64_t tiles_n = (n + kBN - 1) / kBN;
+  const int64_t tiles = tiles_m * tiles_n;
+  Context& ctx = Ctx();
+  const int64_t cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
+  // Only grids that fill the GPU without a K split (smaller products keep the fp32 kernel's
+  // split-K).
+  if (tiles < cus || tiles * kBand > 0x7fffffff) return false;
+  Q8GemmArgs args;
+  args.a = a;
+  args.q = b.q;
+  args.scale = b.scale;
+  args.mode = b.mode;
+  args.const_index = b.const_index;
+  args.c = c;
+  args.m = m;
+  args.k = k;
+  args.n = n;
+  args.tiles_m = static_cast<int32_t>(tiles_m);
+  args.tiles_n = static_cast<int32_t>(tiles_n);
+  args.tiles = static_cast<int32_t>(tiles);
+  args.tiles_per_xcd = static_cast<int32_t>((tiles + kXcds - 1) / kXcds);
+  args.epi = epi;
+  const dim3 grid(static_cast<uint32_t>(args.tiles_per_xcd * kXcds));
+  hipLaunchKernelGGL(GemmQ8Bf16Kernel, grid, dim3(kThreads), 0, stream, args);
+  Check(hipGetLastError(), "GemmQ8Bf16Kernel launch");
+  return true;
+}
+
+}  // namespace accel_hip

@@ -358,6 +358,72 @@ def test_gemm_int8_panels(m, k, n):
         np.testing.assert_allclose(got, case["a"] @ w, rtol=1e-5, atol=1e-5)
 
 
+# ---- int8 GEMM on the bf16 matrix cores: m > 16, k % 32 == 0, at least one 128 x 128 tile per
+# CU (256 on MI355X); activations enter as three exact bf16 parts, weights as exact bf16 ------
+
+@pytest.mark.parametrize("m,k,n,whole", [(512, 256, 8192, False), (500, 96, 8200, True), (2048, 32, 2048, False),
+                                         (260, 1024, 16384, False)])
+def test_gemm_q8_bf16_bound(m, k, n, whole):
+    """Ragged m and n (clamped loads, masked stores), one chunk, a whole-tensor scale: within
+    2 gamma_K of the float64 product, and the plugin tolerance for k <= 256. (At k = 1024 these
+    weights give outputs of std 13 and up to 100, where 1e-5 absolute is below the fp32
+    rounding of any summation order; the fp32-MFMA kernel misses it on more elements than
+    this one, so the gamma_K bound is the test there.)"""
+    case = _split_case(m, k, n, m + k + n, whole_scale=whole)
+    got = matmul_quantized(case)
+    w = dequant_host(case["bq"], k, n)
+    assert_gamma_bound(got, case["a"], w)
+    if k <= 256:
+        np.testing.assert_allclose(got, case["a"].astype(np.float64) @ w.astype(np.float64), rtol=1e-5, atol=1e-5)
+
+
+def test_gemm_q8_bf16_integer_sums_exact():
+    """Integer A with |a| <= 16 and k = 4096: every partial sum is an integer below 2^24, so
+    C = fl(S * scale) bit for bit; a row, column or k slot paired wrongly changes S."""
+    m, k, n = 256, 4096, 16384
+    r = np.random.default_rng(91)
+    a = r.integers(-16, 17, size=(m, k)).astype(np.float32)
+    case = _split_case(m, k, n, 92, a=a)
+    got = matmul_quantized(case)
+    s = a.astype(np.float64) @ case["bq"]["q"].reshape(k, n).astype(np.float64)  # integers below 2^53: exact
+    assert np.abs(s).max() < 2 ** 24
+    same_bits(got, (s.astype(np.float32) * case["bq"]["scale"][None, :]).astype(np.float32))
+
+
+def test_gemm_q8_bf16_full_precision_a():
+    """One power-of-two weight per column: C = fl(a * w * scale) exactly, which needs all 24
+    significand bits of every N(0, 1) activation (all three bf16 parts) to reach the sum."""
+    m, k, n = 640, 512, 6656
+    r = np.random.default_rng(93)
+    rows = r.integers(0, k, size=n)
+    vals = r.choice(np.array([-64, -8, -2, -1, 1, 4, 16, 64], np.int8), size=n)
+    q = np.zeros((k, n), np.int8)
+    q[rows, np.arange(n)] = vals
+    case = _split_case(m, k, n, 94, q=q.ravel())
+    got = matmul_quantized(case)
+    prod = (case["a"][:, rows] * vals.astype(np.float32)[None, :]).astype(np.float32)
+    same_bits(got, (prod * case["bq"]["scale"][None, :]).astype(np.float32))
+
+
+def test_gemm_q8_bf16_epilogues():
+    """alpha, beta * bias, Relu / exact Gelu and a same-shape residual applied to the scaled
+    sums, against the oracle's epilogue of the float64 product."""
+    m, k, n = 512, 128, 8192
+    case = _split_case(m, k, n, 95)
+    r = np.random.default_rng(96)
+    bias = r.standard_normal(n).astype(np.float32)
+    resid = r.standard_normal((m, n)).astype(np.float32)
+    bias_d, res_d = dev(bias), dev(resid)
+    base = (case["a"].astype(np.float64) @ dequant_host(case["bq"], k, n).astype(np.float64)).astype(np.float32)
+    o = oracle()
+    for act in (1, 2):
+        e = Epilogue(alpha=1.5, beta=0.5, bias=bias_d.ptr, bias_rank=1, activation=act, residual=res_d.ptr)
+        e.bias_shape[0] = n
+        got = matmul_quantized(case, e)
+        want = o.gemm_epilogue(base, 1.5, bias, [n], 0.5, act) + resid
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
 def test_gemm_c4_shape_with_fused_rmsnorm():
     """The prefill product at full size, X[2048, 4096] @ int8 W[4096, 14336] per-column scale
     with the RMSNormalization of the output rows fused: 40 sampled rows (first, last, random)
