@@ -18,7 +18,10 @@
 //  * A is loaded as fp32 (float4 along k), split on its way into LDS into three bf16 planes
 //    [part][row][k]; the int8 panel is converted to bf16 and stored transposed, [column][k],
 //    so every MFMA operand (8 consecutive k of one row or column) is one 16-byte LDS read.
-//    Rows are padded to 80 bytes, which keeps those reads free of bank conflicts.
+//    Each 64-byte row holds four 16-byte k groups, group g of row R at slot g ^ ((R/2) % 4):
+//    the eight rows of one read phase then cover all 32 banks, and so do the two rows of one
+//    write phase of A. Each thread writes its W columns in a rotated order (column
+//    (c + oct) % 8 at step c), so that the lanes of one write hit different banks.
 //  * kStages register sets: chunk ch + kStages is requested while chunk ch is multiplied;
 //    the LDS planes are double buffered, one barrier per chunk.
 //  * Tiles are dealt to the 8 XCDs in contiguous runs, ordered in bands of 4 row tiles, so
@@ -39,7 +42,7 @@ constexpr int kBM = 128;
 constexpr int kBN = 128;
 constexpr int kBK = 32;
 constexpr int kThreads = 256;
-constexpr int kRowWords = kBK / 2 + 4;  // one LDS row: 32 bf16 (16 words) + 4 words of padding
+constexpr int kRowWords = kBK / 2;  // one LDS row: 32 bf16 (16 words), k groups swizzled
 constexpr int kAPlaneWords = kBM * kRowWords;
 constexpr int kBufWords = 3 * kAPlaneWords + kBN * kRowWords;  // three A planes + the W plane
 constexpr int kStages = 3;
@@ -90,6 +93,9 @@ __device__ __forceinline__ void LoadPanels(const Q8GemmArgs& p, int64_t m0, int6
   for (int h = 0; h < 2; ++h) r.b[h] = *reinterpret_cast<const u32x2*>(p.q + (kr + h) * p.n + cc);
 }
 
+// Word offset of 16-byte k group g (0..3) of LDS row `row`.
+__device__ __forceinline__ int GroupWord(int row, int g) { return row * kRowWords + 4 * (g ^ ((row >> 1) & 3)); }
+
 __device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels& r) {
   const int kq = tid & 7;
 #pragma unroll
@@ -107,36 +113,48 @@ __device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels
       part[1][h] = PackBf16(r0, r1);
       part[2][h] = PackBf16(r0 - Bf16Low(part[1][h]), r1 - Bf16High(part[1][h]));
     }
+    const int wo = GroupWord(row, kq >> 1) + 2 * (kq & 1);
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-      *reinterpret_cast<u32x2*>(&buf[pl * kAPlaneWords + row * kRowWords + 2 * kq]) = u32x2{part[pl][0], part[pl][1]};
+    for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<u32x2*>(&buf[pl * kAPlaneWords + wo]) = u32x2{part[pl][0], part[pl][1]};
   }
-  // W transposed: word kp of column row c holds rows (2kp, 2kp + 1).
+  // W transposed: word kp of column row nl holds rows (2kp, 2kp + 1). The 8 bytes of each W
+  // row are rotated by s = oct % 8 first (byte c of the result is column (c + s) % 8).
   uint32_t* wplane = buf + 3 * kAPlaneWords;
   const int kp = tid >> 4;
   const int oct = tid & 15;
+  const int s = oct & 7;
+  uint32_t rot[2][2];
 #pragma unroll
-  for (int c = 0; c < 8; ++c)
-    wplane[(8 * oct + c) * kRowWords + kp] =
-        PackBf16(ByteToFloat(r.b[0][c >> 2], c & 3), ByteToFloat(r.b[1][c >> 2], c & 3));
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t lo = (s & 4) ? r.b[h][1] : r.b[h][0];
+    const uint32_t hi = (s & 4) ? r.b[h][0] : r.b[h][1];
+    rot[h][0] = __builtin_amdgcn_alignbyte(hi, lo, s & 3);
+    rot[h][1] = __builtin_amdgcn_alignbyte(lo, hi, s & 3);
+  }
+  const int wsub = kp & 3;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int nl = 8 * oct + ((c + s) & 7);
+    wplane[GroupWord(nl, kp >> 2) + wsub] =
+        PackBf16(ByteToFloat(rot[0][c >> 2], c & 3), ByteToFloat(rot[1][c >> 2], c & 3));
+  }
 }
 
 __device__ __forceinline__ void ComputeChunk(const uint32_t* buf, int lane, int wm, int wn, v16f (&acc)[2][2]) {
   const uint32_t* wplane = buf + 3 * kAPlaneWords;
 #pragma unroll
   for (int ks = 0; ks < kBK; ks += 16) {
-    const int word = ks / 2 + 4 * (lane >> 5);  // 8 consecutive k of this lane's row / column
+    const int g = ks / 8 + (lane >> 5);  // k group: 8 consecutive k of this lane's row / column
     u32x4 av[3][2];
     u32x4 bv[2];
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        av[pl][i] = *reinterpret_cast<const u32x4*>(
-            &buf[pl * kAPlaneWords + (wm * 64 + i * 32 + (lane & 31)) * kRowWords + word]);
+        av[pl][i] = *reinterpret_cast<const u32x4*>(&buf[pl * kAPlaneWords + GroupWord(wm * 64 + i * 32 + (lane & 31), g)]);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      bv[j] = *reinterpret_cast<const u32x4*>(&wplane[(wn * 64 + j * 32 + (lane & 31)) * kRowWords + word]);
+      bv[j] = *reinterpret_cast<const u32x4*>(&wplane[GroupWord(wn * 64 + j * 32 + (lane & 31), g)]);
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
