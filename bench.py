@@ -34,6 +34,9 @@ ROOT = Path(__file__).resolve().parent
 METRIC = "int8-W GEMV HBM GB/s + GEMM fp32-MFMA TFLOP/s (% peak); decode tok/s"
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+# The int8-weight GEMM runs each fp32 product as three exact bf16 MFMA passes (activation split
+# into hi + mid + lo): its roofline is a third of the dense bf16 peak.
+BF16X3_PEAK_TFLOPS = 2500.0 / 3
 K_DIM, N_DIM = 4096, 14336
 COPIES = 8
 
@@ -350,6 +353,10 @@ def main():
             per, tf = leg(hip, args.steps, args.warmup, rng)
             out[name] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
                          "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+            if name.startswith("prefill"):
+                out[name]["mfma_frac"] = None
+                out[name]["vs_fp32_mfma_peak"] = round(tf / FP32_MFMA_PEAK_TFLOPS, 4)
+                out[name]["bf16x3_roofline_frac"] = round(tf / BF16X3_PEAK_TFLOPS, 4)
             log(f"{name}: {per:.4f} ms/step, {tf:.1f} TFLOP/s")
         print(json.dumps(out), flush=True)
         return
@@ -386,9 +393,12 @@ def main():
         log(f"mlp fp32: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
         steps4 = max(1, args.steps // 20)
         per, tf = bench_prefill(hip, steps4, max(1, args.warmup // 20), rng)
-        secondary["prefill_int8_rmsnorm"] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
-                                             "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "steps": steps4,
-                                             "config": "X[2048,4096] @ int8 W[4096,14336] + RMSNorm(eps 1e-5)"}
+        secondary["prefill_int8_rmsnorm"] = {
+            "ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
+            "vs_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "bf16x3_roofline_frac": round(tf / BF16X3_PEAK_TFLOPS, 4),
+            "kernel": "GemmQ8Bf16Kernel: exact fp32 products as 3 bf16 MFMA passes, roofline 833 TFLOP/s",
+            "steps": steps4, "config": "X[2048,4096] @ int8 W[4096,14336] + RMSNorm(eps 1e-5)"}
         log(f"prefill int8+rms: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
         llama = bench_llama(hip, np.random.default_rng(11))
         secondary["llama_decode"] = llama
