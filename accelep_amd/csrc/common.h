@@ -164,8 +164,8 @@ void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
                    const Epilogue& epi, hipStream_t stream);
 // The int8-weight GEMM on the bf16 matrix cores (exact products, activations split into
 // three bf16 parts): k % 32 == 0, n % 8 == 0, A 16-byte and q 8-byte aligned, per-column or
-// whole-tensor scale, no zero points, and at least one 128 x 128 tile per CU. Returns false,
-// launching nothing, otherwise.
+// whole-tensor scale, no zero points (a grid of fewer 128 x 128 tiles than CUs splits K).
+// Returns false, launching nothing, otherwise.
 bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
                       hipStream_t stream);
 // C = A @ B in the reference's order and rounding (one k-ordered chain per output, split

@@ -26,7 +26,11 @@
 //    the LDS planes are double buffered, one barrier per chunk.
 //  * Tiles are dealt to the 8 XCDs in contiguous runs, ordered in bands of 4 row tiles, so
 //    the workgroups resident on one XCD share A rows and W columns in its L2.
+//  * A grid of fewer tiles than CUs splits K (whole chunks); the partial sums go to the
+//    workspace and SplitReduceKernel adds them in split order, scales and applies the epilogue.
 #include "device_common.h"
+
+#include <algorithm>
 
 namespace accel_hip {
 namespace {
@@ -58,6 +62,8 @@ struct Q8GemmArgs {
   float* c;
   int64_t m, k, n;
   int32_t tiles_m, tiles_n, tiles, tiles_per_xcd;
+  int64_t k_per_split;  // a multiple of kBK
+  float* partials;      // [splits][m][n] raw sums when the K range is split, else nullptr
   Epilogue epi;
 };
 
@@ -185,7 +191,8 @@ __global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
   const int tn = in_band / rows_in_band;
   const int64_t m0 = static_cast<int64_t>(tm) * kBM;
   const int64_t n0 = static_cast<int64_t>(tn) * kBN;
-  const int chunks = static_cast<int>(p.k / kBK);
+  const int64_t kb = static_cast<int64_t>(blockIdx.y) * p.k_per_split;
+  const int chunks = static_cast<int>((min(p.k, kb + p.k_per_split) - kb) / kBK);
 
   v16f acc[2][2];
 #pragma unroll
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
   Panels regs[kStages];
 #pragma unroll
   for (int st = 0; st < kStages; ++st)
-    if (st < chunks) LoadPanels(p, m0, n0, static_cast<int64_t>(st) * kBK, tid, regs[st]);
+    if (st < chunks) LoadPanels(p, m0, n0, kb + static_cast<int64_t>(st) * kBK, tid, regs[st]);
   StorePanels(lds, tid, regs[0]);
   __syncthreads();
   for (int base = 0; base < chunks; base += kStages) {
@@ -206,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
     for (int st = 0; st < kStages; ++st) {
       const int ch = base + st;
       if (ch >= chunks) break;  // workgroup-uniform
-      if (ch + kStages < chunks) LoadPanels(p, m0, n0, static_cast<int64_t>(ch + kStages) * kBK, tid, regs[st]);
+      if (ch + kStages < chunks) LoadPanels(p, m0, n0, kb + static_cast<int64_t>(ch + kStages) * kBK, tid, regs[st]);
       ComputeChunk(lds + (ch & 1) * kBufWords, lane, wm, wn, acc);
       if (ch + 1 < chunks) StorePanels(lds + ((ch + 1) & 1) * kBufWords, tid, regs[(st + 1) % kStages]);
       __syncthreads();
@@ -214,6 +221,22 @@ __global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
   }
 
   // Element r of a 32 x 32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
+  if (p.partials != nullptr) {  // SplitReduceKernel adds the splits in order, scales, applies the epilogue
+    float* part = p.partials + static_cast<int64_t>(blockIdx.y) * p.m * p.n;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+      if (col >= p.n) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (row < p.m) part[row * p.n + col] = acc[i][j][r];
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
@@ -239,11 +262,17 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
   const int64_t tiles_m = (m + kBM - 1) / kBM;
   const int64_t tiles_n = (n + kBN - 1) / kBN;
   const int64_t tiles = tiles_m * tiles_n;
-  Context& ctx = Ctx();
-  const int64_t cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
-  // Only grids that fill the GPU without a K split (smaller products keep the fp32 kernel's
-  // split-K).
-  if (tiles < cus || tiles * kBand > 0x7fffffff) return false;
+  Context& ctx0 = Ctx();
+  const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
+  if (tiles * kBand > 0x7fffffff) return false;
+  // A grid short of one tile per CU splits K into ranges of whole chunks (at least 3 each),
+  // to about two workgroups per CU; a second kernel adds the partial sums in split order.
+  const int64_t chunks = k / kBK;
+  int64_t splits = 1;
+  if (tiles < cus) splits = std::max<int64_t>(1, std::min<int64_t>((2 * cus + tiles - 1) / tiles, chunks / 3));
+  const int64_t kper = (chunks + splits - 1) / splits * kBK;
+  splits = (k + kper - 1) / kper;
+  if (splits > 65535) return false;
   Q8GemmArgs args;
   args.a = a;
   args.q = b.q;
@@ -258,10 +287,15 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
   args.tiles_n = static_cast<int32_t>(tiles_n);
   args.tiles = static_cast<int32_t>(tiles);
   args.tiles_per_xcd = static_cast<int32_t>((tiles + kXcds - 1) / kXcds);
+  args.k_per_split = kper;
+  args.partials = nullptr;
   args.epi = epi;
-  const dim3 grid(static_cast<uint32_t>(args.tiles_per_xcd * kXcds));
+  if (splits > 1) args.partials = static_cast<float*>(Scratch(static_cast<size_t>(splits * m * n) * sizeof(float)).workspace);
+  const dim3 grid(static_cast<uint32_t>(args.tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
   hipLaunchKernelGGL(GemmQ8Bf16Kernel, grid, dim3(kThreads), 0, stream, args);
   Check(hipGetLastError(), "GemmQ8Bf16Kernel launch");
+  if (splits > 1) LaunchSplitReduce(args.partials, static_cast<int32_t>(splits), m, n, c, b.mode, b.scale, b.const_index,
+                                    epi, stream);
   return true;
 }
 

@@ -349,13 +349,17 @@ def test_gemv_m1_entry_kernel_epilogues():
 
 @pytest.mark.parametrize("m,k,n", [(512, 576, 1536), (64, 4096, 1024), (100, 200, 300), (2048, 576, 192)])
 def test_gemm_int8_panels(m, k, n):
-    """m > 16: fp32 MFMA GEMM with the int8 panel dequantized in LDS."""
+    """m > 16: the bf16-MFMA GEMM with split K (these grids have fewer 128 x 128 tiles than
+    CUs), or the fp32-MFMA GEMM with the int8 panel dequantized in LDS (zero points, k not a
+    multiple of 32)."""
     case = c3_case(m, k, n, 31 * m + n, zero=(m == 100))
     got = matmul_quantized(case)
     w = dequant_host(case["bq"], k, n)
     assert_gamma_bound(got, case["a"], w)
     if k <= 1024:
-        np.testing.assert_allclose(got, case["a"] @ w, rtol=1e-5, atol=1e-5)
+        # Against the float64 product: numpy's own float32 product misses this tolerance on
+        # about 100 elements of the 512 x 576 x 1536 case.
+        np.testing.assert_allclose(got, case["a"].astype(np.float64) @ w.astype(np.float64), rtol=1e-5, atol=1e-5)
 
 
 # ---- int8 GEMM on the bf16 matrix cores: m > 16, k % 32 == 0, at least one 128 x 128 tile per
@@ -377,13 +381,14 @@ def test_gemm_q8_bf16_bound(m, k, n, whole):
         np.testing.assert_allclose(got, case["a"].astype(np.float64) @ w.astype(np.float64), rtol=1e-5, atol=1e-5)
 
 
-def test_gemm_q8_bf16_integer_sums_exact():
-    """Integer A with |a| <= 16 and k = 4096: every partial sum is an integer below 2^24, so
-    C = fl(S * scale) bit for bit; a row, column or k slot paired wrongly changes S."""
-    m, k, n = 256, 4096, 16384
-    r = np.random.default_rng(91)
+@pytest.mark.parametrize("m,k,n", [(256, 4096, 16384), (100, 2048, 264), (512, 576, 3072)])
+def test_gemm_q8_bf16_integer_sums_exact(m, k, n):
+    """Integer A with |a| <= 16: every partial sum is an integer below 2^24, so C = fl(S *
+    scale) bit for bit; a row, column or k slot paired wrongly changes S. The last two
+    shapes have fewer tiles than CUs and split K (21 and 6 splits)."""
+    r = np.random.default_rng(91 + m)
     a = r.integers(-16, 17, size=(m, k)).astype(np.float32)
-    case = _split_case(m, k, n, 92, a=a)
+    case = _split_case(m, k, n, 92 + m, a=a)
     got = matmul_quantized(case)
     s = a.astype(np.float64) @ case["bq"]["q"].reshape(k, n).astype(np.float64)  # integers below 2^53: exact
     assert np.abs(s).max() < 2 ** 24
