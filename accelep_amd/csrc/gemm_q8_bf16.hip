@@ -7,8 +7,9 @@
 //  * every activation x is split as x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi),
 //    lo = bf16(x - hi - mid); both differences are exact in fp32 and the parts carry all 24
 //    significand bits (for |x| >= 2^-110), so three MFMAs per k step multiply by x exactly
-//    and only the fp32 accumulation rounds, as in the fp32-MFMA GEMM. The column scale
-//    multiplies each finished sum once.
+//    and only the fp32 accumulation rounds, as in the fp32-MFMA GEMM. The hi products and
+//    the mid + lo products go to separate accumulators, added at the end, so the large sum
+//    takes one rounding per MFMA step. The column scale multiplies each finished sum once.
 // Bound: MFMA. 2*m*n*k algorithmic flops per call run as 3 bf16 MFMA passes, so the
 // roofline is a third of the dense bf16 peak (2.5 PFLOP/s / 3 = 833 TFLOP/s), 5.3 times the
 // fp32-MFMA peak.
@@ -22,8 +23,9 @@
 //    the eight rows of one read phase then cover all 32 banks, and so do the two rows of one
 //    write phase of A. Each thread writes its W columns in a rotated order (column
 //    (c + oct) % 8 at step c), so that the lanes of one write hit different banks.
-//  * kStages register sets: chunk ch + kStages is requested while chunk ch is multiplied;
-//    the LDS planes are double buffered, one barrier per chunk.
+//  * kStages register sets (2 for the 128 tile, 3 for the 64 tile): chunk ch + kStages is
+//    requested while chunk ch is multiplied; the LDS planes are double buffered, one barrier
+//    per chunk.
 //  * Tiles are dealt to the 8 XCDs in contiguous runs, ordered in bands of 4 row tiles, so
 //    the workgroups resident on one XCD share A rows and W columns in its L2.
 //  * A grid of fewer tiles than CUs splits K (whole chunks); the partial sums go to the
@@ -42,14 +44,22 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
 constexpr int kBK = 32;
 constexpr int kThreads = 256;
 constexpr int kRowWords = kBK / 2;  // one LDS row: 32 bf16 (16 words), k groups swizzled
-constexpr int kAPlaneWords = kBM * kRowWords;
-constexpr int kBufWords = 3 * kAPlaneWords + kBN * kRowWords;  // three A planes + the W plane
-constexpr int kStages = 3;
+
+// Square workgroup tiles of BM = 128 (waves of 64 x 64, 2 x 2 MFMA tiles) or 64 (waves of
+// 32 x 32, one MFMA tile).
+template <int BM>
+struct Tile {
+  static constexpr int kAPlaneWords = BM * kRowWords;
+  static constexpr int kBufWords = 4 * kAPlaneWords;  // three A planes + the W plane (BN = BM)
+  static constexpr int kS = BM / 64;                  // MFMA tiles per wave along each side
+  static constexpr int kARows = BM / 32;              // float4 loads of A per thread
+  static constexpr int kOcts = BM / 8;                // 8-column octets of a W row
+  // Register sets of panels in flight (the 128 tile's two accumulator sets leave room for 2).
+  static constexpr int kStages = BM == 128 ? 2 : 3;
+};
 constexpr int kXcds = 8;
 constexpr int kBand = 4;  // row tiles per band of the tile order
 
@@ -75,26 +85,32 @@ __device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast
 __device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
 // The global part of one chunk, as loaded: A rows (tid / 8) + 32i, k quad tid % 8; W rows
-// 2 * (tid / 16) and + 1, column octet tid % 16.
+// 2 * kp and 2 * kp + 1 of column octet oct, kp = tid / octets < 16 (for BM = 64 the upper
+// half of the threads load no W).
+template <int BM>
 struct Panels {
-  float4 a[4];
+  float4 a[Tile<BM>::kARows];
   u32x2 b[2];
 };
 
 // Rows and columns past the matrix read a clamped, valid element; their results are never
 // stored (every chunk lies inside k, which is a multiple of kBK).
+template <int BM>
 __device__ __forceinline__ void LoadPanels(const Q8GemmArgs& p, int64_t m0, int64_t n0, int64_t k0, int tid,
-                                           Panels& r) {
+                                           Panels<BM>& r) {
   const int kq = tid & 7;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < Tile<BM>::kARows; ++i) {
     const int64_t row = m0 + (tid >> 3) + 32 * i;
     const int64_t rc = row < p.m ? row : p.m - 1;
     r.a[i] = *reinterpret_cast<const float4*>(p.a + rc * p.k + k0 + 4 * kq);
   }
-  const int64_t col = n0 + 8 * (tid & 15);
+  constexpr int kOcts = Tile<BM>::kOcts;
+  const int kp = tid / kOcts;
+  if (kp >= kBK / 2) return;
+  const int64_t col = n0 + 8 * (tid % kOcts);
   const int64_t cc = col < p.n ? col : p.n - 8;
-  const int64_t kr = k0 + 2 * (tid >> 4);
+  const int64_t kr = k0 + 2 * kp;
 #pragma unroll
   for (int h = 0; h < 2; ++h) r.b[h] = *reinterpret_cast<const u32x2*>(p.q + (kr + h) * p.n + cc);
 }
@@ -102,10 +118,12 @@ __device__ __forceinline__ void LoadPanels(const Q8GemmArgs& p, int64_t m0, int6
 // Word offset of 16-byte k group g (0..3) of LDS row `row`.
 __device__ __forceinline__ int GroupWord(int row, int g) { return row * kRowWords + 4 * (g ^ ((row >> 1) & 3)); }
 
-__device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels& r) {
+template <int BM>
+__device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels<BM>& r) {
+  constexpr int kAPlaneWords = Tile<BM>::kAPlaneWords;
   const int kq = tid & 7;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < Tile<BM>::kARows; ++i) {
     const int row = (tid >> 3) + 32 * i;
     const float x[4] = {r.a[i].x, r.a[i].y, r.a[i].z, r.a[i].w};
     uint32_t part[3][2];
@@ -126,8 +144,10 @@ __device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels
   // W transposed: word kp of column row nl holds rows (2kp, 2kp + 1). The 8 bytes of each W
   // row are rotated by s = oct % 8 first (byte c of the result is column (c + s) % 8).
   uint32_t* wplane = buf + 3 * kAPlaneWords;
-  const int kp = tid >> 4;
-  const int oct = tid & 15;
+  constexpr int kOcts = Tile<BM>::kOcts;
+  const int kp = tid / kOcts;
+  if (kp >= kBK / 2) return;
+  const int oct = tid % kOcts;
   const int s = oct & 7;
   uint32_t rot[2][2];
 #pragma unroll
@@ -146,33 +166,47 @@ __device__ __forceinline__ void StorePanels(uint32_t* buf, int tid, const Panels
   }
 }
 
-__device__ __forceinline__ void ComputeChunk(const uint32_t* buf, int lane, int wm, int wn, v16f (&acc)[2][2]) {
+// The hi parts accumulate into acc_hi, the mid and lo parts into acc_ml: the sum that carries
+// the rounding of most consequence then takes one MFMA add per k step instead of three.
+template <int BM>
+__device__ __forceinline__ void ComputeChunk(const uint32_t* buf, int lane, int wm, int wn,
+                                             v16f (&acc_hi)[Tile<BM>::kS][Tile<BM>::kS],
+                                             v16f (&acc_ml)[Tile<BM>::kS][Tile<BM>::kS]) {
+  constexpr int kAPlaneWords = Tile<BM>::kAPlaneWords;
+  constexpr int S = Tile<BM>::kS;
   const uint32_t* wplane = buf + 3 * kAPlaneWords;
 #pragma unroll
   for (int ks = 0; ks < kBK; ks += 16) {
     const int g = ks / 8 + (lane >> 5);  // k group: 8 consecutive k of this lane's row / column
-    u32x4 av[3][2];
-    u32x4 bv[2];
+    u32x4 bv[S];
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
+    for (int j = 0; j < S; ++j)
+      bv[j] = *reinterpret_cast<const u32x4*>(&wplane[GroupWord(wn * (BM / 2) + j * 32 + (lane & 31), g)]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        av[pl][i] = *reinterpret_cast<const u32x4*>(&buf[pl * kAPlaneWords + GroupWord(wm * 64 + i * 32 + (lane & 31), g)]);
+    for (int pl = 0; pl < 3; ++pl) {
+      u32x4 av[S];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      bv[j] = *reinterpret_cast<const u32x4*>(&wplane[GroupWord(wn * 64 + j * 32 + (lane & 31), g)]);
+      for (int i = 0; i < S; ++i)
+        av[i] = *reinterpret_cast<const u32x4*>(
+            &buf[pl * kAPlaneWords + GroupWord(wm * (BM / 2) + i * 32 + (lane & 31), g)]);
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
+      for (int i = 0; i < S; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[pl][i]),
-                                                              __builtin_bit_cast(bf16x8, bv[j]), acc[i][j], 0, 0, 0);
+        for (int j = 0; j < S; ++j) {
+          v16f& acc = pl == 0 ? acc_hi[i][j] : acc_ml[i][j];
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[i]),
+                                                        __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
+        }
+    }
   }
 }
 
-__global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
+template <int BM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 128 ? 2 : 3))) void GemmQ8Bf16Kernel(
+    Q8GemmArgs p) {
+  constexpr int kBufWords = Tile<BM>::kBufWords;
+  constexpr int S = Tile<BM>::kS;
+  constexpr int kStages = Tile<BM>::kStages;
   __shared__ __align__(16) uint32_t lds[2 * kBufWords];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -189,20 +223,23 @@ __global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
   const int rows_in_band = min(kBand, p.tiles_m - band * kBand);
   const int tm = band * kBand + in_band % rows_in_band;
   const int tn = in_band / rows_in_band;
-  const int64_t m0 = static_cast<int64_t>(tm) * kBM;
-  const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BM;
   const int64_t kb = static_cast<int64_t>(blockIdx.y) * p.k_per_split;
   const int chunks = static_cast<int>((min(p.k, kb + p.k_per_split) - kb) / kBK);
 
-  v16f acc[2][2];
+  v16f acc[S][S], acc_ml[S][S];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < S; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < S; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.f;
+        acc_ml[i][j][r] = 0.f;
+      }
 
-  Panels regs[kStages];
+  Panels<BM> regs[kStages];
 #pragma unroll
   for (int st = 0; st < kStages; ++st)
     if (st < chunks) LoadPanels(p, m0, n0, kb + static_cast<int64_t>(st) * kBK, tid, regs[st]);
@@ -214,39 +251,46 @@ __global__ __launch_bounds__(kThreads) void GemmQ8Bf16Kernel(Q8GemmArgs p) {
       const int ch = base + st;
       if (ch >= chunks) break;  // workgroup-uniform
       if (ch + kStages < chunks) LoadPanels(p, m0, n0, kb + static_cast<int64_t>(ch + kStages) * kBK, tid, regs[st]);
-      ComputeChunk(lds + (ch & 1) * kBufWords, lane, wm, wn, acc);
+      ComputeChunk<BM>(lds + (ch & 1) * kBufWords, lane, wm, wn, acc, acc_ml);
       if (ch + 1 < chunks) StorePanels(lds + ((ch + 1) & 1) * kBufWords, tid, regs[(st + 1) % kStages]);
       __syncthreads();
     }
   }
 
+#pragma unroll
+  for (int i = 0; i < S; ++i)
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + acc_ml[i][j][r];
+
   // Element r of a 32 x 32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
   if (p.partials != nullptr) {  // SplitReduceKernel adds the splits in order, scales, applies the epilogue
     float* part = p.partials + static_cast<int64_t>(blockIdx.y) * p.m * p.n;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < S; ++j) {
+      const int64_t col = n0 + wn * (BM / 2) + j * 32 + (lane & 31);
       if (col >= p.n) continue;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < S; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
           if (row < p.m) part[row * p.n + col] = acc[i][j][r];
         }
     }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+  for (int j = 0; j < S; ++j) {
+    const int64_t col = n0 + wn * (BM / 2) + j * 32 + (lane & 31);
     if (col >= p.n) continue;
     const float cs = p.scale[p.mode == kScalePerCol ? col : p.const_index];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < S; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row < p.m) StoreC(p.c, row, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(acc[i][j][r], cs), row, col, p.n, p.epi));
       }
   }
@@ -259,11 +303,13 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
   if (b.q == nullptr || b.zero != nullptr || (b.mode != kScalePerCol && b.mode != kScaleConst)) return false;
   if (m < 1 || k < kBK || n < 8 || k % kBK != 0 || n % 8 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a) % 16 != 0 || reinterpret_cast<uintptr_t>(b.q) % 8 != 0) return false;
-  const int64_t tiles_m = (m + kBM - 1) / kBM;
-  const int64_t tiles_n = (n + kBN - 1) / kBN;
-  const int64_t tiles = tiles_m * tiles_n;
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
+  // 128 x 128 tiles when they give one per CU, else 64 x 64.
+  const int bm = ((m + 127) / 128) * ((n + 127) / 128) >= cus ? 128 : 64;
+  const int64_t tiles_m = (m + bm - 1) / bm;
+  const int64_t tiles_n = (n + bm - 1) / bm;
+  const int64_t tiles = tiles_m * tiles_n;
   if (tiles * kBand > 0x7fffffff) return false;
   // A grid short of one tile per CU splits K into ranges of whole chunks (at least 3 each),
   // to about two workgroups per CU; a second kernel adds the partial sums in split order.
@@ -292,7 +338,8 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
   args.epi = epi;
   if (splits > 1) args.partials = static_cast<float*>(Scratch(static_cast<size_t>(splits * m * n) * sizeof(float)).workspace);
   const dim3 grid(static_cast<uint32_t>(args.tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
-  hipLaunchKernelGGL(GemmQ8Bf16Kernel, grid, dim3(kThreads), 0, stream, args);
+  if (bm == 128) hipLaunchKernelGGL(GemmQ8Bf16Kernel<128>, grid, dim3(kThreads), 0, stream, args);
+  else hipLaunchKernelGGL(GemmQ8Bf16Kernel<64>, grid, dim3(kThreads), 0, stream, args);
   Check(hipGetLastError(), "GemmQ8Bf16Kernel launch");
   if (splits > 1) LaunchSplitReduce(args.partials, static_cast<int32_t>(splits), m, n, c, b.mode, b.scale, b.const_index,
                                     epi, stream);
