@@ -250,9 +250,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 
     for (int st = 0; st < kStages; ++st) {
       const int ch = base + st;
       if (ch >= chunks) break;  // workgroup-uniform
-      if (ch + kStages < chunks) LoadPanels(p, m0, n0, kb + static_cast<int64_t>(ch + kStages) * kBK, tid, regs[st]);
+      // No branch inside a step, so the scheduler can interleave the next panel's conversion
+      // and LDS stores with this chunk's MFMAs. Past the end, the loads repeat the last chunk
+      // and the store goes to the idle buffer; neither is used.
+      const int nxt = min(ch + kStages, chunks - 1);
+      LoadPanels(p, m0, n0, kb + static_cast<int64_t>(nxt) * kBK, tid, regs[st]);
       ComputeChunk<BM>(lds + (ch & 1) * kBufWords, lane, wm, wn, acc, acc_ml);
-      if (ch + 1 < chunks) StorePanels(lds + ((ch + 1) & 1) * kBufWords, tid, regs[(st + 1) % kStages]);
+      StorePanels(lds + ((ch + 1) & 1) * kBufWords, tid, regs[(st + 1) % kStages]);
       __syncthreads();
     }
   }
