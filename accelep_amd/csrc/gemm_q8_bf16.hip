@@ -257,6 +257,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 
       LoadPanels(p, m0, n0, kb + static_cast<int64_t>(nxt) * kBK, tid, regs[st]);
       ComputeChunk<BM>(lds + (ch & 1) * kBufWords, lane, wm, wn, acc, acc_ml);
       StorePanels(lds + ((ch + 1) & 1) * kBufWords, tid, regs[(st + 1) % kStages]);
+      if (BM == 128) {
+        // Interleave: one MFMA, then a share of the conversion work and of the LDS stores.
+#pragma unroll
+        for (int q = 0; q < 24; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+        }
+      }
       __syncthreads();
     }
   }
