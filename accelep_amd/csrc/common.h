@@ -101,11 +101,12 @@ inline size_t StagedGroupBytes(int64_t k, int64_t n) {
 // built on first use; nullptr when q is not inside a live allocation of this library.
 const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);
 void LaunchTileGroups(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
-// Whether LaunchGemvQ8 takes an m-row product with this k from the group-interleaved copy
-// (the caller stages that copy instead of the 8-column tiles).
+// Whether LaunchGemvQ8 takes an m-row product with this k and weight view from the
+// group-interleaved copy (the caller stages that copy instead of the 8-column tiles).
 constexpr int64_t kGemvGroupMinM = 3;
-inline bool GemvWantsGroups(int64_t m, int64_t k) {
-  return m >= kGemvGroupMinM && m <= 16 && k % kGemvGroupRows == 0;
+inline bool GemvWantsGroups(int64_t m, int64_t k, const Q8View& v) {
+  return m >= kGemvGroupMinM && m <= 16 && k % kGemvGroupRows == 0 && v.zero == nullptr &&
+         (v.mode == kScalePerCol || v.mode == kScaleConst);
 }
 
 struct Epilogue {

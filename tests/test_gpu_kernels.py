@@ -451,11 +451,13 @@ def test_gemm_c4_shape_with_fused_rmsnorm():
     assert np.isfinite(y).all()
 
 
-def test_staged_weight_follows_rewrites():
-    """The GEMV reads a staged column-tiled copy of W; rewriting W (host copy, or W used as a
-    kernel output) must be seen by the next call."""
+@pytest.mark.parametrize("m", [2, 4])
+def test_staged_weight_follows_rewrites(m):
+    """The GEMV reads a staged copy of W (8-column tiles at m = 2, the group-interleaved form
+    at m = 4); rewriting W (host copy, or W used as a kernel output) must be seen by the next
+    call."""
     r = np.random.default_rng(77)
-    m, k, n = 2, 256, 320
+    k, n = 256, 320
     q1 = r.integers(-127, 128, size=k * n, dtype=np.int8)
     q2 = r.integers(-127, 128, size=k * n, dtype=np.int8)
     s = r.uniform(1e-3, 1e-2, size=n).astype(np.float32)
