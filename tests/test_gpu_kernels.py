@@ -429,6 +429,42 @@ def test_gemm_q8_bf16_epilogues():
         np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
 
 
+@pytest.mark.parametrize("m,k,n", [(4, 4096, 1792), (100, 2048, 264)])
+def test_split_products_replay_from_graph(m, k, n):
+    """A product whose K is split (the split-bf16 GEMV with its per-group arrival counters,
+    16 splits; the bf16 GEMM with its workspace, 21 splits) captured in a HIP graph and
+    replayed three times, with other eager products between the replays: every replay stores
+    the eager result's bits (the counters are left zero by each launch)."""
+    L = lib()
+    r = np.random.default_rng(m + n)
+    q = r.integers(-127, 128, size=k * n, dtype=np.int8)
+    s = r.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    qd, sd, ad = dev(q), dev(s), dev(a)
+    plane = quant_plane(qd, sd, None, [k, n], 1)
+    out = dev(np.zeros((m, n), np.float32))
+
+    def call():
+        check(L.accel_hip_matmul_quantized(ad.ptr, None, None, C.byref(plane), out.ptr, m, k, n))
+
+    call()
+    want = out.numpy()
+    call()  # warm (staging, workspace) before the capture
+    check(L.accel_hip_capture_begin())
+    call()
+    g = C.c_void_p()
+    check(L.accel_hip_capture_end(C.byref(g)))
+    try:
+        other = _split_case(8, 1024, 1000, 7)
+        for _ in range(3):
+            out.upload(np.zeros((m, n), np.float32))
+            check(L.accel_hip_graph_launch(g, 1))
+            same_bits(out.numpy(), want)
+            matmul_quantized(other)  # eager work between the replays
+    finally:
+        check(L.accel_hip_graph_destroy(g))
+
+
 def test_gemm_c4_shape_with_fused_rmsnorm():
     """The prefill product at full size, X[2048, 4096] @ int8 W[4096, 14336] per-column scale
     with the RMSNormalization of the output rows fused: 40 sampled rows (first, last, random)
