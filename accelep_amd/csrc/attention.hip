@@ -745,7 +745,7 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
       if (work_bytes < need) Fail(ACCEL_HIP_INVALID_ARGUMENT, "attention scratch is too small");
       scratch = work;
     } else {
-      scratch = static_cast<float*>(Scratch(need).workspace);
+      scratch = static_cast<float*>(Workspace(need));
     }
   }
   const bool aligned = (reinterpret_cast<uintptr_t>(k) % 16 == 0) && (reinterpret_cast<uintptr_t>(v) % 16 == 0) &&

@@ -54,6 +54,8 @@ bool PlaneView(const AccelHipQuantPlane& p, int64_t rows, int64_t cols, Q8View* 
   return false;
 }
 
+}  // namespace
+
 Epilogue ToEpilogue(const AccelHipEpilogue* e) {
   Epilogue out;
   if (e == nullptr) return out;
@@ -79,6 +81,8 @@ Epilogue ToEpilogue(const AccelHipEpilogue* e) {
   return out;
 }
 
+namespace {
+
 // The bias of a fused epilogue must fit [m, n] by right-aligned broadcast.
 void CheckBias(const Epilogue& e, int64_t m, int64_t n) {
   if (e.bias == nullptr) return;
@@ -90,9 +94,11 @@ void CheckBias(const Epilogue& e, int64_t m, int64_t n) {
   }
 }
 
+}  // namespace
+
 // Runs the matmul with the fused epilogue; the trailing RmsNorm (if any) reads C.
 void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, const AccelHipQuantPlane* bq, float* c,
-               int64_t m, int64_t k, int64_t n, const Epilogue& epi) {
+               int64_t m, int64_t k, int64_t n, const Epilogue& epi, bool stage_weights) {
   Context& ctx = Ctx();
   if (m * n == 0) return;
   CheckBias(epi, m, n);
@@ -126,8 +132,8 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
     if (ctx.exact_products) {
       LaunchExactMatmul(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream);
     } else if (q8 && m <= 16) {
-      if (GemvWantsGroups(m, k, view)) view.grouped = StagedGroupTiles(view.q, k, n, ctx.stream);
-      else if (m <= 4) view.tiled = StagedColumnTiles(view.q, k, n, ctx.stream);
+      if (GemvWantsGroups(m, k, view)) view.grouped = StagedGroupTiles(view.q, k, n, ctx.stream, stage_weights);
+      else if (m <= 4) view.tiled = StagedColumnTiles(view.q, k, n, ctx.stream, stage_weights);
       LaunchGemvQ8(a_f, view, c, m, k, n, main, ctx.stream);
     } else {
       LaunchGemmF32(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream);
@@ -146,7 +152,6 @@ void QuantizedChecks(const float* a, const AccelHipQuantPlane* aq, const float* 
   if (bq != nullptr) CheckPlane(bq, "B");
 }
 
-}  // namespace
 }  // namespace accel_hip
 
 using namespace accel_hip;
@@ -171,7 +176,7 @@ ACCEL_HIP_API int accel_hip_matmul(AccelHipBuffer a, AccelHipBuffer b, AccelHipB
     RequireBytes(b, CheckedBytes(k, n), "MatMul B is out of range");
     RequireBytes(c, CheckedBytes(m, n), "MatMul C is out of range");
     RunMatmul(static_cast<const float*>(a.data), nullptr, static_cast<const float*>(b.data), nullptr,
-              static_cast<float*>(c.data), m, k, n, Epilogue{});
+              static_cast<float*>(c.data), m, k, n, Epilogue{}, true);
     NotePackedCall(k);
     NoteKernelMatmul();
   });
@@ -183,7 +188,7 @@ ACCEL_HIP_API int accel_hip_matmul_fused(const float* a, const float* b, float* 
     if (m < 0 || k < 0 || n < 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "negative matrix dimension");
     if ((m * n > 0 && c == nullptr) || (m * k > 0 && a == nullptr) || (k * n > 0 && b == nullptr))
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "MatMul operand is missing");
-    RunMatmul(a, nullptr, b, nullptr, c, m, k, n, ToEpilogue(epilogue));
+    RunMatmul(a, nullptr, b, nullptr, c, m, k, n, ToEpilogue(epilogue), true);
     NotePackedCall(k);
     NoteKernelMatmul();
   });
@@ -195,7 +200,7 @@ ACCEL_HIP_API int accel_hip_matmul_quantized(const float* a, const AccelHipQuant
                                              int64_t n) {
   return Guard([&] {
     QuantizedChecks(a, a_quant, b, b_quant, c, m, k, n);
-    RunMatmul(a, a_quant, b, b_quant, c, m, k, n, Epilogue{});
+    RunMatmul(a, a_quant, b, b_quant, c, m, k, n, Epilogue{}, true);
     NotePackedCall(k);
     NoteKernelMatmul();
   });
@@ -206,7 +211,7 @@ ACCEL_HIP_API int accel_hip_matmul_quantized_fused(const float* a, const AccelHi
                                                    int64_t n, const AccelHipEpilogue* epilogue) {
   return Guard([&] {
     QuantizedChecks(a, a_quant, b, b_quant, c, m, k, n);
-    RunMatmul(a, a_quant, b, b_quant, c, m, k, n, ToEpilogue(epilogue));
+    RunMatmul(a, a_quant, b, b_quant, c, m, k, n, ToEpilogue(epilogue), true);
     NotePackedCall(k);
     NoteKernelMatmul();
   });
@@ -263,6 +268,7 @@ ACCEL_HIP_API int accel_hip_embedding(AccelHipBuffer ids, int64_t id_offset, Acc
     RequireBytes(out, CheckedBytes(seq, hidden), "Embedding output is out of range");
     if (seq == 0 || hidden == 0) return;
     Context& ctx = Ctx();
+    RefuseInCapture("Embedding (it reads its range flag back)");
     int32_t* bad = static_cast<int32_t*>(Temp(kTempFlags, 64));
     Check(hipMemsetAsync(bad, 0, sizeof(int32_t), ctx.stream), "hipMemsetAsync");
     NoteDeviceWrite(out.data, CheckedBytes(seq, hidden));
@@ -285,6 +291,7 @@ ACCEL_HIP_API int accel_hip_embedding_q8(AccelHipBuffer ids, int64_t id_offset, 
     if (table == nullptr || row_scale == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Embedding table is out of range");
     if (seq == 0 || hidden == 0) return;
     Context& ctx = Ctx();
+    RefuseInCapture("Embedding (it reads its range flag back)");
     int32_t* bad = static_cast<int32_t*>(Temp(kTempFlags, 64));
     Check(hipMemsetAsync(bad, 0, sizeof(int32_t), ctx.stream), "hipMemsetAsync");
     NoteDeviceWrite(out.data, CheckedBytes(seq, hidden));
@@ -392,8 +399,9 @@ ACCEL_HIP_API int accel_hip_sample_token(AccelHipBuffer logits, AccelHipBuffer c
     RequireBytes(logits, CheckedBytes(vocab, 1), "SampleToken logits are out of range");
     RequireBytes(chosen_ids, CheckedIntBytes(CheckedSpan(chosen_index, 1)), "SampleToken ids are out of range");
     Context& ctx = Ctx();
-    uint32_t* word = static_cast<uint32_t*>(Temp(kTempFlags, 64)) + 4;
     const bool draw = temperature > 0.f;
+    if (draw) RefuseInCapture("SampleToken with temperature > 0 (its rng state makes a host round trip)");
+    uint32_t* word = static_cast<uint32_t*>(Temp(kTempFlags, 64)) + 4;
     if (draw) Check(hipMemcpyAsync(word, rng_state, sizeof(uint32_t), hipMemcpyHostToDevice, ctx.stream), "hipMemcpyAsync");
     if (draw) Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
     NoteDeviceWrite(static_cast<int32_t*>(chosen_ids.data) + chosen_index, sizeof(int32_t));

@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "accel_hip.h"
 
@@ -35,13 +36,54 @@ struct Context {
 
 // Initialises GPU 0 and the stream on first use.
 Context& Ctx();
-// Ensures workspace >= bytes; returns the context.
-Context& Scratch(size_t bytes);
+// True while the library stream is capturing a HIP graph.
+bool Capturing();
+// Fails with ACCEL_HIP_RUNTIME_ERROR while the library stream is capturing: `what` allocates,
+// frees, synchronizes or writes with a memset, none of which a captured graph may hold.
+void RefuseInCapture(const char* what);
+// Split-K workspace of at least `bytes` (one per call: a later request may return the same
+// memory). Grown on demand outside a capture; inside one it must already be large enough.
+void* Workspace(size_t bytes);
 // Library-owned device temporaries, one per purpose, grown on demand (the stream is
 // drained before a buffer is replaced; a new buffer starts zeroed). Distinct from the
 // split-K workspace. kTempArrivals holds counters that every kernel using them leaves zero.
 enum TempSlot { kTempDequantA = 0, kTempDequantB = 1, kTempFlags = 2, kTempArrivals = 3, kTempCount = 4 };
 void* Temp(TempSlot slot, size_t bytes);
+// Bumped whenever the split-K workspace or a temporary buffer is replaced. A graph captured
+// under an older value may point into a replaced block: accel_hip_graph_launch refuses it.
+uint64_t Generation();
+void BumpGeneration();
+// Whether a handle from accel_hip_capture_end may still be launched: no workspace or temporary
+// replaced and no staged weight copy its capture read dropped since then.
+bool GraphIsCurrent(const void* graph_exec);
+// Device memory that kernels already queued (or a captured graph) may still read: freed at
+// the next point where the stream can be drained (ReleasePending), never inside a capture or
+// a no-allocation call.
+void DeferFree(void* ptr);
+void ReleasePending();
+
+// A fixed block of device memory that serves Workspace() and Temp() requests for the calls
+// made while it is installed on this thread (a bump allocator, reset per install), instead of
+// the library's growable buffers: used by the entry point that must not allocate. A request
+// that does not fit fails with ACCEL_HIP_INVALID_ARGUMENT; an arrival-counter request is
+// zeroed with a fill kernel on the library stream.
+struct Arena {
+  char* base = nullptr;
+  size_t bytes = 0;
+  size_t used = 0;
+};
+class ScopedArena {
+ public:
+  explicit ScopedArena(Arena* arena);
+  ~ScopedArena();
+  ScopedArena(const ScopedArena&) = delete;
+  ScopedArena& operator=(const ScopedArena&) = delete;
+
+ private:
+  Arena* previous_;
+};
+// The arena installed on this thread, or nullptr.
+Arena* CurrentArena();
 
 // Stats of include/accel/runtime.h (AcceleratorStats) and the packed-GEMM probes.
 void NoteKernelMatmul();
@@ -74,13 +116,22 @@ inline size_t StagedTileBytes(int64_t k, int64_t n) {
          static_cast<size_t>(kGemvTileCols);
 }
 // The staged copy of the [k, n] int8 matrix at q, built on first use; nullptr when q is not
-// inside a live allocation of this library (then the raw layout is read).
-const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);
-// Incremented whenever a staged copy is freed: a HIP graph that captured kernels reading
-// staged copies is stale once this has moved.
-uint64_t StagingEpoch();
+// inside a live allocation of this library (then the raw layout is read). With `create`
+// false an existing copy is returned and none is built (no allocation). Building one inside
+// a graph capture fails with ACCEL_HIP_RUNTIME_ERROR.
+const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create = true);
+// The staged copies read by the calls recorded into a HIP graph: BeginStagedUses at the start
+// of a capture, EndStagedUses at its end. StagedUsesLive is false once one of them has been
+// dropped (the graph would read freed memory).
+struct StagedUses {
+  uint64_t drops = 0;  // copies dropped before the capture ended
+  std::vector<uint64_t> serials;
+};
+void BeginStagedUses();
+StagedUses EndStagedUses();
+bool StagedUsesLive(const StagedUses& uses);
 // Every write into device memory through this library calls this for the written range;
-// staged copies of that allocation are dropped.
+// staged copies of that allocation are dropped (their memory is freed later, DeferFree).
 void NoteDeviceWrite(const void* ptr, size_t bytes);
 // Heap hooks (context.cc): the allocation containing ptr; false if none.
 bool FindAllocation(const void* ptr, uint64_t* id, const char** base, size_t* bytes);
@@ -99,7 +150,7 @@ inline size_t StagedGroupBytes(int64_t k, int64_t n) {
 }
 // The staged group-interleaved copy of the [k, n] int8 matrix at q (k % kGemvGroupRows == 0),
 // built on first use; nullptr when q is not inside a live allocation of this library.
-const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream);
+const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create = true);
 void LaunchTileGroups(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
 // Whether LaunchGemvQ8 takes an m-row product with this k and weight view from the
 // group-interleaved copy (the caller stages that copy instead of the 8-column tiles).
@@ -133,6 +184,17 @@ struct Epilogue {
            rms_weight == nullptr;
   }
 };
+
+// ---- matmul dispatch shared by the C-ABI entry points (capi.cc) ------------------------
+Epilogue ToEpilogue(const AccelHipEpilogue* e);
+// The argument checks of accel::MatMulQuantized (src/sim_device.cc:541-548).
+void QuantizedChecks(const float* a, const AccelHipQuantPlane* aq, const float* b, const AccelHipQuantPlane* bq,
+                     float* c, int64_t m, int64_t k, int64_t n);
+// C = A @ B with the fused epilogue, then the epilogue's RmsNorm pass (if any). With
+// stage_weights false a GEMV only reads a staged weight copy that already exists and builds
+// none (it reads W in place instead): no device memory is allocated.
+void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, const AccelHipQuantPlane* bq, float* c,
+               int64_t m, int64_t k, int64_t n, const Epilogue& epi, bool stage_weights);
 
 // ---- kernel launchers (defined in *.hip) ----------------------------------------------
 

@@ -50,6 +50,15 @@ std::mutex g_scratch_mu;
 constexpr int kEventSlots = 8;
 hipEvent_t g_events[kEventSlots];
 
+// What accel_hip_capture_end hands out: the executable graph, the Generation() at the start
+// of its capture and the staged weight copies its kernels read.
+struct GraphHandle {
+  hipGraphExec_t exec;
+  uint64_t generation;
+  StagedUses staged;
+};
+uint64_t g_capture_generation = 0;
+
 size_t BlockSize(size_t bytes) {
   const size_t store = bytes == 0 ? 1 : bytes;
   return (store + 255) & ~size_t(255);
@@ -106,34 +115,117 @@ Context& Ctx() {
   return g_ctx;
 }
 
-// Workspaces only grow, and a replaced block is kept, not freed: a HIP graph captured before
-// the growth still holds the old address and may be replayed. Each growth at least doubles,
-// so the kept blocks add up to less than the current one.
-std::vector<void*> g_retired;
+bool Capturing() {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  Check(hipStreamIsCapturing(Ctx().stream, &status), "hipStreamIsCapturing");
+  return status != hipStreamCaptureStatusNone;
+}
 
-Context& Scratch(size_t bytes) {
+void RefuseInCapture(const char* what) {
+  if (Capturing())
+    Fail(ACCEL_HIP_RUNTIME_ERROR, std::string(what) +
+                                      " cannot run while a HIP graph is being captured: it allocates, frees, "
+                                      "synchronizes or writes with a memset; run it once before capturing");
+}
+
+namespace {
+std::atomic<uint64_t> g_generation{1};
+std::mutex g_pending_mu;
+// Reserved up front so that DeferFree does not allocate host memory in the usual case.
+std::vector<void*> g_pending = [] {
+  std::vector<void*> v;
+  v.reserve(256);
+  return v;
+}();
+thread_local Arena* g_arena = nullptr;
+
+// Serves a request from the installed arena (256-byte aligned), or returns nullptr when none.
+void* FromArena(size_t bytes, const char* what) {
+  Arena* arena = g_arena;
+  if (arena == nullptr) return nullptr;
+  const size_t start = (arena->used + 255) & ~size_t(255);
+  if (start > arena->bytes || bytes > arena->bytes - start)
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, std::string(what) + " needs " + std::to_string(bytes) +
+                                         " bytes, more than the no-allocation scratch has left (" +
+                                         std::to_string(arena->bytes - std::min(start, arena->bytes)) + " of " +
+                                         std::to_string(arena->bytes) + " bytes)");
+  arena->used = start + bytes;
+  return arena->base + start;
+}
+}  // namespace
+
+uint64_t Generation() { return g_generation.load(); }
+void BumpGeneration() { g_generation.fetch_add(1); }
+
+bool GraphIsCurrent(const void* graph_exec) {
+  const GraphHandle* g = static_cast<const GraphHandle*>(graph_exec);
+  return g != nullptr && g->generation == Generation() && StagedUsesLive(g->staged);
+}
+
+void DeferFree(void* ptr) {
+  if (ptr == nullptr) return;
+  std::lock_guard<std::mutex> lock(g_pending_mu);
+  g_pending.push_back(ptr);
+}
+
+void ReleasePending() {
+  if (g_arena != nullptr) return;
+  std::vector<void*> drop;
+  {
+    std::lock_guard<std::mutex> lock(g_pending_mu);
+    if (g_pending.empty()) return;
+    if (Capturing()) return;
+    drop.swap(g_pending);
+    g_pending.reserve(256);
+  }
+  // Kernels queued before the drop may still read these blocks; captured graphs that point
+  // into them are stale (Generation moved) and are refused at launch.
+  Check(hipStreamSynchronize(Ctx().stream), "hipStreamSynchronize");
+  for (void* p : drop) Check(hipFree(p), "hipFree(deferred)");
+}
+
+ScopedArena::ScopedArena(Arena* arena) : previous_(g_arena) {
+  arena->used = 0;
+  g_arena = arena;
+}
+ScopedArena::~ScopedArena() { g_arena = previous_; }
+Arena* CurrentArena() { return g_arena; }
+
+// Workspaces only grow. A replaced block goes to the deferred frees and the generation moves,
+// so a graph captured before the growth is refused rather than replayed into freed memory.
+void* Workspace(size_t bytes) {
+  if (void* p = FromArena(bytes, "split-K workspace")) return p;
   Context& ctx = Ctx();
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (bytes > ctx.workspace_bytes) {
+    RefuseInCapture("growing the split-K workspace");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
-    if (ctx.workspace != nullptr) g_retired.push_back(ctx.workspace);
+    if (ctx.workspace != nullptr) DeferFree(ctx.workspace);
     ctx.workspace = nullptr;
+    BumpGeneration();
     const size_t grown = std::max(bytes, ctx.workspace_bytes * 2);
     Check(hipMalloc(&ctx.workspace, grown), "hipMalloc(workspace)");
     ctx.workspace_bytes = grown;
   }
-  return ctx;
+  return ctx.workspace;
 }
 
 void* Temp(TempSlot slot, size_t bytes) {
   static void* buffers[kTempCount] = {};
   static size_t sizes[kTempCount] = {};
+  if (void* p = FromArena(bytes, "temporary buffer")) {
+    if (slot == kTempArrivals)  // counters must start at zero: cleared by a kernel, not a memset
+      LaunchFill(static_cast<float*>(p), 0.f, static_cast<int64_t>((bytes + 3) / 4), Ctx().stream);
+    return p;
+  }
   Context& ctx = Ctx();
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (bytes > sizes[slot]) {
+    RefuseInCapture("growing a temporary buffer");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
-    if (buffers[slot] != nullptr) g_retired.push_back(buffers[slot]);
+    if (buffers[slot] != nullptr) DeferFree(buffers[slot]);
     buffers[slot] = nullptr;
+    BumpGeneration();
     const size_t grown = std::max<size_t>(bytes, std::max<size_t>(sizes[slot] * 2, 256));
     Check(hipMalloc(&buffers[slot], grown), "hipMalloc(temp)");
     Check(hipMemset(buffers[slot], 0, grown), "hipMemset(temp)");
@@ -202,6 +294,8 @@ ACCEL_HIP_API int accel_hip_allocate(size_t bytes, AccelHipBuffer* out) {
   return Guard([&] {
     if (out == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "allocate needs an output buffer");
     Context& ctx = Ctx();
+    RefuseInCapture("Allocate");
+    ReleasePending();
     const size_t block = BlockSize(bytes);
     void* ptr = nullptr;
     {
@@ -237,6 +331,7 @@ ACCEL_HIP_API int accel_hip_free(AccelHipBuffer buffer) {
   return Guard([&] {
     if (buffer.data == nullptr) return;
     Context& ctx = Ctx();
+    RefuseInCapture("Free");
     size_t block = 0;
     {
       std::lock_guard<std::mutex> lock(g_heap_mu);
@@ -248,6 +343,7 @@ ACCEL_HIP_API int accel_hip_free(AccelHipBuffer buffer) {
       g_live.fetch_sub(1, std::memory_order_relaxed);
     }
     DropStagedForAllocation(buffer.id);
+    ReleasePending();
     {
       std::lock_guard<std::mutex> lock(g_heap_mu);
       if (g_cached_bytes + block <= kCacheLimit) {
@@ -264,6 +360,8 @@ ACCEL_HIP_API int accel_hip_free(AccelHipBuffer buffer) {
 ACCEL_HIP_API int accel_hip_trim(void) {
   return Guard([] {
     Context& ctx = Ctx();
+    RefuseInCapture("Trim");
+    ReleasePending();
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
     std::lock_guard<std::mutex> lock(g_heap_mu);
     for (auto& kv : g_cache) Check(hipFree(kv.second), "hipFree");
@@ -280,6 +378,7 @@ ACCEL_HIP_API int accel_hip_copy_h2d(AccelHipBuffer dst, const void* src, size_t
     if (src == nullptr || dst.data == nullptr || bytes > dst.bytes)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "invalid host-to-device copy");
     Context& ctx = Ctx();
+    RefuseInCapture("CopyHostToDevice");
     NoteDeviceWrite(dst.data, bytes);
     Check(hipMemcpyAsync(dst.data, src, bytes, hipMemcpyHostToDevice, ctx.stream), "hipMemcpyAsync(H2D)");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
@@ -294,6 +393,7 @@ ACCEL_HIP_API int accel_hip_copy_d2h(void* dst, AccelHipBuffer src, size_t bytes
     if (dst == nullptr || src.data == nullptr || bytes > src.bytes)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "invalid device-to-host copy");
     Context& ctx = Ctx();
+    RefuseInCapture("CopyDeviceToHost");
     Check(hipMemcpyAsync(dst, src.data, bytes, hipMemcpyDeviceToHost, ctx.stream), "hipMemcpyAsync(D2H)");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
     NoteBytesToHost(bytes);
@@ -305,6 +405,7 @@ ACCEL_HIP_API int accel_hip_peek(void* dst, const void* device_src, size_t bytes
     if (bytes == 0) return;
     if (dst == nullptr || device_src == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "invalid peek");
     Context& ctx = Ctx();
+    RefuseInCapture("peek");
     Check(hipMemcpyAsync(dst, device_src, bytes, hipMemcpyDeviceToHost, ctx.stream), "hipMemcpyAsync(peek)");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
   });
@@ -315,6 +416,7 @@ ACCEL_HIP_API int accel_hip_poke(void* device_dst, const void* src, size_t bytes
     if (bytes == 0) return;
     if (src == nullptr || device_dst == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "invalid poke");
     Context& ctx = Ctx();
+    RefuseInCapture("poke");
     NoteDeviceWrite(device_dst, bytes);
     Check(hipMemcpyAsync(device_dst, src, bytes, hipMemcpyHostToDevice, ctx.stream), "hipMemcpyAsync(poke)");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
@@ -383,20 +485,29 @@ ACCEL_HIP_API int accel_hip_event_record(int32_t slot) {
 
 ACCEL_HIP_API int accel_hip_capture_begin(void) {
   return Guard([] {
-    Check(hipStreamBeginCapture(Ctx().stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    Context& ctx = Ctx();
+    if (Capturing()) Fail(ACCEL_HIP_RUNTIME_ERROR, "a HIP graph capture is already in progress");
+    ReleasePending();
+    g_capture_generation = Generation();
+    Check(hipStreamBeginCapture(ctx.stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    BeginStagedUses();
   });
 }
 
 ACCEL_HIP_API int accel_hip_capture_end(void** graph_exec) {
   return Guard([&] {
     if (graph_exec == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "capture_end needs an output");
+    *graph_exec = nullptr;
+    StagedUses staged = EndStagedUses();
     hipGraph_t graph = nullptr;
     Check(hipStreamEndCapture(Ctx().stream, &graph), "hipStreamEndCapture");
     hipGraphExec_t exec = nullptr;
     const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
     Check(st, "hipGraphInstantiate");
-    *graph_exec = exec;
+    // A workspace replaced or a read copy dropped since the capture began (during it too)
+    // makes the graph stale.
+    *graph_exec = new GraphHandle{exec, g_capture_generation, std::move(staged)};
   });
 }
 
@@ -404,14 +515,22 @@ ACCEL_HIP_API int accel_hip_graph_launch(void* graph_exec, int32_t times) {
   return Guard([&] {
     if (graph_exec == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "null graph");
     Context& ctx = Ctx();
-    for (int32_t i = 0; i < times; ++i)
-      Check(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), ctx.stream), "hipGraphLaunch");
+    const GraphHandle* g = static_cast<const GraphHandle*>(graph_exec);
+    if (!GraphIsCurrent(g))
+      Fail(ACCEL_HIP_RUNTIME_ERROR,
+           "stale HIP graph: device memory it points into (a staged weight copy, the split-K workspace or a "
+           "temporary) was replaced or dropped after it was captured; capture it again");
+    for (int32_t i = 0; i < times; ++i) Check(hipGraphLaunch(g->exec, ctx.stream), "hipGraphLaunch");
   });
 }
 
 ACCEL_HIP_API int accel_hip_graph_destroy(void* graph_exec) {
   return Guard([&] {
-    if (graph_exec != nullptr) Check(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+    if (graph_exec == nullptr) return;
+    GraphHandle* g = static_cast<GraphHandle*>(graph_exec);
+    const hipError_t st = hipGraphExecDestroy(g->exec);
+    delete g;
+    Check(st, "hipGraphExecDestroy");
   });
 }
 

@@ -432,8 +432,7 @@ void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
   args.partials = nullptr;
   args.epi = epi;
   if (splits > 1) {
-    Context& ctx = Scratch(static_cast<size_t>(splits * m * n) * sizeof(float));
-    args.partials = static_cast<float*>(ctx.workspace);
+    args.partials = static_cast<float*>(Workspace(static_cast<size_t>(splits * m * n) * sizeof(float)));
   }
   const dim3 grid(static_cast<uint32_t>(tiles_n), static_cast<uint32_t>(tiles_m), static_cast<uint32_t>(splits));
   if (bm == 128) Launch<128, 128>(args, q8, grid, stream);

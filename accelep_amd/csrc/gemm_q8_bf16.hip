@@ -349,7 +349,7 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
   args.k_per_split = kper;
   args.partials = nullptr;
   args.epi = epi;
-  if (splits > 1) args.partials = static_cast<float*>(Scratch(static_cast<size_t>(splits * m * n) * sizeof(float)).workspace);
+  if (splits > 1) args.partials = static_cast<float*>(Workspace(static_cast<size_t>(splits * m * n) * sizeof(float)));
   const dim3 grid(static_cast<uint32_t>(args.tiles_per_xcd * kXcds), static_cast<uint32_t>(splits));
   if (bm == 128) hipLaunchKernelGGL(GemmQ8Bf16Kernel<128>, grid, dim3(kThreads), 0, stream, args);
   else hipLaunchKernelGGL(GemmQ8Bf16Kernel<64>, grid, dim3(kThreads), 0, stream, args);

@@ -1105,8 +1105,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   args.partials = nullptr;
   args.epi = epi;
   if (splits > 1) {
-    Context& ctx = Scratch(static_cast<size_t>(splits * m * n) * sizeof(float));
-    args.partials = static_cast<float*>(ctx.workspace);
+    args.partials = static_cast<float*>(Workspace(static_cast<size_t>(splits * m * n) * sizeof(float)));
   }
   static_assert(kNarrowTile == kGemvTileCols, "staged tiles must match the narrow kernel tile");
   args.tiled = narrow ? b.tiled : nullptr;

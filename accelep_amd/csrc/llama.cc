@@ -123,7 +123,6 @@ struct Model {
   // replayed for every step after it. Dropped when a weight changes or the product mode does.
   void* decode_graph = nullptr;
   bool decode_graph_exact = false;
-  uint64_t decode_graph_epoch = 0;
   bool decode_warm = false;
   // Decode-row fusions (accel_llama_set_fused_inputs): bit 0, RMSNorm and SiLU*up inside the
   // next GEMV; bit 1, RoPE + KV append + attention + combine as one kernel.
@@ -280,7 +279,7 @@ struct Model {
   // captures it into a graph, and later calls replay the graph.
   void DecodeStep(int32_t* state) {
     const bool exact = Ctx().exact_products;
-    if (decode_graph != nullptr && (decode_graph_exact != exact || decode_graph_epoch != StagingEpoch()))
+    if (decode_graph != nullptr && (decode_graph_exact != exact || !GraphIsCurrent(decode_graph)))
       DropDecodeGraph();
     // ACCEL_LLAMA_EAGER=1 launches every step directly (a profiler then sees each dispatch).
     static const bool eager = [] {
@@ -306,7 +305,6 @@ struct Model {
       }
       if (accel_hip_capture_end(&decode_graph) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       decode_graph_exact = exact;
-      decode_graph_epoch = StagingEpoch();
     }
     if (accel_hip_graph_launch(decode_graph, 1) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
   }
@@ -456,17 +454,22 @@ void UploadPart(const Part& p, bool int8, const void* block, const float* scale)
   }
   const size_t elem = int8 ? 1 : sizeof(float);
   char* base = int8 ? w.q.as<char>() : w.f.as<char>();
-  Check(hipMemcpy2D(base + p.col0 * elem, static_cast<size_t>(p.total) * elem, block, static_cast<size_t>(p.width) * elem,
-                    static_cast<size_t>(p.width) * elem, static_cast<size_t>(p.in), hipMemcpyHostToDevice),
-        "hipMemcpy2D");
-  NoteBytesToDevice(static_cast<size_t>(p.in * p.width) * elem);
+  // On the library stream, behind the allocation's zero-fill (a stream-ordered memset there):
+  // a copy on another stream could land first and be zeroed over.
+  const hipStream_t s = Ctx().stream;
   NoteDeviceWrite(base, static_cast<size_t>(p.in * p.total) * elem);  // drops a staged copy of the old bytes
-  if (int8) {
-    Check(hipMemcpy(w.scale.as<float>() + p.col0, scale, static_cast<size_t>(p.width) * sizeof(float),
-                    hipMemcpyHostToDevice),
-          "hipMemcpy");
-    NoteBytesToDevice(static_cast<size_t>(p.width) * sizeof(float));
-  }
+  Check(hipMemcpy2DAsync(base + p.col0 * elem, static_cast<size_t>(p.total) * elem, block,
+                         static_cast<size_t>(p.width) * elem, static_cast<size_t>(p.width) * elem,
+                         static_cast<size_t>(p.in), hipMemcpyHostToDevice, s),
+        "hipMemcpy2DAsync");
+  if (int8)
+    Check(hipMemcpyAsync(w.scale.as<float>() + p.col0, scale, static_cast<size_t>(p.width) * sizeof(float),
+                         hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync");
+  // The host blocks may be temporaries of the caller: wait until they have been read.
+  Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  NoteBytesToDevice(static_cast<size_t>(p.in * p.width) * elem);
+  if (int8) NoteBytesToDevice(static_cast<size_t>(p.width) * sizeof(float));
   w.filled |= 1u << p.index;
 }
 

@@ -10,13 +10,18 @@
 //
 // A copy is keyed by (allocation id, byte offset, k, n) and dropped when its allocation is
 // freed or written through this library (host-to-device copies, pokes, kernel outputs).
-// Device memory is only writable through this library, so a copy can never go stale.
+// Device memory is only writable through this library, so a copy can never go stale. A
+// dropped copy's memory is freed later (DeferFree) and the generation moves, so a HIP graph
+// that captured kernels reading it is refused instead of replayed. A copy is never built
+// inside a graph capture: the build allocates and would only be recorded, not run.
 #include <atomic>
 #include <cstring>
 #include <list>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <unordered_set>
+#include <vector>
 
 #include "common.h"
 #include "host_util.h"
@@ -40,6 +45,7 @@ struct Entry {
   int8_t* data;
   size_t bytes;
   uint64_t last_use;
+  uint64_t serial;  // unique per built copy
 };
 
 std::mutex g_mu;
@@ -47,15 +53,21 @@ std::map<Key, Entry> g_staged;
 size_t g_staged_bytes = 0;
 uint64_t g_tick = 0;
 std::atomic<bool> g_any{false};  // fast path for writes when nothing is staged
-std::atomic<uint64_t> g_epoch{0};  // counts dropped copies (a captured graph may hold one)
 constexpr size_t kStagedLimit = size_t(64) << 30;
+uint64_t g_next_serial = 1;
+std::unordered_set<uint64_t> g_live_serials;
+std::atomic<uint64_t> g_drops{0};
+// Serials of the copies that kernels recorded during the current graph capture read.
+std::atomic<bool> g_recording{false};
+std::vector<uint64_t> g_recorded;
 
 void FreeEntry(Entry& e) {
-  // A kernel may still be reading the copy: drain the stream first.
-  Check(hipStreamSynchronize(Ctx().stream), "hipStreamSynchronize");
-  Check(hipFree(e.data), "hipFree(staged)");
+  // Kernels already queued (or a captured graph) may still read the copy: it is freed once
+  // the stream has been drained, and graphs whose capture read it are refused at launch.
+  DeferFree(e.data);
   g_staged_bytes -= e.bytes;
-  g_epoch.fetch_add(1);
+  g_live_serials.erase(e.serial);
+  g_drops.fetch_add(1);
 }
 
 void EvictFor(size_t bytes) {
@@ -68,7 +80,7 @@ void EvictFor(size_t bytes) {
   }
 }
 
-const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStream_t stream) {
+const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStream_t stream, bool create) {
   if (k <= 0 || n <= 0) return nullptr;
   uint64_t id = 0;
   const char* base = nullptr;
@@ -82,15 +94,21 @@ const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStrea
   auto it = g_staged.find(key);
   if (it != g_staged.end()) {
     it->second.last_use = ++g_tick;
+    if (g_recording.load(std::memory_order_relaxed)) g_recorded.push_back(it->second.serial);
     return it->second.data;
   }
+  if (!create) return nullptr;
+  RefuseInCapture("staging an int8 weight copy for the GEMV (its first use)");
+  ReleasePending();
   const size_t bytes = layout == kLayoutGroups ? StagedGroupBytes(k, n) : StagedTileBytes(k, n);
   EvictFor(bytes);
   int8_t* dst = nullptr;
   if (hipMalloc(reinterpret_cast<void**>(&dst), bytes) != hipSuccess) return nullptr;  // fall back to raw
   if (layout == kLayoutGroups) LaunchTileGroups(q, k, n, dst, stream);
   else LaunchTileColumns(q, k, n, dst, stream);
-  g_staged.emplace(key, Entry{dst, bytes, ++g_tick});
+  const uint64_t serial = g_next_serial++;
+  g_staged.emplace(key, Entry{dst, bytes, ++g_tick, serial});
+  g_live_serials.insert(serial);
   g_staged_bytes += bytes;
   g_any.store(true);
   return dst;
@@ -98,16 +116,37 @@ const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStrea
 
 }  // namespace
 
-const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream) {
-  return Staged(q, k, n, kLayoutTiles, stream);
+const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
+  return Staged(q, k, n, kLayoutTiles, stream, create);
 }
 
-const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream) {
+const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
   if (k % kGemvGroupRows != 0) return nullptr;
-  return Staged(q, k, n, kLayoutGroups, stream);
+  return Staged(q, k, n, kLayoutGroups, stream, create);
 }
 
-uint64_t StagingEpoch() { return g_epoch.load(); }
+void BeginStagedUses() {
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_recorded.clear();
+  g_recording.store(true);
+}
+
+StagedUses EndStagedUses() {
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_recording.store(false);
+  StagedUses uses;
+  uses.drops = g_drops.load();
+  uses.serials.swap(g_recorded);
+  return uses;
+}
+
+bool StagedUsesLive(const StagedUses& uses) {
+  if (uses.drops == g_drops.load()) return true;  // nothing dropped since the capture ended
+  std::lock_guard<std::mutex> lock(g_mu);
+  for (uint64_t serial : uses.serials)
+    if (g_live_serials.count(serial) == 0) return false;
+  return true;
+}
 
 void NoteDeviceWrite(const void* ptr, size_t bytes) {
   if (!g_any.load() || ptr == nullptr) return;

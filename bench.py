@@ -110,16 +110,18 @@ class Hip:
 GRAPHS = True  # --no-graph: launch every step directly (profiler counter runs see each dispatch)
 
 
-def timed_steps(hip, step, steps, warmup, period=200):
+def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
     """Warms up, captures the timed calls into graphs of up to `period` steps, times exactly `steps`.
 
-    `period` is a multiple of the weight-copy rotation, so step i always reads copy i % 8 and
-    a replay never restarts on a copy that is still cached. Inside a graph consecutive kernels
-    start back to back; graphs of a few hundred nodes keep the per-launch queue gap off the
-    average, so the event-timed step matches the profiler's per-kernel duration."""
-    # At least one call before capturing: first use may grow the split-K workspace or stage
-    # the weight tiles, which synchronizes and therefore cannot happen inside a capture.
-    for i in range(max(warmup, 1)):
+    Step i reads weight copy i % rotation. The warm-up calls every copy at least once, so
+    each is staged (the GEMV's first use of a weight builds its tiled copy, which the library
+    refuses inside a capture) and the workspaces have their final size before anything is
+    captured. The graph period is a whole number of rotations, so every replay walks the
+    copies in the same order and a copy is never read again before the other copies
+    (> 256 MB) have streamed through the cache. Inside a graph consecutive kernels start back
+    to back; graphs of a few hundred nodes keep the per-launch queue gap off the average, so
+    the event-timed step matches the profiler's per-kernel duration."""
+    for i in range(max(warmup, rotation, 1)):
         step(i)
     hip.sync()
     if not GRAPHS:
@@ -129,6 +131,8 @@ def timed_steps(hip, step, steps, warmup, period=200):
         hip.check(hip.L.accel_hip_event_record(1))
         return hip.L.accel_hip_event_elapsed_ms(0, 1)
     period = min(period, steps)
+    if period > rotation:
+        period -= period % rotation
     full = hip.graph(step, period)
     rest = steps % period
     tail = hip.graph(step, rest) if rest else None
@@ -155,7 +159,7 @@ def bench_gemv(hip, m, steps, warmup, copies, rng):
         hip.check(hip.L.accel_hip_matmul_quantized(x.ptr, None, None, C.byref(planes[i % copies]), out.ptr, m, K_DIM,
                                                    N_DIM))
 
-    ms = timed_steps(hip, step, steps, warmup, period=25 * copies)
+    ms = timed_steps(hip, step, steps, warmup, period=25 * copies, rotation=copies)
     per = ms / steps
     return per, gemv_bytes(m) / (per * 1e-3) / 1e9
 
@@ -210,12 +214,47 @@ def bench_prefill(hip, steps, warmup, rng):
 
 SMOL = dict(vocab=49152, hidden=576, layers=30, heads=9, kv_heads=3, intermediate=1536, context=640, eps=1e-5,
             rope_theta=100000.0)
+# Bytes one decode token reads at least once: int8 layer weights 106,168,320 + their scales
+# 622,080 + int8 LM head 28,311,552 + norms 140,544 + the K/V rows of 30 layers at the mean
+# position of a 512 + 128 generation (46,080 B per position, 576 positions on average).
+LLAMA_DECODE_BYTES = 106_168_320 + 622_080 + 28_311_552 + 140_544 + 46_080 * 576
+
+
+def llama_q8_weights(cfg, rng):
+    """SmolLM2-135M-shape random-init weights in Hugging Face layout ([out, in] matrices):
+    every linear weight and the tied embedding / LM head ~ N(0, 0.02), quantized per output row
+    (s = max|w| / 127, q = rint(w / s)); norm weights ~ N(1, 0.1). Yields (kind, layer, q, s)
+    for the int8 matrices and (kind, layer, w, None) for the norms."""
+    H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
+    hd = H // cfg["heads"]
+
+    def q8(rows, cols):
+        w = (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+        s = (np.abs(w).max(axis=1) / np.float32(127)).astype(np.float32)
+        s[s == 0] = 1
+        return np.rint(w / s[:, None]).clip(-127, 127).astype(np.int8), s
+
+    def norm():
+        return (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+
+    emb_q, emb_s = q8(V, H)
+    yield 1, -1, emb_q, emb_s
+    yield 3, -1, emb_q, emb_s  # LM head tied to the embedding
+    yield 2, -1, norm(), None
+    shapes = {6: (cfg["heads"] * hd, H), 7: (cfg["kv_heads"] * hd, H), 8: (cfg["kv_heads"] * hd, H),
+              9: (H, cfg["heads"] * hd), 10: (I, H), 11: (I, H), 12: (H, I)}
+    for layer in range(cfg["layers"]):
+        yield 4, layer, norm(), None
+        yield 5, layer, norm(), None
+        for kind, (rows, cols) in shapes.items():
+            q, sc = q8(rows, cols)
+            yield kind, layer, q, sc
 
 
 def bench_llama(hip, rng, reps=3):
-    """SmolLM2-135M-shape Llama on the GPU (accel_llama_*): random int8 weights with per-row
-    scales, 512 prompt ids, greedy. Prefill = generate with one new token; decode = the extra
-    time of 128 more tokens. Best of `reps`."""
+    """SmolLM2-135M-shape Llama on the GPU (accel_llama_*): the int8 weights of
+    llama_q8_weights, 512 random prompt ids, 128 greedy tokens. Prefill = generate with one
+    new token; decode = the extra time of 128 more tokens. Best of `reps`."""
     from accelep_amd.capi import F32P, I8P, I32P, LlamaConfig
 
     L = hip.L
@@ -223,30 +262,16 @@ def bench_llama(hip, rng, reps=3):
     h = L.accel_llama_create(C.byref(LlamaConfig(**cfg)))
     if not h:
         raise RuntimeError(L.accel_llama_last_error().decode())
-    H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
-    hd = H // cfg["heads"]
-    shapes = {6: (cfg["heads"] * hd, H), 7: (cfg["kv_heads"] * hd, H), 8: (cfg["kv_heads"] * hd, H),
-              9: (H, cfg["heads"] * hd), 10: (I, H), 11: (I, H), 12: (H, I)}
-
-    def q8(kind, layer, rows, cols):
-        q = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
-        s = np.full(rows, 0.02 / 127 * 3, np.float32)
-        assert L.accel_llama_weight_q8(h, kind, layer, q.ctypes.data_as(I8P), s.ctypes.data_as(F32P), rows,
-                                       cols) == 0, L.accel_llama_last_error()
-
-    def norm(kind, layer):
-        w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
-        assert L.accel_llama_weight(h, kind, layer, w.ctypes.data_as(F32P), H, 1) == 0
-
+    V = cfg["vocab"]
     try:
-        q8(1, -1, V, H)
-        q8(3, -1, V, H)
-        norm(2, -1)
-        for layer in range(cfg["layers"]):
-            norm(4, layer)
-            norm(5, layer)
-            for kind, (rows, cols) in shapes.items():
-                q8(kind, layer, rows, cols)
+        for kind, layer, w, sc in llama_q8_weights(cfg, rng):
+            if sc is None:
+                rc = L.accel_llama_weight(h, kind, layer, w.ctypes.data_as(F32P), w.shape[0], 1)
+            else:
+                rc = L.accel_llama_weight_q8(h, kind, layer, w.ctypes.data_as(I8P), sc.ctypes.data_as(F32P),
+                                             w.shape[0], w.shape[1])
+            if rc != 0:
+                raise RuntimeError(L.accel_llama_last_error().decode())
         prompt = rng.integers(0, V, size=512).astype(np.int32)
         out = np.zeros(129, np.int32)
         count = C.c_int32()
@@ -260,14 +285,17 @@ def bench_llama(hip, rng, reps=3):
                 raise RuntimeError(L.accel_llama_last_error().decode())
             return dt
 
-        generate(129)  # warm-up: staging of the int8 weights, workspaces
+        generate(129)  # warm-up: staging of the int8 weights, workspaces, the decode graph
         pre = min(generate(1) for _ in range(reps))
         full = min(generate(129) for _ in range(reps))
         decode = max(full - pre, 1e-9)
         return {"prefill_ms": round(pre * 1e3, 2), "prefill_tok_s": round(512 / pre, 1),
                 "decode_ms_per_token": round(decode / 128 * 1e3, 4), "decode_tok_s": round(128 / decode, 1),
+                "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / LLAMA_DECODE_BYTES, 1),
+                "decode_roofline_frac": round((128 / decode) / (HBM_PEAK_GBS * 1e9 / LLAMA_DECODE_BYTES), 4),
                 "config": "SmolLM2-135M shape (30 layers, hidden 576, 9/3 heads, inter 1536, vocab 49152), "
-                          "int8 weights, 512 prompt ids, 128 greedy tokens, wall clock, best of 3"}
+                          "linear weights and tied embedding/LM head N(0,0.02) quantized to int8 per output row, "
+                          "norms N(1,0.1), 512 random prompt ids, 128 greedy tokens, wall clock, best of 3"}
     finally:
         L.accel_llama_destroy(h)
 
@@ -284,8 +312,43 @@ def calibrate_traffic(hip):
     src.free()
 
 
-def cpu_baseline(rng):
-    """The reference's MatMulQuantized (compiled AccelEP sources) on the M=1 headline workload."""
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+class OneCore:
+    """Pins the calling thread to one CPU of its current set for the CPU legs (the reference's
+    SimDevice is single-threaded), in-process: sched_setaffinity on this thread, restored on
+    exit. The GPU runtime's own threads keep their affinity."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        self.cpu = min(self.saved)
+        os.sched_setaffinity(0, {self.cpu})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+
+
+def _median_time(fn, runs):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def cpu_baseline(rng, runs=3):
+    """The reference's MatMulQuantized (compiled AccelEP sources) on the M=1 headline workload,
+    pinned to one core; median of `runs` after one warm-up call."""
     sys.path.insert(0, str(ROOT / "tests"))
     from oracle_ctypes import make_plane, oracle, reference
 
@@ -296,12 +359,9 @@ def cpu_baseline(rng):
     s = rng.uniform(1e-3, 1e-2, size=N_DIM).astype(np.float32)
     a = rng.standard_normal((1, K_DIM)).astype(np.float32)
     plane, keep = make_plane(q, s, None, [K_DIM, N_DIM], 1)
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
+    with OneCore() as core:
         impl.matmul_quantized(a, None, None, plane, 1, K_DIM, N_DIM)
-        times.append(time.perf_counter() - t0)
-    best = min(times)
+        best = _median_time(lambda: impl.matmul_quantized(a, None, None, plane, 1, K_DIM, N_DIM), runs)
     return {
         "value": round(gemv_bytes(1) / best / 1e9, 4),
         "unit": "GB/s",
@@ -309,9 +369,90 @@ def cpu_baseline(rng):
         "kind": kind,
         "sample": (f"full M=1 workload X[1,4096] @ int8 W[4096,14336] per-column scale, "
                    f"{'AccelEP MatMulQuantized (src/sim_device.cc:541-602) compiled -O2' if ref else 'oracle port'}, "
-                   f"single thread, best of 2 runs: {best:.2f} s/call; host has {os.cpu_count()} logical CPUs"),
+                   f"one thread pinned to CPU {core.cpu} ({cpu_model()}; host has {os.cpu_count()} logical CPUs), "
+                   f"median of {runs} after a warm-up: {best:.2f} s/call"),
         "seconds_per_call": round(best, 3),
     }
+
+
+def cpu_prefill_sample(rng, rows=64, cols=N_DIM // 8):
+    """C4 on the reference path is hours, so it is timed on a block: X[rows,4096] @ int8
+    W[4096,cols] (per-column scale) plus SimRmsNorm of the block's rows, pinned to one core, and
+    extrapolated linearly to 2048 rows and 14336 columns (the reference blocks M by 64 and N by
+    256, so its time is linear in both at these multiples)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ctypes import make_plane, reference
+
+    ref = reference()
+    if ref is None:
+        return None
+    q = rng.integers(-127, 128, size=K_DIM * cols, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, size=cols).astype(np.float32)
+    a = rng.standard_normal((rows, K_DIM)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    plane, keep = make_plane(q, s, None, [K_DIM, cols], 1)
+    with OneCore() as core:
+        def run():
+            c = ref.matmul_quantized(a, None, None, plane, rows, K_DIM, cols)
+            ref.rmsnorm(c, g, rows, cols, 1e-5, 0)
+        t = _median_time(run, 2)
+    scale = (2048 / rows) * (N_DIM / cols)
+    total = t * scale
+    return {"seconds_extrapolated": round(total, 1), "TFLOP/s": round(2 * 2048 * K_DIM * N_DIM / total / 1e12, 6),
+            "cores": 1, "kind": "reference", "extrapolated": True,
+            "sample": (f"AccelEP MatMulQuantized + SimRmsNorm on X[{rows},4096] @ int8 W[4096,{cols}], one thread "
+                       f"pinned to CPU {core.cpu}, median of 2: {t:.2f} s, times {scale:.0f} for the full "
+                       f"2048 x 4096 x 14336 workload (extrapolated)")}
+
+
+def cpu_llama_sample(rng, prompt_ids=32, new=16):
+    """C5 on the reference path (accel_llama_* of AccelEP's llama_model.cc through oracle/_ref)
+    on a bounded sample: the SmolLM2-135M shape with the same weight generator (float weights
+    fl(q*s), as the reference takes them), a `prompt_ids`-id prompt and `new` greedy tokens,
+    pinned to one core. Prefill and decode are reported per token; the 512 + 128 workload's
+    decode positions are longer, which adds the attention over ~600 cached rows (~1% of a
+    token's 0.3 GFLOP of weights at this shape)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ctypes import F32P, I32P, LlamaConfig as RefConfig, reference
+
+    ref = reference()
+    if ref is None:
+        return None
+    L = ref.lib
+    cfg = SMOL
+    h = L.accel_llama_create(C.byref(RefConfig(**cfg)))
+    if not h:
+        return None
+    try:
+        for kind, layer, w, sc in llama_q8_weights(cfg, rng):
+            f = w if sc is None else (w.astype(np.float32) * sc[:, None]).astype(np.float32)
+            f = np.ascontiguousarray(f)
+            rows, cols = (f.shape[0], 1) if f.ndim == 1 else f.shape
+            if L.accel_llama_weight(h, kind, layer, f.ctypes.data_as(F32P), rows, cols) != 0:
+                return None
+        prompt = rng.integers(0, cfg["vocab"], size=prompt_ids).astype(np.int32)
+        out = np.zeros(new + 1, np.int32)
+        count = C.c_int32()
+
+        def generate(k):
+            t0 = time.perf_counter()
+            rc = L.accel_llama_generate(h, prompt.ctypes.data_as(I32P), prompt.size, k, -1, 0.0, 0, 0,
+                                        out.ctypes.data_as(I32P), C.byref(count))
+            if rc != 0:
+                raise RuntimeError(L.accel_llama_last_error().decode())
+            return time.perf_counter() - t0
+
+        with OneCore() as core:
+            pre = generate(1)
+            full = generate(new + 1)
+        decode = max(full - pre, 1e-9) / new
+        return {"prefill_tok_s": round(prompt_ids / pre, 2), "decode_s_per_token": round(decode, 4),
+                "decode_tok_s": round(1 / decode, 3), "cores": 1, "kind": "reference",
+                "sample": (f"AccelEP LlamaModel Generate (src/llama_model.cc) compiled -O2, SmolLM2-135M shape, "
+                           f"{prompt_ids}-id prompt ({pre:.2f} s) + {new} greedy tokens ({full - pre:.2f} s), "
+                           f"one thread pinned to CPU {core.cpu}")}
+    finally:
+        L.accel_llama_destroy(h)
 
 
 def main():
@@ -385,13 +526,13 @@ def main():
         per, gbs = bench_gemv(hip, 1, args.steps, args.warmup, 1, rng)
         secondary["gemv_m1_cache_warm"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
                                            "note": "one weight copy, L2/MALL may serve it; not HBM-honest"}
-        steps2 = max(1, args.steps // 4)
+        steps2 = max(10, args.steps // 4)
         per, tf = bench_mlp(hip, steps2, max(1, args.warmup // 4), rng)
         secondary["mlp_fp32"] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
                                  "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "steps": steps2,
                                  "config": "X[256,1024] Gemm1024x4096+bias+gelu, Gemm4096x1024+bias+residual"}
         log(f"mlp fp32: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
-        steps4 = max(1, args.steps // 20)
+        steps4 = max(10, args.steps // 20)
         per, tf = bench_prefill(hip, steps4, max(1, args.warmup // 20), rng)
         secondary["prefill_int8_rmsnorm"] = {
             "ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
@@ -407,9 +548,18 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline (reference MatMulQuantized, 1 thread) ...")
+        log("cpu baseline (reference MatMulQuantized, 1 pinned thread) ...")
         cpu = cpu_baseline(np.random.default_rng(7))
         log(f"cpu baseline: {cpu['value']} GB/s ({cpu['seconds_per_call']} s/call)")
+        if not args.only_headline:
+            pf = cpu_prefill_sample(np.random.default_rng(8))
+            if pf is not None and "prefill_int8_rmsnorm" in secondary:
+                secondary["prefill_int8_rmsnorm"]["cpu_reference"] = pf
+                log(f"cpu prefill (extrapolated): {pf['seconds_extrapolated']} s")
+            ll = cpu_llama_sample(np.random.default_rng(9))
+            if ll is not None and "llama_decode" in secondary:
+                secondary["llama_decode"]["cpu_reference"] = ll
+                log(f"cpu llama: decode {ll['decode_s_per_token']} s/token, prefill {ll['prefill_tok_s']} tok/s")
 
     line = {
         "metric": METRIC,

@@ -8,7 +8,8 @@ is absent (a GPU host without the reference sources).
 
 Run: python tests/golden/make_golden.py               (reference_outputs.npz)
      python tests/golden/make_golden.py --llama-full   (llama_smol_full.npz: the SmolLM2-135M-shape
-                                                       forward, 30 layers, 512 + 128 tokens; minutes)
+                                                       forward, 30 layers, 512 + 128 tokens, greedy
+                                                       and top-k; tens of minutes)
 """
 
 from __future__ import annotations
@@ -33,11 +34,20 @@ def main():
         raise SystemExit("oracle/_ref/libaccel_ref.so is missing: run `make -C oracle` with the reference tree present")
     if "--llama-full" in sys.argv:
         import time
-        case = llama_full_case()
-        t0 = time.time()
-        toks, logits = run_reference_llama(ref, case)
-        np.savez_compressed(HERE / "llama_smol_full.npz", ids=toks, prefill_logits=logits)
-        print(f"wrote {HERE / 'llama_smol_full.npz'}: {toks.size} ids in {time.time() - t0:.0f} s")
+        out = {}
+        for case, prefix in ((llama_full_case(), ""), (llama_full_case(sampled=True), "topk_")):
+            t0 = time.time()
+            toks, logits = run_reference_llama(ref, case)
+            steps, rows, gaps = run_reference_decode_rows(ref, case, toks, DECODE_ROW_STEPS)
+            out[prefix + "ids"] = toks
+            out[prefix + "prefill_logits"] = logits
+            out[prefix + "decode_steps"] = steps
+            out[prefix + "decode_logits"] = rows
+            out[prefix + "top2_gap"] = gaps
+            print(f"{case['name']}: {toks.size} ids ({np.unique(toks).size} distinct), min top-2 gap "
+                  f"{gaps.min():.3g}, {time.time() - t0:.0f} s", flush=True)
+        np.savez_compressed(HERE / "llama_smol_full.npz", **out)
+        print(f"wrote {HERE / 'llama_smol_full.npz'}")
         return
     out = {}
 
@@ -104,6 +114,54 @@ def main():
 
     np.savez_compressed(HERE / "reference_outputs.npz", **out)
     print(f"wrote {len(out)} arrays to {HERE / 'reference_outputs.npz'}")
+
+
+DECODE_ROW_STEPS = (1, 32, 64, 127)
+
+
+def run_reference_decode_rows(ref, case, toks, keep_steps):
+    """Logit rows of decode steps: after the prompt, step t forwards id toks[t - 1] at position
+    len(prompt) + t - 1 and its row chooses toks[t]. The rows of `keep_steps` are stored (each
+    the reference's own bits: the oracle restatement's row, kept only after the reference
+    reports max|ref - row| == 0 at that step), with the top-1 minus top-2 logit gap of every
+    row from the prefill (index 0) to the last decode step."""
+    import ctypes as C
+    from oracle_ctypes import F32P, I32P, LlamaConfig, oracle
+
+    L = ref.lib
+    O = oracle().lib
+    cfg = LlamaConfig(**case["config"])
+    h = L.accel_llama_create(C.byref(cfg))
+    o = O.orc_llama_create(C.byref(cfg))
+    assert h and o
+    vocab = case["config"]["vocab"]
+    try:
+        for (kind, layer, w) in case["weights"]:
+            w = np.ascontiguousarray(w, np.float32)
+            rows, cols = (w.shape[0], 1) if w.ndim == 1 else w.shape
+            assert L.accel_llama_weight(h, kind, layer, w.ctypes.data_as(F32P), rows, cols) == 0
+            assert O.orc_llama_weight(o, kind, layer, w.ctypes.data_as(F32P), rows, cols) == 0
+        prompt = np.ascontiguousarray(case["prompt"], np.int32)
+        row = np.zeros(vocab, np.float32)
+        mx = C.c_float()
+        gaps = np.zeros(toks.size, np.float64)
+        kept = []
+        for t in range(toks.size):
+            ids = prompt if t == 0 else np.ascontiguousarray(toks[t - 1:t], np.int32)
+            assert L.accel_llama_forward_ids(h, ids.ctypes.data_as(I32P), ids.size, 1 if t == 0 else 0) == 0
+            assert O.orc_llama_forward_ids(o, ids.ctypes.data_as(I32P), ids.size, 1 if t == 0 else 0) == 0
+            assert O.orc_llama_logits(o, row.ctypes.data_as(F32P), vocab) == 0
+            top = np.sort(row.astype(np.float64))[-2:]
+            gaps[t] = top[1] - top[0]
+            if t in keep_steps:
+                assert L.accel_llama_logit_max_abs(h, row.ctypes.data_as(F32P), vocab, C.byref(mx)) == 0
+                if mx.value != 0.0:
+                    raise SystemExit(f"{case['name']}: oracle logits of step {t} differ from the reference by {mx.value}")
+                kept.append(row.copy())
+        return np.array(keep_steps, np.int32), np.stack(kept), gaps
+    finally:
+        L.accel_llama_destroy(h)
+        O.orc_llama_destroy(o)
 
 
 def run_reference_llama(ref, case):

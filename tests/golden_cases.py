@@ -241,10 +241,15 @@ def llama_cases():
     return cases
 
 
-def llama_full_case():
-    """The SmolLM2-135M-shape forward: 30 layers, 512 prompt ids, 128 greedy tokens."""
+def llama_full_case(sampled=False):
+    """The SmolLM2-135M-shape forward: 30 layers, 512 prompt ids, 128 tokens, greedy (the
+    configured workload) or top-k sampled (temperature 0.8, top 40, seed 11), whose ids do
+    not settle on a fixed point."""
     cfg = llama_config("smol")
     w, q = llama_weights(cfg, 105)
     prompt = _rng(106).integers(0, cfg["vocab"], size=512).astype(np.int32)
+    if sampled:
+        return dict(name="smol_full_topk", config=cfg, weights=w, quant=q, prompt=prompt, max_new=128, eos=-1,
+                    temperature=0.8, seed=11, top_k=40)
     return dict(name="smol_full_greedy", config=cfg, weights=w, quant=q, prompt=prompt, max_new=128, eos=-1,
                 temperature=0.0, seed=0, top_k=0)

@@ -1,0 +1,184 @@
+"""HIP graph capture through the C-ABI (accel_hip_capture_begin/end, accel_hip_graph_launch):
+what a capture must refuse, and stale graphs.
+
+* A call that would allocate, free, synchronize or memset while the library stream is being
+  captured returns ACCEL_HIP_RUNTIME_ERROR and enqueues nothing: building a staged weight copy
+  (the GEMV's first use of W), growing the split-K workspace, Allocate, the counted copies.
+  The same call made eagerly afterwards gives the correct product (no half-built copy left
+  behind).
+* A graph whose capture read a staged weight copy is refused at launch once that copy has
+  been dropped (W rewritten or freed): the launch returns ACCEL_HIP_RUNTIME_ERROR and the
+  graph is never replayed. A graph that did not read the dropped copy still replays.
+
+No test here replays a graph whose memory was released: every refusal is decided on the host
+before anything is launched.
+"""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from hip_helpers import Buffer, HipError, assert_gamma_bound, check, dequant_host, dev, lib, quant_plane, same_bits
+
+pytestmark = pytest.mark.gpu
+
+RUNTIME_ERROR = 5
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    check(lib().accel_hip_init())
+    yield
+
+
+def _gemv(m, k, n, seed):
+    r = np.random.default_rng(seed)
+    q = r.integers(-127, 128, size=k * n, dtype=np.int8)
+    s = r.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    qd, sd, ad = dev(q), dev(s), dev(a)
+    plane = quant_plane(qd, sd, None, [k, n], 1)
+    out = dev(np.zeros((m, n), np.float32))
+    w = dequant_host(dict(q=q, scale=s, zero=None, shape=[k, n], axis=1, offset=0), k, n)
+    return dict(q=q, s=s, a=a, qd=qd, sd=sd, ad=ad, plane=plane, out=out, w=w, m=m, k=k, n=n)
+
+
+def _call(g):
+    return lib().accel_hip_matmul_quantized(g["ad"].ptr, None, None, C.byref(g["plane"]), g["out"].ptr, g["m"],
+                                            g["k"], g["n"])
+
+
+def _end_capture():
+    handle = C.c_void_p()
+    check(lib().accel_hip_capture_end(C.byref(handle)))
+    return handle
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_capture_refuses_first_use_staging(m):
+    """The first GEMV on a weight builds its staged copy; inside a capture that is refused, and
+    an eager call after the capture (before any replay) computes the right product."""
+    L = lib()
+    g = _gemv(m, 1024, 2048, 10 + m)
+    print(f"capture staging m={m}", flush=True)
+    check(L.accel_hip_capture_begin())
+    try:
+        rc = _call(g)
+        msg = L.accel_hip_last_error().decode()
+    finally:
+        graph = _end_capture()
+        check(L.accel_hip_graph_destroy(graph))
+    assert rc == RUNTIME_ERROR, (rc, msg)
+    assert "captur" in msg and "staging" in msg
+    check(_call(g))
+    assert_gamma_bound(g["out"].numpy(), g["a"], g["w"])
+
+
+def test_capture_refuses_heap_calls_and_workspace_growth():
+    L = lib()
+    target = dev(np.zeros(4, np.float32))
+    host = np.arange(4, dtype=np.float32)
+    check(L.accel_hip_capture_begin())
+    try:
+        b = Buffer()
+        rc_alloc = L.accel_hip_allocate(256, C.byref(b))
+        msg_alloc = L.accel_hip_last_error().decode()
+        rc_copy = L.accel_hip_copy_h2d(target.buffer, host.ctypes.data, host.nbytes)
+        msg_copy = L.accel_hip_last_error().decode()
+    finally:
+        graph = _end_capture()
+        check(L.accel_hip_graph_destroy(graph))
+    assert rc_alloc == RUNTIME_ERROR and "Allocate" in msg_alloc, (rc_alloc, msg_alloc)
+    assert rc_copy == RUNTIME_ERROR and "CopyHostToDevice" in msg_copy, (rc_copy, msg_copy)
+    assert not target.numpy().any()  # the refused copy wrote nothing
+    # A split-K GEMM (64 tiles of 64 x 64, K split 8 ways: 8 MB of partial sums). If no earlier
+    # call grew the workspace that far, the capture refuses to grow it and enqueues nothing;
+    # either way the eager call afterwards gives the product.
+    m, k, n = 64, 8192, 4096
+    r = np.random.default_rng(3)
+    a_h = r.standard_normal((m, k)).astype(np.float32)
+    b_h = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
+    a, bw, c = dev(a_h), dev(b_h), dev(np.zeros((m, n), np.float32))
+    check(L.accel_hip_capture_begin())
+    try:
+        rc = L.accel_hip_matmul_fused(a.ptr, bw.ptr, c.ptr, m, k, n, None)
+        msg = L.accel_hip_last_error().decode()
+    finally:
+        graph = _end_capture()
+        check(L.accel_hip_graph_destroy(graph))
+    if rc != 0:
+        assert rc == RUNTIME_ERROR and "workspace" in msg, (rc, msg)
+    check(L.accel_hip_matmul_fused(a.ptr, bw.ptr, c.ptr, m, k, n, None))
+    assert_gamma_bound(c.numpy(), a_h, b_h)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_graph_refused_after_its_staged_copy_is_dropped(m):
+    """Capture a GEMV that reads W's staged copy; rewrite W (which drops the copy): the launch
+    of the old graph is refused and nothing runs. A second graph over another weight, whose
+    copy was not dropped, still replays with the eager bits. Re-capturing after the rewrite
+    gives the new product."""
+    L = lib()
+    g1 = _gemv(m, 512, 1536, 30 + m)
+    g2 = _gemv(m, 512, 1536, 40 + m)
+    for g in (g1, g2):
+        check(_call(g))  # stages W before the capture
+    want2 = g2["out"].numpy()
+    check(L.accel_hip_capture_begin())
+    try:
+        check(_call(g1))
+    finally:
+        graph1 = _end_capture()
+    check(L.accel_hip_capture_begin())
+    try:
+        check(_call(g2))
+    finally:
+        graph2 = _end_capture()
+    try:
+        check(L.accel_hip_graph_launch(graph1, 1))  # still current
+        assert_gamma_bound(g1["out"].numpy(), g1["a"], g1["w"])
+        q_new = np.random.default_rng(99).integers(-127, 128, size=g1["k"] * g1["n"], dtype=np.int8)
+        g1["qd"].upload(q_new)  # drops the staged copy graph1 reads
+        g1["out"].upload(np.full((m, g1["n"]), 7.0, np.float32))
+        print(f"launching stale graph m={m} (must be refused on the host)", flush=True)
+        rc = L.accel_hip_graph_launch(graph1, 1)
+        msg = L.accel_hip_last_error().decode()
+        assert rc == RUNTIME_ERROR and "stale" in msg, (rc, msg)
+        assert (g1["out"].numpy() == 7.0).all()  # nothing ran
+        g2["out"].upload(np.zeros((m, g2["n"]), np.float32))
+        check(L.accel_hip_graph_launch(graph2, 2))  # its copy is alive
+        same_bits(g2["out"].numpy(), want2)
+        check(L.accel_hip_graph_destroy(graph1))
+        graph1 = None
+        check(_call(g1))  # restages
+        w_new = dequant_host(dict(q=q_new, scale=g1["s"], zero=None, shape=[g1["k"], g1["n"]], axis=1, offset=0),
+                             g1["k"], g1["n"])
+        want1 = g1["out"].numpy()
+        assert_gamma_bound(want1, g1["a"], w_new)
+        check(L.accel_hip_capture_begin())
+        try:
+            check(_call(g1))
+        finally:
+            graph1 = _end_capture()
+        g1["out"].upload(np.zeros((m, g1["n"]), np.float32))
+        check(L.accel_hip_graph_launch(graph1, 1))
+        same_bits(g1["out"].numpy(), want1)
+    finally:
+        if graph1 is not None:
+            check(L.accel_hip_graph_destroy(graph1))
+        check(L.accel_hip_graph_destroy(graph2))
+
+
+def test_capture_inside_capture_is_refused():
+    L = lib()
+    check(L.accel_hip_capture_begin())
+    try:
+        rc = L.accel_hip_capture_begin()
+        msg = L.accel_hip_last_error().decode()
+    finally:
+        graph = _end_capture()
+        check(L.accel_hip_graph_destroy(graph))
+    assert rc == RUNTIME_ERROR and "already" in msg
+    with pytest.raises(HipError):
+        check(L.accel_hip_graph_launch(None, 1))
