@@ -36,6 +36,9 @@ struct Context {
 
 // Initialises GPU 0 and the stream on first use.
 Context& Ctx();
+// Takes the device address of the no-allocation entry point's fixed scratch array on
+// ctx.device (which must be current); called once per device by the library's init.
+void InitNoAllocScratch(const Context& ctx);
 // True while the library stream is capturing a HIP graph.
 bool Capturing();
 // Fails with ACCEL_HIP_RUNTIME_ERROR while the library stream is capturing: `what` allocates,

@@ -93,6 +93,11 @@ void InitOnce() {
       return;
     }
   }
+  try {
+    InitNoAllocScratch(g_ctx);  // with device 0 current
+  } catch (const Error& e) {
+    g_init_error = e;
+  }
 }
 
 }  // namespace

@@ -149,6 +149,19 @@ ACCEL_HIP_API int accel_hip_matmul_fused(const float* a, const float* b, float* 
 ACCEL_HIP_API int accel_hip_matmul_quantized_fused(const float* a, const AccelHipQuantPlane* a_quant, const float* b,
                                                    const AccelHipQuantPlane* b_quant, float* c, int64_t m, int64_t k,
                                                    int64_t n, const AccelHipEpilogue* epilogue);
+/* No counterpart in the reference. accel_hip_matmul_quantized_fused for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same arguments, checks, results and counters. It calls no hipMalloc,
+ * hipFree or other allocating routine: the scratch its kernels need (split-K partial sums,
+ * arrival counters, a dequantized operand for plane layouts the kernels do not index) comes
+ * from one fixed 64 MiB device array per GPU, held until the process ends, and a call whose
+ * scratch would exceed it returns ACCEL_HIP_INVALID_ARGUMENT. A staged GEMV copy of W is read
+ * only if an earlier call built one (otherwise W is read in place). Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU race. */
+ACCEL_HIP_API int accel_hip_matmul_quantized_fused_noalloc(const float* a, const AccelHipQuantPlane* a_quant,
+                                                           const float* b, const AccelHipQuantPlane* b_quant, float* c,
+                                                           int64_t m, int64_t k, int64_t n,
+                                                           const AccelHipEpilogue* epilogue);
 /* Device::Transpose (device.h:84-85; src/sim_device.cc:198-209): dst[j, i] = src[i, j]. */
 ACCEL_HIP_API int accel_hip_transpose(AccelHipBuffer src, AccelHipBuffer dst, int64_t rows, int64_t cols);
 /* Device::GemmEpilogue (device.h:87-92; src/sim_device.cc:211-245). bias may be NULL. */
