@@ -102,6 +102,7 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
   Context& ctx = Ctx();
   if (m * n == 0) return;
   CheckBias(epi, m, n);
+  bool rms_done = false;
   NoteDeviceWrite(c, static_cast<size_t>(m * n) * sizeof(float));
   if (epi.rms_out != nullptr) NoteDeviceWrite(epi.rms_out, static_cast<size_t>(m * n) * sizeof(float));
   if (k == 0) {
@@ -136,10 +137,17 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
       else if (m <= 4) view.tiled = StagedColumnTiles(view.q, k, n, ctx.stream, stage_weights);
       LaunchGemvQ8(a_f, view, c, m, k, n, main, ctx.stream);
     } else {
-      LaunchGemmF32(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream);
+      if (q8 && GemmWantsBf16Image(m, k, n, view)) view.bf16 = StagedBf16Image(view.q, k, n, ctx.stream, stage_weights);
+      RmsRequest rms;
+      rms.weight = epi.rms_weight;
+      rms.eps = epi.rms_eps;
+      rms.out = epi.rms_out;
+      rms_done = LaunchGemmF32(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream,
+                               epi.rms_weight != nullptr ? &rms : nullptr);
     }
   }
-  if (epi.rms_weight != nullptr) LaunchRmsNormRows(c, epi.rms_weight, epi.rms_out, m, n, epi.rms_eps, ctx.stream);
+  if (epi.rms_weight != nullptr && !rms_done)
+    LaunchRmsNormRows(c, epi.rms_weight, epi.rms_out, m, n, epi.rms_eps, ctx.stream);
 }
 
 void QuantizedChecks(const float* a, const AccelHipQuantPlane* aq, const float* b, const AccelHipQuantPlane* bq,

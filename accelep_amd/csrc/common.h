@@ -50,7 +50,15 @@ void* Workspace(size_t bytes);
 // Library-owned device temporaries, one per purpose, grown on demand (the stream is
 // drained before a buffer is replaced; a new buffer starts zeroed). Distinct from the
 // split-K workspace. kTempArrivals holds counters that every kernel using them leaves zero.
-enum TempSlot { kTempDequantA = 0, kTempDequantB = 1, kTempFlags = 2, kTempArrivals = 3, kTempCount = 4 };
+enum TempSlot {
+  kTempDequantA = 0,
+  kTempDequantB = 1,
+  kTempFlags = 2,
+  kTempArrivals = 3,
+  kTempSplitA = 4,   // the bf16 GEMM's hi/mid/lo activation image
+  kTempRowSums = 5,  // per-tile row sums of squares of a GEMM with a fused RMSNorm
+  kTempCount = 6
+};
 void* Temp(TempSlot slot, size_t bytes);
 // Bumped whenever the split-K workspace or a temporary buffer is replaced. A graph captured
 // under an older value may point into a replaced block: accel_hip_graph_launch refuses it.
@@ -87,6 +95,9 @@ class ScopedArena {
 };
 // The arena installed on this thread, or nullptr.
 Arena* CurrentArena();
+// Whether `bytes` more of scratch can be served: always without an arena, else if they fit
+// in what the arena has left.
+bool WorkspaceFits(size_t bytes);
 
 // Stats of include/accel/runtime.h (AcceleratorStats) and the packed-GEMM probes.
 void NoteKernelMatmul();
@@ -107,6 +118,7 @@ struct Q8View {
   int64_t const_index = 0;        // scale/zero index in kScaleConst mode
   const int8_t* tiled = nullptr;  // staged column-tiled copy of q (kGemvTileCols wide), or nullptr
   const int8_t* grouped = nullptr;  // staged group-interleaved copy of q, or nullptr
+  const void* bf16 = nullptr;       // staged bf16 copy in the GEMM's MFMA operand order, or nullptr
 };
 
 // ---- weight staging (staging.cc) --------------------------------------------------------
@@ -155,6 +167,17 @@ inline size_t StagedGroupBytes(int64_t k, int64_t n) {
 // built on first use; nullptr when q is not inside a live allocation of this library.
 const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create = true);
 void LaunchTileGroups(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
+// bf16 copy of a [k, n] int8 matrix (k % 32 == 0) in the operand order of
+// v_mfma_f32_32x32x16_bf16's B operand, for the int8-weight GEMM: 32-column block cb (columns
+// past n zero) and 16-row step s form 1 KB at (cb * k/16 + s) * 1024 bytes, 16 bytes per lane
+// l = the 8 values W[16s + 8(l / 32) + j][32cb + l % 32], j = 0..7, each float(q) exactly.
+inline size_t StagedBf16Bytes(int64_t k, int64_t n) {
+  return static_cast<size_t>((n + 31) / 32) * static_cast<size_t>(k / 16) * 1024;
+}
+const void* StagedBf16Image(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create = true);
+void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream);
+// Whether the int8-weight GEMM runs this product from a staged bf16 copy (the caller stages it).
+bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v);
 // Whether LaunchGemvQ8 takes an m-row product with this k and weight view from the
 // group-interleaved copy (the caller stages that copy instead of the 8-column tiles).
 constexpr int64_t kGemvGroupMinM = 3;
@@ -225,15 +248,27 @@ constexpr int64_t kGemvPrologueMaxK = 4096;
 // kGemvPrologueMaxK.
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
                   hipStream_t stream, const GemvPrologue* prologue = nullptr);
-// C[m, n] = A[m, k] @ B[k, n]; B is fp32 (b) or int8 (bq.q != nullptr). fp32 MFMA.
-void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
-                   const Epilogue& epi, hipStream_t stream);
+// An RMSNormalization of the product's rows (after the epilogue) that a GEMM may take over:
+// out[i, :] = RmsNorm(C[i, :]) with the weight and eps given (SimRmsNorm's arithmetic).
+struct RmsRequest {
+  const float* weight = nullptr;
+  float eps = 0.f;
+  float* out = nullptr;
+};
+// C[m, n] = A[m, k] @ B[k, n]; B is fp32 (b) or int8 (bq.q != nullptr). fp32 MFMA. With rms,
+// returns true when the kernel also produced the normalized rows (the caller runs the pass
+// otherwise).
+bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
+                   const Epilogue& epi, hipStream_t stream, const RmsRequest* rms = nullptr);
 // The int8-weight GEMM on the bf16 matrix cores (exact products, activations split into
 // three bf16 parts): k % 32 == 0, n % 8 == 0, A 16-byte and q 8-byte aligned, per-column or
 // whole-tensor scale, no zero points (a grid of fewer 128 x 128 tiles than CUs splits K).
-// Returns false, launching nothing, otherwise.
+// With b.bf16 (GemmWantsBf16Image) the activations are split once per call into an image
+// the tiles copy as-is, the weight operands come from the staged bf16 copy, and an rms
+// request is served inside (per-tile row sums of squares, then one scaling pass); *rms_done
+// tells whether it was. Returns false, launching nothing, when the conditions do not hold.
 bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
-                      hipStream_t stream);
+                      hipStream_t stream, const RmsRequest* rms = nullptr, bool* rms_done = nullptr);
 // C = A @ B in the reference's order and rounding (one k-ordered chain per output, split
 // products, per-element dequantization); B is fp32 (b) or int8 (bq.q != nullptr).
 void LaunchExactMatmul(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,

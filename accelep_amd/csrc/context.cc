@@ -195,6 +195,12 @@ ScopedArena::ScopedArena(Arena* arena) : previous_(g_arena) {
 }
 ScopedArena::~ScopedArena() { g_arena = previous_; }
 Arena* CurrentArena() { return g_arena; }
+bool WorkspaceFits(size_t bytes) {
+  const Arena* arena = g_arena;
+  if (arena == nullptr) return true;
+  const size_t start = (arena->used + 255) & ~size_t(255);
+  return start <= arena->bytes && bytes <= arena->bytes - start;
+}
 
 // Workspaces only grow. A replaced block goes to the deferred frees and the generation moves,
 // so a graph captured before the growth is refused rather than replayed into freed memory.
@@ -233,7 +239,9 @@ void* Temp(TempSlot slot, size_t bytes) {
     BumpGeneration();
     const size_t grown = std::max<size_t>(bytes, std::max<size_t>(sizes[slot] * 2, 256));
     Check(hipMalloc(&buffers[slot], grown), "hipMalloc(temp)");
-    Check(hipMemset(buffers[slot], 0, grown), "hipMemset(temp)");
+    // On the library stream: a null-stream memset is not ordered against it (the stream is
+    // non-blocking) and could land after a kernel that already wrote the new buffer.
+    Check(hipMemsetAsync(buffers[slot], 0, grown, ctx.stream), "hipMemsetAsync(temp)");
     sizes[slot] = grown;
   }
   return buffers[slot];

@@ -382,12 +382,13 @@ void Launch(const GemmArgs& args, bool q8, dim3 grid, hipStream_t stream) {
 
 }  // namespace
 
-void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
-                   const Epilogue& epi, hipStream_t stream) {
+bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
+                   const Epilogue& epi, hipStream_t stream, const RmsRequest* rms) {
   if (m < 1 || n < 1 || k < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMM shape out of range");
   Context& ctx0 = Ctx();
   const bool q8 = bq.q != nullptr;
-  if (q8 && LaunchGemmQ8Bf16(a, bq, c, m, k, n, epi, stream)) return;
+  bool rms_done = false;
+  if (q8 && LaunchGemmQ8Bf16(a, bq, c, m, k, n, epi, stream, rms, &rms_done)) return rms_done;
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // Large tiles when they alone give about two workgroups per CU; 64x64 otherwise.
   int bm = 128, bn = 128;
@@ -439,6 +440,7 @@ void LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
   else Launch<64, 64>(args, q8, grid, stream);
   Check(hipGetLastError(), "GemmKernel launch");
   if (splits > 1) LaunchSplitReduce(args.partials, args.splits, m, n, c, kScalePerRow, nullptr, 0, epi, stream);
+  return false;
 }
 
 }  // namespace accel_hip

@@ -309,13 +309,366 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 
   }
 }
 
+// ---- the 128-tile GEMM from an activation image and a staged bf16 weight ---------------
+//
+// The kernel above spends most of its VALU issue splitting A (in each of the column tiles
+// that read it) and converting W (in each of the row tiles). Here both happen once:
+//  * SplitAImageKernel splits A once per call into the hi/mid/lo image: for row tile tm and
+//    chunk c, 24 KB holding exactly what one chunk's three LDS planes hold (same swizzle), so
+//    a tile copies it into LDS with 16-byte loads and stores and no arithmetic;
+//  * the weight is staged once as bf16 in the B-operand order of v_mfma_f32_32x32x16_bf16
+//    (StagedBf16Image), so each wave loads its B operands straight from memory, one 16-byte
+//    load per lane and 32 x 16 block, with no LDS round trip and no conversion.
+// Products stay exact (the same three parts and the same accumulators as above).
+// With a fused RMSNorm each tile also leaves the double sum of squares of its stored values
+// per row ([tiles_n][m]); RmsScaleKernel adds a row's tile sums in tile order and scales it.
+
+constexpr int kImgRows = 128;
+constexpr int kImgPlaneWords = kImgRows * kRowWords;  // 2048 words
+constexpr int kImgBlockWords = 3 * kImgPlaneWords;    // 24 KB per (row tile, chunk)
+constexpr int kImgBlockVecs = kImgBlockWords / 4;     // 1536 16-byte pieces, 6 per thread
+constexpr int kImgBStages = 3;                         // weight-operand register sets in flight
+
+// One thread per (row tile, chunk, row, k group): the three parts of 8 activations.
+__global__ void SplitAImageKernel(const float* __restrict__ a, uint32_t* __restrict__ img, int64_t m, int64_t k,
+                                  int32_t chunks, int64_t items) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= items) return;
+  const int64_t blk = t >> 9;  // tm * chunks + c
+  const int rem = static_cast<int>(t & 511);
+  const int r = rem >> 2;
+  const int g = rem & 3;
+  const int64_t tm = blk / chunks;
+  const int c = static_cast<int>(blk - tm * chunks);
+  const int64_t row = tm * kImgRows + r;
+  float x[8];
+  if (row < m) {
+    const float4* src = reinterpret_cast<const float4*>(a + row * k + static_cast<int64_t>(c) * kBK + 8 * g);
+    const float4 v0 = src[0], v1 = src[1];
+    x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+    x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = 0.f;
+  }
+  uint32_t part[3][4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const float x0 = x[2 * h];
+    const float x1 = x[2 * h + 1];
+    part[0][h] = PackBf16(x0, x1);
+    const float r0 = x0 - Bf16Low(part[0][h]);
+    const float r1 = x1 - Bf16High(part[0][h]);
+    part[1][h] = PackBf16(r0, r1);
+    part[2][h] = PackBf16(r0 - Bf16Low(part[1][h]), r1 - Bf16High(part[1][h]));
+  }
+  uint32_t* dst = img + blk * kImgBlockWords + GroupWord(r, g);
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl)
+    *reinterpret_cast<u32x4*>(dst + pl * kImgPlaneWords) = u32x4{part[pl][0], part[pl][1], part[pl][2], part[pl][3]};
+}
+
+// One thread per 16-byte lane piece of the staged bf16 weight (layout: StagedBf16Bytes).
+__global__ void TileBf16Kernel(const int8_t* __restrict__ q, int64_t k, int64_t n, u32x4* __restrict__ out,
+                               int64_t k_steps, int64_t items) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= items) return;
+  const int lane = static_cast<int>(t & 63);
+  const int64_t blk = t >> 6;
+  const int64_t cb = blk / k_steps;
+  const int64_t st = blk - cb * k_steps;
+  const int64_t col = cb * 32 + (lane & 31);
+  const int64_t k0 = st * 16 + 8 * (lane >> 5);
+  uint32_t w[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const float q0 = col < n ? static_cast<float>(q[(k0 + 2 * h) * n + col]) : 0.f;
+    const float q1 = col < n ? static_cast<float>(q[(k0 + 2 * h + 1) * n + col]) : 0.f;
+    w[h] = PackBf16(q0, q1);
+  }
+  out[t] = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+struct ImageArgs {
+  const u32x4* a_img;  // [tiles_m][chunks] blocks of kImgBlockVecs
+  const u32x4* w_img;  // staged bf16 weight, [col_blocks][k_steps][64]
+  const float* scale;
+  int32_t mode;
+  int64_t const_index;
+  float* c;
+  int64_t m, k, n;
+  int32_t tiles_m, tiles_n, tiles, tiles_per_xcd, chunks, col_blocks;
+  int64_t k_steps;  // k / 16
+  double* row_ss;   // [tiles_n][m] row sums of squares of the stored values, or nullptr
+  Epilogue epi;
+};
+
+__device__ __forceinline__ void LoadImageA(const ImageArgs& p, int64_t a_block, int ch, int tid, u32x4 (&r)[6]) {
+  const u32x4* src = p.a_img + (a_block + ch) * kImgBlockVecs;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) r[i] = src[i * kThreads + tid];
+}
+
+// B operands of one chunk for this wave: k steps 2ch, 2ch + 1 of its two 32-column blocks
+// (blocks past the weight repeat the last one; their columns are never stored).
+__device__ __forceinline__ void LoadImageB(const ImageArgs& p, int cb0, int ch, int lane, u32x4 (&r)[2][2]) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t cb = min(cb0 + j, p.col_blocks - 1);
+      r[ks][j] = p.w_img[(cb * p.k_steps + 2 * ch + ks) * 64 + lane];
+    }
+}
+
+__device__ __forceinline__ void StoreImageA(uint32_t* buf, int tid, const u32x4 (&r)[6]) {
+#pragma unroll
+  for (int i = 0; i < 6; ++i) reinterpret_cast<u32x4*>(buf)[i * kThreads + tid] = r[i];
+}
+
+__device__ __forceinline__ void ComputeImageChunk(const uint32_t* buf, const u32x4 (&bv)[2][2], int lane, int wm,
+                                                  v16f (&acc_hi)[2][2], v16f (&acc_ml)[2][2]) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int g = 2 * ks + (lane >> 5);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+      u32x4 av[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        av[i] = *reinterpret_cast<const u32x4*>(&buf[pl * kImgPlaneWords + GroupWord(wm * 64 + i * 32 + (lane & 31), g)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          v16f& acc = pl == 0 ? acc_hi[i][j] : acc_ml[i][j];
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[i]),
+                                                        __builtin_bit_cast(bf16x8, bv[ks][j]), acc, 0, 0, 0);
+        }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void GemmQ8Bf16ImageKernel(ImageArgs p) {
+  __shared__ __align__(16) uint32_t lds[2 * kImgBlockWords];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int t = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
+  if (t >= p.tiles) return;
+  const int band_tiles = kBand * p.tiles_n;
+  const int band = t / band_tiles;
+  const int in_band = t % band_tiles;
+  const int rows_in_band = min(kBand, p.tiles_m - band * kBand);
+  const int tm = band * kBand + in_band % rows_in_band;
+  const int tn = in_band / rows_in_band;
+  const int64_t m0 = static_cast<int64_t>(tm) * kImgRows;
+  const int64_t n0 = static_cast<int64_t>(tn) * kImgRows;
+  const int64_t a_block = static_cast<int64_t>(tm) * p.chunks;
+  const int cb0 = tn * 4 + wn * 2;
+  const int chunks = p.chunks;
+
+  v16f acc[2][2], acc_ml[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.f;
+        acc_ml[i][j][r] = 0.f;
+      }
+
+  // A: chunk ch sits in LDS buffer ch % 2 while chunk ch + 1 waits in areg[(ch + 1) % 2] and
+  // chunk ch + 2 is loading into areg[ch % 2]. B: chunk ch's operands in breg[ch % 3], the
+  // next two chunks' loading. Loads past the last chunk repeat it (never used).
+  u32x4 areg[2][6];
+  u32x4 breg[kImgBStages][2][2];
+  LoadImageA(p, a_block, 0, tid, areg[0]);
+  LoadImageA(p, a_block, min(1, chunks - 1), tid, areg[1]);
+#pragma unroll
+  for (int s = 0; s < kImgBStages; ++s) LoadImageB(p, cb0, min(s, chunks - 1), lane, breg[s]);
+  StoreImageA(lds, tid, areg[0]);
+  __syncthreads();
+  constexpr int kUnroll = 6;  // lcm of the two rings, so every ring index is static
+  for (int base = 0; base < chunks; base += kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int ch = base + u;
+      if (ch >= chunks) break;  // workgroup-uniform
+      LoadImageA(p, a_block, min(ch + 2, chunks - 1), tid, areg[u % 2]);
+      ComputeImageChunk(lds + (u % 2) * kImgBlockWords, breg[u % kImgBStages], lane, wm, acc, acc_ml);
+      StoreImageA(lds + ((u + 1) % 2) * kImgBlockWords, tid, areg[(u + 1) % 2]);
+      LoadImageB(p, cb0, min(ch + kImgBStages, chunks - 1), lane, breg[u % kImgBStages]);
+      __syncthreads();
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + acc_ml[i][j][r];
+
+  // Element r of a 32 x 32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
+  float cs[2];
+  bool col_ok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    col_ok[j] = col < p.n;
+    cs[j] = col_ok[j] ? p.scale[p.mode == kScalePerCol ? col : p.const_index] : 0.f;
+  }
+  double* row_part = reinterpret_cast<double*>(lds);  // [2 wn][128 rows], after the last barrier
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rl = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int64_t row = m0 + rl;
+      double ss = 0.0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (row < p.m && col_ok[j]) {  // the epilogue reads bias and residual only inside [m, n]
+          const float v = ApplyEpilogue(__fmul_rn(acc[i][j][r], cs[j]), row, col, p.n, p.epi);
+          StoreC(p.c, row, col, p.n, p.epi, v);
+          ss += static_cast<double>(v) * static_cast<double>(v);
+        }
+      }
+      if (p.row_ss != nullptr) {
+        // Sum over the wave's 64 columns: the 32 lanes holding this row, then LDS per wave column.
+        ss += XorLane<1>(ss);
+        ss += XorLane<2>(ss);
+        ss += XorLane<4>(ss);
+        ss += XorLane<8>(ss);
+        ss += XorLane<16>(ss);
+        if ((lane & 31) == 0) row_part[wn * kImgRows + rl] = ss;
+      }
+    }
+  if (p.row_ss != nullptr) {
+    __syncthreads();
+    if (tid < kImgRows && m0 + tid < p.m)
+      p.row_ss[static_cast<int64_t>(tn) * p.m + m0 + tid] = row_part[tid] + row_part[kImgRows + tid];
+  }
+}
+
+// out[row, :] = float(double(c[row, :]) * inv) * w with inv = 1/sqrt(ss/n + eps) and ss the
+// row's tile sums added in tile order (SimRmsNorm's arithmetic, src/sim_rmsnorm.cc:7-20).
+// One workgroup per row; c and out may be the same buffer.
+__global__ void RmsScaleKernel(const float* c, const double* __restrict__ row_ss, int32_t tiles_n,
+                               const float* __restrict__ w, float* out, int64_t m, int64_t n, float eps, bool vec) {
+  __shared__ double part[256];
+  __shared__ double inv_s;
+  const int64_t row = blockIdx.x;
+  for (int t = threadIdx.x; t < tiles_n; t += blockDim.x) {
+    if (t < 256) part[t] = row_ss[static_cast<int64_t>(t) * m + row];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double total = 0.0;
+    for (int t = 0; t < tiles_n && t < 256; ++t) total += part[t];
+    for (int t = 256; t < tiles_n; ++t) total += row_ss[static_cast<int64_t>(t) * m + row];
+    inv_s = 1.0 / sqrt(total / static_cast<double>(n) + static_cast<double>(eps));
+  }
+  __syncthreads();
+  const double inv = inv_s;
+  const float* in = c + row * n;
+  float* o = out + row * n;
+  if (vec) {  // n % 4 == 0 and c, w, out 16-byte aligned
+    for (int64_t i = 4 * threadIdx.x; i < n; i += 4 * blockDim.x) {
+      const float4 x = *reinterpret_cast<const float4*>(in + i);
+      const float4 g = *reinterpret_cast<const float4*>(w + i);
+      float4 y;
+      y.x = __fmul_rn(static_cast<float>(static_cast<double>(x.x) * inv), g.x);
+      y.y = __fmul_rn(static_cast<float>(static_cast<double>(x.y) * inv), g.y);
+      y.z = __fmul_rn(static_cast<float>(static_cast<double>(x.z) * inv), g.z);
+      y.w = __fmul_rn(static_cast<float>(static_cast<double>(x.w) * inv), g.w);
+      *reinterpret_cast<float4*>(o + i) = y;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x)
+      o[i] = __fmul_rn(static_cast<float>(static_cast<double>(in[i]) * inv), w[i]);
+  }
+}
+
 }  // namespace
 
+void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream) {
+  const int64_t k_steps = k / 16;
+  const int64_t items = (n + 31) / 32 * k_steps * 64;
+  if (items <= 0) return;
+  const int64_t grid = (items + kThreads - 1) / kThreads;
+  if (grid > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "weight too large to stage");
+  hipLaunchKernelGGL(TileBf16Kernel, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, q, k, n,
+                     static_cast<u32x4*>(dst), k_steps, items);
+  Check(hipGetLastError(), "TileBf16Kernel launch");
+}
+
+bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v) {
+  if (v.q == nullptr || v.zero != nullptr || (v.mode != kScalePerCol && v.mode != kScaleConst)) return false;
+  if (m < 1 || k < 2 * kBK || n < 8 || k % kBK != 0 || n % 8 != 0 || k / kBK > 0x7fffffff) return false;
+  Context& ctx = Ctx();
+  const int64_t cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
+  return ((m + 127) / 128) * ((n + 127) / 128) >= cus;  // the 128-tile grid, no K split
+}
+
 bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
-                      hipStream_t stream) {
+                      hipStream_t stream, const RmsRequest* rms, bool* rms_done) {
+  if (rms_done != nullptr) *rms_done = false;
   if (b.q == nullptr || b.zero != nullptr || (b.mode != kScalePerCol && b.mode != kScaleConst)) return false;
   if (m < 1 || k < kBK || n < 8 || k % kBK != 0 || n % 8 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a) % 16 != 0 || reinterpret_cast<uintptr_t>(b.q) % 8 != 0) return false;
+  if (b.bf16 != nullptr && GemmWantsBf16Image(m, k, n, b)) {
+    const int64_t tiles_m = (m + kImgRows - 1) / kImgRows;
+    const int64_t tiles_n = (n + kImgRows - 1) / kImgRows;
+    const int64_t chunks = k / kBK;
+    const size_t img_bytes = static_cast<size_t>(tiles_m * chunks) * kImgBlockWords * sizeof(uint32_t);
+    const size_t ss_bytes = rms != nullptr ? static_cast<size_t>(tiles_n * m) * sizeof(double) : 0;
+    if (tiles_m * tiles_n * kBand <= 0x7fffffff && WorkspaceFits(img_bytes + ss_bytes + 512)) {
+      ImageArgs ia;
+      ia.a_img = static_cast<const u32x4*>(Temp(kTempSplitA, img_bytes));
+      ia.w_img = static_cast<const u32x4*>(b.bf16);
+      ia.scale = b.scale;
+      ia.mode = b.mode;
+      ia.const_index = b.const_index;
+      ia.c = c;
+      ia.m = m;
+      ia.k = k;
+      ia.n = n;
+      ia.tiles_m = static_cast<int32_t>(tiles_m);
+      ia.tiles_n = static_cast<int32_t>(tiles_n);
+      ia.tiles = static_cast<int32_t>(tiles_m * tiles_n);
+      ia.tiles_per_xcd = static_cast<int32_t>((ia.tiles + kXcds - 1) / kXcds);
+      ia.chunks = static_cast<int32_t>(chunks);
+      ia.col_blocks = static_cast<int32_t>((n + 31) / 32);
+      ia.k_steps = k / 16;
+      ia.row_ss = rms != nullptr ? static_cast<double*>(Temp(kTempRowSums, ss_bytes)) : nullptr;
+      ia.epi = epi;
+      const int64_t items = tiles_m * chunks * 512;
+      hipLaunchKernelGGL(SplitAImageKernel, dim3(static_cast<uint32_t>((items + kThreads - 1) / kThreads)),
+                         dim3(kThreads), 0, stream, a, const_cast<uint32_t*>(reinterpret_cast<const uint32_t*>(ia.a_img)),
+                         m, k, ia.chunks, items);
+      Check(hipGetLastError(), "SplitAImageKernel launch");
+      hipLaunchKernelGGL(GemmQ8Bf16ImageKernel, dim3(static_cast<uint32_t>(ia.tiles_per_xcd * kXcds)), dim3(kThreads),
+                         0, stream, ia);
+      Check(hipGetLastError(), "GemmQ8Bf16ImageKernel launch");
+      if (rms != nullptr) {
+        if (m > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "RmsNorm has too many rows");
+        const bool vec = n % 4 == 0 && reinterpret_cast<uintptr_t>(c) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(rms->weight) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(rms->out) % 16 == 0;
+        hipLaunchKernelGGL(RmsScaleKernel, dim3(static_cast<uint32_t>(m)), dim3(kThreads), 0, stream, c, ia.row_ss,
+                           ia.tiles_n, rms->weight, rms->out, m, n, rms->eps, vec);
+        Check(hipGetLastError(), "RmsScaleKernel launch");
+        if (rms_done != nullptr) *rms_done = true;
+      }
+      return true;
+    }
+  }
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // 128 x 128 tiles when they give one per CU, else 64 x 64.

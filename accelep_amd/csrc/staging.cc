@@ -5,7 +5,8 @@
 // few columns walks k rows 14 KB apart, which HBM serves at well under half its streaming
 // rate. On its first use by the GEMV, the matrix is copied once into 8-column tiles, each
 // tile's k x 8 bytes contiguous (the m > 1 MFMA GEMV takes a group-interleaved form of the
-// same tiles instead); later calls read the copy. The original bytes stay as
+// same tiles instead, and the int8-weight GEMM a bf16 copy in its MFMA operand order); later
+// calls read the copy. The original bytes stay as
 // they are, so every counted copy and every other kernel still sees the EP's layout.
 //
 // A copy is keyed by (allocation id, byte offset, k, n) and dropped when its allocation is
@@ -29,7 +30,7 @@
 namespace accel_hip {
 namespace {
 
-enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1 };
+enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1, kLayoutBf16 = 2 };
 
 struct Key {
   uint64_t id;
@@ -100,11 +101,14 @@ const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStrea
   if (!create) return nullptr;
   RefuseInCapture("staging an int8 weight copy for the GEMV (its first use)");
   ReleasePending();
-  const size_t bytes = layout == kLayoutGroups ? StagedGroupBytes(k, n) : StagedTileBytes(k, n);
+  const size_t bytes = layout == kLayoutGroups ? StagedGroupBytes(k, n)
+                       : layout == kLayoutBf16  ? StagedBf16Bytes(k, n)
+                                                : StagedTileBytes(k, n);
   EvictFor(bytes);
   int8_t* dst = nullptr;
   if (hipMalloc(reinterpret_cast<void**>(&dst), bytes) != hipSuccess) return nullptr;  // fall back to raw
   if (layout == kLayoutGroups) LaunchTileGroups(q, k, n, dst, stream);
+  else if (layout == kLayoutBf16) LaunchTileBf16(q, k, n, dst, stream);
   else LaunchTileColumns(q, k, n, dst, stream);
   const uint64_t serial = g_next_serial++;
   g_staged.emplace(key, Entry{dst, bytes, ++g_tick, serial});
@@ -123,6 +127,11 @@ const int8_t* StagedColumnTiles(const int8_t* q, int64_t k, int64_t n, hipStream
 const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
   if (k % kGemvGroupRows != 0) return nullptr;
   return Staged(q, k, n, kLayoutGroups, stream, create);
+}
+
+const void* StagedBf16Image(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
+  if (k % 32 != 0) return nullptr;
+  return Staged(q, k, n, kLayoutBf16, stream, create);
 }
 
 void BeginStagedUses() {

@@ -487,6 +487,31 @@ def test_gemm_c4_shape_with_fused_rmsnorm():
     assert np.isfinite(y).all()
 
 
+def test_gemm_image_path_fused_rmsnorm_ragged():
+    """The 128-tile GEMM from the activation image and the staged bf16 weight, with ragged m
+    and n, alpha, bias and Gelu before a fused RMSNormalization: the stored product meets the
+    gamma_K bound (plus the epilogue's roundings), and every normalized row equals the oracle's
+    RMSNorm of the stored row to 1e-6 (the row sums of squares are added per tile, in double)."""
+    m, k, n = 300, 256, 12296
+    case = _split_case(m, k, n, 4300)
+    r = np.random.default_rng(4301)
+    gamma_w = (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+    bias = (0.1 * r.standard_normal(n)).astype(np.float32)
+    g_d, b_d = dev(gamma_w), dev(bias)
+    out = dev(np.zeros((m, n), np.float32))
+    e = Epilogue(alpha=1.25, beta=1.0, bias=b_d.ptr, bias_rank=1, activation=2, rms_weight=g_d.ptr, rms_eps=1e-5,
+                 rms_out=out.ptr)
+    e.bias_shape[0] = n
+    got = matmul_quantized(case, e)
+    y = out.numpy()
+    w = dequant_host(case["bq"], k, n)
+    o = oracle()
+    want = o.gemm_epilogue((case["a"].astype(np.float64) @ w.astype(np.float64)).astype(np.float32), 1.25, bias, [n],
+                           1.0, 2)
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(y, o.rmsnorm(np.ascontiguousarray(got), gamma_w, m, n, 1e-5), rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("m", [2, 4])
 def test_staged_weight_follows_rewrites(m):
     """The GEMV reads a staged copy of W (8-column tiles at m = 2, the group-interleaved form

@@ -53,13 +53,14 @@ def _run(p, noalloc, epi=None):
 
 
 # (m, k, n): split-bf16 GEMV (4 splits, arrival counters), split-K narrow GEMV (few tiles),
-# m = 1 entry GEMV, wide GEMV (m = 16, W in place), bf16 GEMM with split K (small grid),
-# fp32-panel GEMM (per-row scale, zero points) with split K.
+# m = 1 entry GEMV, bf16 GEMM with split K (small grid), bf16 GEMM from the activation image
+# (staged bf16 weight), fp32-panel GEMM (per-row scale, zero points) with split K.
 CASES = [
     ("split_bf16_gemv", (16, 4096, 2048), dict()),
     ("split_k_gemv", (2, 4096, 512), dict()),
     ("m1_gemv", (1, 2048, 4096), dict()),
     ("bf16_gemm_split", (100, 2048, 264), dict()),
+    ("bf16_gemm_image", (512, 256, 8192), dict()),
     ("f32_gemm_zero_rowscale", (40, 1024, 96), dict(axis=0, zero=True)),
 ]
 
