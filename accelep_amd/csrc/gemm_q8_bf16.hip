@@ -329,7 +329,18 @@ constexpr int kImgBlockWords = 3 * kImgPlaneWords;    // 24 KB per (row tile, ch
 constexpr int kImgBlockVecs = kImgBlockWords / 4;     // 1536 16-byte pieces, 6 per thread
 constexpr int kImgBStages = 3;                         // weight-operand register sets in flight
 
+// Word offset of 16-byte k group g of image row `row`: g ^ f(row) with f(row) = ((row >> 1) ^
+// (row >> 2)) & 3. A 16-byte LDS read by 8 (32 banks) or 16 (64 banks) lanes of consecutive
+// rows then covers every bank once: those rows' bases take 2 (or 4) bank quarters, and f sends
+// the rows sharing a base to distinct groups.
+template <int kSwz>
+__device__ __forceinline__ int ImageWord(int row, int g) {
+  if constexpr (kSwz == 0) return GroupWord(row, g);
+  return row * kRowWords + 4 * (g ^ (((row >> 1) ^ (row >> 2)) & 3));
+}
+
 // One thread per (row tile, chunk, row, k group): the three parts of 8 activations.
+template <int kSwz>
 __global__ void SplitAImageKernel(const float* __restrict__ a, uint32_t* __restrict__ img, int64_t m, int64_t k,
                                   int32_t chunks, int64_t items) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -362,7 +373,7 @@ __global__ void SplitAImageKernel(const float* __restrict__ a, uint32_t* __restr
     part[1][h] = PackBf16(r0, r1);
     part[2][h] = PackBf16(r0 - Bf16Low(part[1][h]), r1 - Bf16High(part[1][h]));
   }
-  uint32_t* dst = img + blk * kImgBlockWords + GroupWord(r, g);
+  uint32_t* dst = img + blk * kImgBlockWords + ImageWord<kSwz>(r, g);
 #pragma unroll
   for (int pl = 0; pl < 3; ++pl)
     *reinterpret_cast<u32x4*>(dst + pl * kImgPlaneWords) = u32x4{part[pl][0], part[pl][1], part[pl][2], part[pl][3]};
@@ -426,29 +437,45 @@ __device__ __forceinline__ void StoreImageA(uint32_t* buf, int tid, const u32x4 
   for (int i = 0; i < 6; ++i) reinterpret_cast<u32x4*>(buf)[i * kThreads + tid] = r[i];
 }
 
+// The chunk's six operand groups (2 k steps x 3 planes), each two 16-byte LDS reads of A and
+// four MFMAs. The reads of group g + 1 are issued before the MFMAs of group g, so each LDS
+// round trip runs under the previous group's matrix work instead of ahead of its own.
+template <int kSwz>
+__device__ __forceinline__ void ReadImageGroup(const uint32_t* buf, int lane, int wm, int grp, u32x4 (&av)[2]) {
+  const int ks = grp / 3, pl = grp % 3;
+  const int g = 2 * ks + (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    av[i] = *reinterpret_cast<const u32x4*>(&buf[pl * kImgPlaneWords + ImageWord<kSwz>(wm * 64 + i * 32 + (lane & 31), g)]);
+}
+
+template <int kSwz>
 __device__ __forceinline__ void ComputeImageChunk(const uint32_t* buf, const u32x4 (&bv)[2][2], int lane, int wm,
                                                   v16f (&acc_hi)[2][2], v16f (&acc_ml)[2][2]) {
+  u32x4 av[2][2];
+  ReadImageGroup<kSwz>(buf, lane, wm, 0, av[0]);
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int g = 2 * ks + (lane >> 5);
+  for (int grp = 0; grp < 6; ++grp) {
+    if (grp + 1 < 6) ReadImageGroup<kSwz>(buf, lane, wm, grp + 1, av[(grp + 1) & 1]);
+    const int ks = grp / 3, pl = grp % 3;
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl) {
-      u32x4 av[2];
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        av[i] = *reinterpret_cast<const u32x4*>(&buf[pl * kImgPlaneWords + GroupWord(wm * 64 + i * 32 + (lane & 31), g)]);
+      for (int j = 0; j < 2; ++j) {
+        v16f& acc = pl == 0 ? acc_hi[i][j] : acc_ml[i][j];
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[grp & 1][i]),
+                                                      __builtin_bit_cast(bf16x8, bv[ks][j]), acc, 0, 0, 0);
+      }
+  }
+  // Keep that order: group g + 1's two LDS reads, then group g's four MFMAs.
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          v16f& acc = pl == 0 ? acc_hi[i][j] : acc_ml[i][j];
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[i]),
-                                                        __builtin_bit_cast(bf16x8, bv[ks][j]), acc, 0, 0, 0);
-        }
-    }
+  for (int grp = 0; grp < 6; ++grp) {
+    if (grp + 1 < 6) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                  // MFMA
   }
 }
 
+template <int kSwz, int kNB>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void GemmQ8Bf16ImageKernel(ImageArgs p) {
   __shared__ __align__(16) uint32_t lds[2 * kImgBlockWords];
   const int tid = threadIdx.x;
@@ -484,24 +511,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // A: chunk ch sits in LDS buffer ch % 2 while chunk ch + 1 waits in areg[(ch + 1) % 2] and
   // chunk ch + 2 is loading into areg[ch % 2]. B: chunk ch's operands in breg[ch % 3], the
   // next two chunks' loading. Loads past the last chunk repeat it (never used).
+  u32x4 breg[kNB][2][2];
+#pragma unroll
+  for (int s = 0; s < kNB; ++s) LoadImageB(p, cb0, min(s, chunks - 1), lane, breg[s]);
   u32x4 areg[2][6];
-  u32x4 breg[kImgBStages][2][2];
   LoadImageA(p, a_block, 0, tid, areg[0]);
   LoadImageA(p, a_block, min(1, chunks - 1), tid, areg[1]);
-#pragma unroll
-  for (int s = 0; s < kImgBStages; ++s) LoadImageB(p, cb0, min(s, chunks - 1), lane, breg[s]);
   StoreImageA(lds, tid, areg[0]);
   __syncthreads();
-  constexpr int kUnroll = 6;  // lcm of the two rings, so every ring index is static
+  constexpr int kUnroll = kNB == 3 ? 6 : 2 * kNB;  // a multiple of both rings, so every ring index is static
   for (int base = 0; base < chunks; base += kUnroll) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int ch = base + u;
       if (ch >= chunks) break;  // workgroup-uniform
       LoadImageA(p, a_block, min(ch + 2, chunks - 1), tid, areg[u % 2]);
-      ComputeImageChunk(lds + (u % 2) * kImgBlockWords, breg[u % kImgBStages], lane, wm, acc, acc_ml);
+      ComputeImageChunk<kSwz>(lds + (u % 2) * kImgBlockWords, breg[u % kNB], lane, wm, acc, acc_ml);
       StoreImageA(lds + ((u + 1) % 2) * kImgBlockWords, tid, areg[(u + 1) % 2]);
-      LoadImageB(p, cb0, min(ch + kImgBStages, chunks - 1), lane, breg[u % kImgBStages]);
+      LoadImageB(p, cb0, min(ch + kNB, chunks - 1), lane, breg[u % kNB]);
       __syncthreads();
     }
   }
@@ -649,12 +676,12 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
       ia.row_ss = rms != nullptr ? static_cast<double*>(Temp(kTempRowSums, ss_bytes)) : nullptr;
       ia.epi = epi;
       const int64_t items = tiles_m * chunks * 512;
-      hipLaunchKernelGGL(SplitAImageKernel, dim3(static_cast<uint32_t>((items + kThreads - 1) / kThreads)),
-                         dim3(kThreads), 0, stream, a, const_cast<uint32_t*>(reinterpret_cast<const uint32_t*>(ia.a_img)),
-                         m, k, ia.chunks, items);
+      const dim3 sgrid(static_cast<uint32_t>((items + kThreads - 1) / kThreads));
+      uint32_t* img = const_cast<uint32_t*>(reinterpret_cast<const uint32_t*>(ia.a_img));
+      hipLaunchKernelGGL(SplitAImageKernel<1>, sgrid, dim3(kThreads), 0, stream, a, img, m, k, ia.chunks, items);
       Check(hipGetLastError(), "SplitAImageKernel launch");
-      hipLaunchKernelGGL(GemmQ8Bf16ImageKernel, dim3(static_cast<uint32_t>(ia.tiles_per_xcd * kXcds)), dim3(kThreads),
-                         0, stream, ia);
+      hipLaunchKernelGGL((GemmQ8Bf16ImageKernel<1, kImgBStages>), dim3(static_cast<uint32_t>(ia.tiles_per_xcd * kXcds)),
+                         dim3(kThreads), 0, stream, ia);
       Check(hipGetLastError(), "GemmQ8Bf16ImageKernel launch");
       if (rms != nullptr) {
         if (m > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "RmsNorm has too many rows");
