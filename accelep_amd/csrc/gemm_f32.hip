@@ -380,6 +380,131 @@ void Launch(const GemmArgs& args, bool q8, dim3 grid, hipStream_t stream) {
   else hipLaunchKernelGGL((GemmKernel<BM, BN, false>), grid, dim3(kThreads), 0, stream, args);
 }
 
+// ---- small grids: the waves of a workgroup split K, operands straight from memory ------
+//
+// A product whose 64 x 64 tiles barely cover the CUs (the MLP's 256 x 1024 x 4096 and
+// 256 x 4096 x 1024) gives each SIMD one wave. In the LDS kernel above that wave runs one or
+// two dependent MFMA chains and meets a barrier every 16 k. Here each of the 4 waves takes the
+// whole 64 x 64 tile over a quarter of the workgroup's K range, as 4 x 4 independent
+// v_mfma_f32_16x16x4f32 chains, with no LDS and no barrier until the end:
+//  * the 16 k of one group are assigned to MFMA steps so that every load is a float4: lane
+//    group q = lane / 16 of row tile i loads A[16i + lane % 16][kb + 4q .. 4q + 3], whose
+//    element s is its A operand in step s (k = kb + 4q + s); in step s the lane loads
+//    B[kb + 4q + s][4(lane % 16) .. + 3], whose element j is its B operand for column tile j,
+//    so MFMA column c of tile j is the tile's column 4c + j. The product sums every k of the
+//    group once, in another order; 8 loads feed 64 MFMAs;
+//  * operands of the next two groups are in flight while one group's 64 MFMAs run;
+//  * the four wave partials meet in LDS and are added in wave order; a K split across
+//    workgroups (for grids with fewer tiles than CUs) goes through the workspace and
+//    SplitReduceKernel, as above. (Combining the splits in the last workgroup to arrive, with
+//    agent-scope stores and loads of the partial tiles, measured slower on the MLP's
+//    256 x 4096 x 1024: 73 against 55 us per MLP step.)
+// Full tiles only: m and n multiples of 64, K per wave a multiple of 4 groups of 16, A and B
+// 16-byte aligned.
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWsTile = 64;
+constexpr int kWsGroupK = 16;
+constexpr int kWsStages = 4;  // groups in flight (32 loads, below the 63 the load counter tracks)
+constexpr int kWsPad = kWsTile + 1;  // LDS row stride of the partial tiles (no bank conflicts)
+
+struct WsArgs {
+  const float* a;
+  const float* b;
+  float* c;
+  int64_t m, k, n;
+  int64_t k_per_wg;    // K range of one workgroup (a multiple of 4 * kWsGroupK)
+  float* partials;     // [splits][m][n] when K is split across workgroups, else nullptr
+  Epilogue epi;
+};
+
+struct WsOperands {
+  float4 a[4];  // row tiles 0..3: 4 consecutive k of this lane's row
+  float4 b[4];  // steps 0..3: 4 consecutive columns (one per column tile) of this lane's k row
+};
+
+__device__ __forceinline__ void LoadWsGroup(const WsArgs& p, int64_t m0, int64_t n0, int64_t kb, int lane,
+                                            WsOperands& r) {
+  const int q = lane >> 4, l16 = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r.a[i] = *reinterpret_cast<const float4*>(p.a + (m0 + 16 * i + l16) * p.k + kb + 4 * q);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) r.b[s] = *reinterpret_cast<const float4*>(p.b + (kb + 4 * q + s) * p.n + n0 + 4 * l16);
+}
+
+__device__ __forceinline__ float Lane4(const float4& v, int s) {
+  return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w;
+}
+
+// kGroups > 0: the K range of a wave is exactly kGroups groups and the loop is unrolled whole
+// (straight-line code, so each MFMA group waits only for its own loads; a loop head merges the
+// loads in flight and drains them all). kGroups == 0: any multiple of kWsStages groups.
+template <int kGroups>
+__global__ __launch_bounds__(kThreads) void GemmF32WaveSplitKernel(WsArgs p) {
+  __shared__ float red[4][kWsTile][kWsPad];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t tiles_n = p.n / kWsTile;
+  const int64_t tile = blockIdx.x;
+  const int64_t m0 = (tile / tiles_n) * kWsTile;
+  const int64_t n0 = (tile % tiles_n) * kWsTile;
+  const int64_t k_wave = p.k_per_wg / 4;
+  const int64_t kbeg = static_cast<int64_t>(blockIdx.y) * p.k_per_wg + wave * k_wave;
+  const int groups = kGroups > 0 ? kGroups : static_cast<int>(k_wave / kWsGroupK);
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  WsOperands ops[kWsStages];
+#pragma unroll
+  for (int st = 0; st < kWsStages; ++st)
+    LoadWsGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(st, groups - 1)) * kWsGroupK, lane, ops[st]);
+  // groups is a multiple of kWsStages: the unrolled body has no exit, so the loop head sees one
+  // pattern of loads in flight and waits only for the group it needs.
+#pragma unroll (kGroups > 0 ? kGroups / kWsStages : 1)
+  for (int base = 0; base < groups; base += kWsStages) {
+#pragma unroll
+    for (int st = 0; st < kWsStages; ++st) {
+      const int g = base + st;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(Lane4(ops[st].a[i], s), Lane4(ops[st].b[s], j), acc[i][j], 0,
+                                                             0, 0);
+      // The group kWsStages ahead (repeating the last one past the end; never used), issued here:
+      // the barrier keeps the scheduler from sinking the loads to their use.
+      LoadWsGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(g + kWsStages, groups - 1)) * kWsGroupK, lane, ops[st]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // Element r of tile (i, j): row 16i + 4 * (lane / 16) + r, column 4 * (lane % 16) + j.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][16 * i + 4 * (lane >> 4) + r][4 * (lane & 15) + j] = acc[i][j][r];
+  __syncthreads();
+#pragma unroll 4
+  for (int u = 0; u < kWsTile * kWsTile / kThreads; ++u) {
+    const int idx = u * kThreads + tid;
+    const int row = idx / kWsTile, col = idx % kWsTile;
+    const float v = red[0][row][col] + red[1][row][col] + red[2][row][col] + red[3][row][col];
+    const int64_t gr = m0 + row, gc = n0 + col;
+    if (p.partials != nullptr) p.partials[(static_cast<int64_t>(blockIdx.y) * p.m + gr) * p.n + gc] = v;
+    else StoreC(p.c, gr, gc, p.n, p.epi, ApplyEpilogue(v, gr, gc, p.n, p.epi));
+  }
+}
+
 }  // namespace
 
 bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
@@ -393,6 +518,36 @@ bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
   // Large tiles when they alone give about two workgroups per CU; 64x64 otherwise.
   int bm = 128, bn = 128;
   auto tiles_for = [&](int tm, int tn) { return ((m + tm - 1) / tm) * ((n + tn - 1) / tn); };
+  if (!q8 && tiles_for(128, 128) < 2 * cus && m % kWsTile == 0 && n % kWsTile == 0 &&
+      reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 && m / kWsTile <= 65535) {
+    // Small fp32 grid: waves split K (GemmF32WaveSplitKernel); K split across workgroups too
+    // when the tiles leave CUs idle, into ranges of whole 4-wave groups.
+    const int64_t wtiles = (m / kWsTile) * (n / kWsTile);
+    const int64_t unit = 4 * kWsGroupK * kWsStages;  // per workgroup: 4 waves x whole stage rings
+    int64_t wsplits = wtiles < cus ? std::max<int64_t>(1, std::min<int64_t>((cus + wtiles - 1) / wtiles, k / (4 * unit)))
+                                   : 1;
+    while (wsplits > 1 && k % (wsplits * unit) != 0) --wsplits;
+    if (k % (wsplits * unit) == 0 && wtiles <= 0x7fffffff) {
+      WsArgs ws;
+      ws.a = a;
+      ws.b = b;
+      ws.c = c;
+      ws.m = m;
+      ws.k = k;
+      ws.n = n;
+      ws.k_per_wg = k / wsplits;
+      ws.partials = wsplits > 1 ? static_cast<float*>(Workspace(static_cast<size_t>(wsplits * m * n) * sizeof(float)))
+                                : nullptr;
+      ws.epi = epi;
+      const dim3 grid(static_cast<uint32_t>(wtiles), static_cast<uint32_t>(wsplits));
+      if (ws.k_per_wg / 4 == 16 * kWsGroupK) hipLaunchKernelGGL(GemmF32WaveSplitKernel<16>, grid, dim3(kThreads), 0, stream, ws);
+      else hipLaunchKernelGGL(GemmF32WaveSplitKernel<0>, grid, dim3(kThreads), 0, stream, ws);
+      Check(hipGetLastError(), "GemmF32WaveSplitKernel launch");
+      if (wsplits > 1)
+        LaunchSplitReduce(ws.partials, static_cast<int32_t>(wsplits), m, n, c, kScalePerRow, nullptr, 0, epi, stream);
+      return false;
+    }
+  }
   if (tiles_for(128, 128) < 2 * cus) {
     bm = 64;
     bn = 64;

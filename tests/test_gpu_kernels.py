@@ -151,8 +151,14 @@ def test_matmul_probes_and_zero_k():
     assert e.value.kind == "invalid_argument" and "MatMul A is out of range" in e.value.message
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 1024, 4096), (256, 4096, 1024), (77, 300, 129), (1, 576, 49)])
+@pytest.mark.parametrize("m,k,n", [(256, 1024, 4096), (256, 4096, 1024), (77, 300, 129), (1, 576, 49), (64, 64, 64),
+                                   (128, 4096, 256), (64, 512, 64), (64, 2048, 192), (128, 1536, 128), (64, 1088, 704)])
 def test_matmul_against_oracle(m, k, n):
+    """fp32 GEMM. The 64 x 64 wave-split kernel takes small full-tile grids: 16 groups per wave
+    unrolled (256 x 1024 x 4096), with K also split over workgroups and combined by the last to
+    arrive (256 x 4096 x 1024: 4 splits; 128 x 4096 x 256: 4; 64 x 2048 x 192: 2), and the
+    looped form (64 x 512 x 64: 8 groups; 128 x 1536 x 128: 24). The LDS kernel takes the rest.
+    Every element within 2 gamma_K of the float64 product."""
     r = np.random.default_rng(m * 7 + k)
     a = r.standard_normal((m, k)).astype(np.float32)
     b = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
