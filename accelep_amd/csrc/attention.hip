@@ -714,6 +714,168 @@ __global__ __launch_bounds__(kSplitThreads) void DecodeAttentionKernel(
   if (tid == 0) atomicExch(&arrivals[h], 0u);
 }
 
+// ---- decode row, head_dim 64, fast mode: a fixed number of splits, combined by the consumer --
+// One workgroup per (head, split). The position range [0, position] is cut into `splits`
+// contiguous ranges of ceil((position + 1) / splits) positions (at most 256: one key row per
+// thread, one memory round after the position arrives). Each workgroup rotates its head's q,
+// and the one holding the new position rotates the new k, uses the new k and v from LDS for
+// it and, for the first query head of the kv group, stores them into the cache rows, as
+// DecodeAttentionKernel does. It writes its split's (max m, sum l, acc[64]) to `partial`
+// [heads][splits][2 + 64] and stops there: no arrival count, no combine. A split with no
+// positions writes m = -inf, l = 0, acc = 0. The reader combines the splits in split order:
+// w_s = e^(m_s - max m) (0 for m_s = -inf), out = sum_s w_s acc_s / sum_s w_s l_s
+// (StageInputRow's attention prologue of the int8 GEMV). The scores keep the reference's dot
+// order; the softmax sums run in another order (rounding only), so this is a fast-mode path.
+constexpr int kDecodeSplitThreads = 256;
+constexpr int kDecodeSplitRows = kDecodeSplitThreads;  // positions per split at most
+constexpr int kDecodeSplitMin = 8;  // the GEMV prologue reads the first 8 splits unconditionally
+constexpr int kDecodeSplitMax = 64;
+static_assert(kDecodeSplitMaxBytesPerHead == kDecodeSplitMax * (2 + kStepDim) * sizeof(float), "partial room");
+
+__global__ __launch_bounds__(kDecodeSplitThreads) void DecodeSplitAttentionKernel(
+    const float* q_raw, const float* k_raw, const float* v_raw, float* k_cache, float* v_cache, const float* cos_t,
+    const float* sin_t, int32_t position_arg, const int32_t* position_dev, int32_t group, int32_t kv_heads,
+    int32_t splits, float* partial) {
+  constexpr int kWaves = kDecodeSplitThreads / 64;
+  constexpr int kCols = 4;
+  constexpr int kQuads = kStepDim / kCols;                 // 16 column quads
+  constexpr int kGroups = kDecodeSplitThreads / kQuads;    // 16 position groups
+  constexpr int kPerGroup = kDecodeSplitRows / kGroups;    // 16 positions per group at most
+  __shared__ __align__(16) float qs[kStepDim];
+  __shared__ __align__(16) float knew[kStepDim];
+  __shared__ __align__(16) float vnew[kStepDim];
+  __shared__ float es[kDecodeSplitRows];
+  __shared__ float acc_part[kGroups * kStepDim];
+  __shared__ float wred[2][kWaves];
+  asm volatile("" ::"s"(k_cache), "s"(v_cache), "s"(q_raw), "s"(k_raw), "s"(v_raw), "s"(cos_t), "s"(sin_t),
+               "s"(position_arg), "s"(group), "s"(kv_heads), "s"(splits), "s"(partial));
+  const int position = position_dev != nullptr ? *position_dev : position_arg;
+  const int h = blockIdx.x;
+  const int sp = blockIdx.y;
+  const int kv = h / group;
+  const int total = position + 1;
+  const int len = (total + splits - 1) / splits;  // <= kDecodeSplitRows (launcher)
+  const int t0 = sp * len;
+  const int n = min(len, total - t0);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  float* mine = partial + (h * splits + sp) * (2 + kStepDim);
+  if (n <= 0) {  // uniform over the workgroup
+    if (tid < kStepDim) mine[2 + tid] = 0.f;
+    if (tid == 0) {
+      mine[0] = -INFINITY;
+      mine[1] = 0.f;
+    }
+    return;
+  }
+  const bool tail = t0 + n == total;  // this split holds the new position
+  const int kv_row = kv_heads * kStepDim;
+
+  // Every load of the workgroup is issued here, in one round: the rotation's inputs, this
+  // thread's key row, and the value rows of its (position group, column quad).
+  constexpr int kHalf = kStepDim / 2;
+  const int ri = tid % kHalf;
+  const bool rot_q = (tid >> 5) == 2;  // tid 64 .. 95: q; 96 .. 127: the new k
+  const float* rsrc = rot_q ? q_raw + h * kStepDim : k_raw + kv * kStepDim;
+  const float rx0 = rsrc[ri];
+  const float rx1 = rsrc[kHalf + ri];
+  const float rc0 = cos_t[position * kStepDim + ri];
+  const float rc1 = cos_t[position * kStepDim + kHalf + ri];
+  const float rs0 = sin_t[position * kStepDim + ri];
+  const float rs1 = sin_t[position * kStepDim + kHalf + ri];
+  const float rv = v_raw[kv * kStepDim + (tid & (kStepDim - 1))];
+  const int cq = tid % kQuads;
+  const int g = tid / kQuads;
+  float4 kx[kStepDim / 4];
+  const bool score_lane = tid < n && t0 + tid != position;
+  if (score_lane) {
+    const float4* kr = reinterpret_cast<const float4*>(k_cache + (t0 + tid) * kv_row + kv * kStepDim);
+#pragma unroll
+    for (int j = 0; j < kStepDim / 4; ++j) kx[j] = kr[j];
+  }
+  float4 vx[kPerGroup];
+#pragma unroll
+  for (int i = 0; i < kPerGroup; ++i) {
+    const int t = g + i * kGroups;
+    if (t < n) vx[i] = *reinterpret_cast<const float4*>(v_cache + (t0 + t) * kv_row + kv * kStepDim + cq * kCols);
+  }
+
+  if (rot_q || (tail && (tid >> 5) == 3)) {
+    float* dst = rot_q ? qs : knew;
+    dst[ri] = __fsub_rn(__fmul_rn(rx0, rc0), __fmul_rn(rx1, rs0));
+    dst[kHalf + ri] = __fadd_rn(__fmul_rn(rx1, rc1), __fmul_rn(rx0, rs1));
+  } else if (tail && (tid >> 6) == 2) {
+    vnew[tid - 128] = rv;
+  }
+  __syncthreads();
+  if (tail && h == kv * group && tid < kStepDim) {
+    k_cache[position * kv_row + kv * kStepDim + tid] = knew[tid];
+    v_cache[position * kv_row + kv * kStepDim + tid] = vnew[tid];
+  }
+
+  // Scores: d ascending, each product rounded before its add.
+  const float scale = __fdiv_rn(1.f, __fsqrt_rn(static_cast<float>(kStepDim)));
+  float x = -INFINITY;
+  if (tid < n) {
+    if (!score_lane) {
+#pragma unroll
+      for (int j = 0; j < kStepDim / 4; ++j) kx[j] = reinterpret_cast<const float4*>(knew)[j];
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < kStepDim / 4; ++j) {
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 0], kx[j].x));
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 1], kx[j].y));
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 2], kx[j].z));
+      dot = __fadd_rn(dot, __fmul_rn(qs[4 * j + 3], kx[j].w));
+    }
+    x = __fmul_rn(dot, scale);
+  }
+  // The split's max, then e = exp(x - max) and its sum: waves, then the wave values in order.
+  const float wmax = WaveButterfly(x, [](float a, float b) { return fmaxf(a, b); });
+  if (lane == 0) wred[0][wave] = wmax;
+  __syncthreads();
+  float m = wred[0][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmaxf(m, wred[0][w]);
+  const float e = tid < n ? expf(__fsub_rn(x, m)) : 0.f;
+  es[tid] = e;
+  const float wsum = WaveButterfly(e, [](float a, float b) { return __fadd_rn(a, b); });
+  if (lane == 0) wred[1][wave] = wsum;
+  __syncthreads();
+  // acc[d] over the split: thread (g, cq) adds positions g, g + 16, ... in order.
+  float acc[kCols] = {0.f, 0.f, 0.f, 0.f};
+  const float4 vn4 = reinterpret_cast<const float4*>(vnew)[cq];
+#pragma unroll
+  for (int i = 0; i < kPerGroup; ++i) {
+    const int t = g + i * kGroups;
+    if (t < n) {
+      const float ev = es[t];
+      const float4 v4 = t0 + t == position ? vn4 : vx[i];
+      acc[0] = __fadd_rn(acc[0], __fmul_rn(ev, v4.x));
+      acc[1] = __fadd_rn(acc[1], __fmul_rn(ev, v4.y));
+      acc[2] = __fadd_rn(acc[2], __fmul_rn(ev, v4.z));
+      acc[3] = __fadd_rn(acc[3], __fmul_rn(ev, v4.w));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) acc_part[g * kStepDim + cq * kCols + j] = acc[j];
+  __syncthreads();
+  if (tid < kStepDim) {
+    float o = acc_part[tid];
+    for (int gg = 1; gg < kGroups; ++gg) o = __fadd_rn(o, acc_part[gg * kStepDim + tid]);
+    mine[2 + tid] = o;
+  }
+  if (tid == 0) {
+    float l = wred[1][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) l = __fadd_rn(l, wred[1][w]);
+    mine[0] = m;
+    mine[1] = l;
+  }
+}
+
 constexpr int64_t kSplitMaxSeq = 4;
 
 }  // namespace
@@ -821,5 +983,37 @@ bool LaunchDecodeAttention(const float* q, const float* k, const float* v, float
   Check(hipGetLastError(), "DecodeAttentionKernel launch");
   return true;
 }
+
+
+int DecodeAttentionSplits(int64_t max_position) {
+  // A power of two (the combine's butterflies), at least 8, each split at most 256 positions.
+  const int64_t need = (max_position + 1 + kDecodeSplitRows - 1) / kDecodeSplitRows;
+  int64_t splits = kDecodeSplitMin;
+  while (splits < need) splits *= 2;
+  return splits > kDecodeSplitMax ? 0 : static_cast<int>(splits);
+}
+
+int LaunchDecodeSplitAttention(const float* q, const float* k, const float* v, float* k_cache, float* v_cache,
+                               const float* cos_table, const float* sin_table, int64_t position, int64_t heads,
+                               int64_t kv_heads, int64_t head_dim, hipStream_t stream, const int32_t* position_dev,
+                               int64_t max_position, float* partial, size_t partial_bytes) {
+  if (head_dim != kStepDim || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || partial == nullptr) return 0;
+  const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!aligned(k_cache) || !aligned(v_cache)) return 0;
+  const int64_t top = position_dev != nullptr ? max_position : position;
+  const int splits = DecodeAttentionSplits(top);
+  if (splits == 0 || heads > 65535 || (top + 1) * kv_heads * kStepDim > 0x7fffffff ||
+      heads * splits * (2 + kStepDim) > 0x7fffffff)
+    return 0;
+  if (partial_bytes < static_cast<size_t>(heads * splits * (2 + kStepDim)) * sizeof(float))
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "attention scratch is too small");
+  hipLaunchKernelGGL(DecodeSplitAttentionKernel, dim3(static_cast<uint32_t>(heads), static_cast<uint32_t>(splits)),
+                     dim3(kDecodeSplitThreads), 0, stream, q, k, v, k_cache, v_cache, cos_table, sin_table,
+                     static_cast<int32_t>(position), position_dev, static_cast<int32_t>(heads / kv_heads),
+                     static_cast<int32_t>(kv_heads), static_cast<int32_t>(splits), partial);
+  Check(hipGetLastError(), "DecodeSplitAttentionKernel launch");
+  return splits;
+}
+
 
 }  // namespace accel_hip

@@ -413,8 +413,9 @@ ACCEL_HIP_API int accel_hip_sample_token(AccelHipBuffer logits, AccelHipBuffer c
     if (draw) Check(hipMemcpyAsync(word, rng_state, sizeof(uint32_t), hipMemcpyHostToDevice, ctx.stream), "hipMemcpyAsync");
     if (draw) Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
     NoteDeviceWrite(static_cast<int32_t*>(chosen_ids.data) + chosen_index, sizeof(int32_t));
+    void* greedy = draw ? nullptr : Temp(kTempGreedy, GreedyWorkBytes(vocab));
     LaunchSampleToken(static_cast<const float*>(logits.data), static_cast<int32_t*>(chosen_ids.data) + chosen_index,
-                      vocab, temperature, word, top_k, ctx.stream);
+                      vocab, temperature, word, top_k, ctx.stream, nullptr, greedy, draw ? 0 : GreedyWorkBytes(vocab));
     if (draw) {
       Check(hipMemcpyAsync(rng_state, word, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx.stream), "hipMemcpyAsync");
       Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");

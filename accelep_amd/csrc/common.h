@@ -57,7 +57,8 @@ enum TempSlot {
   kTempArrivals = 3,
   kTempSplitA = 4,   // the bf16 GEMM's hi/mid/lo activation image
   kTempRowSums = 5,  // per-tile row sums of squares of a GEMM with a fused RMSNorm
-  kTempCount = 6
+  kTempGreedy = 6,   // the many-workgroup greedy pick's count and keys
+  kTempCount = 7
 };
 void* Temp(TempSlot slot, size_t bytes);
 // Bumped whenever the split-K workspace or a temporary buffer is replaced. A graph captured
@@ -238,8 +239,14 @@ struct GemvPrologue {
   // Used where the m = 1 entry kernel runs (even k <= 4096, x and w 8-byte aligned).
   bool rms_after = false;
   const float* silu_up = nullptr;
+  // Decode attention partials [k / 64 heads][attn_splits][2 + 64] (m, l, acc[64]) of
+  // LaunchDecodeSplitAttention: the input row is their combine, head h at rows 64h .. 64h + 63
+  // (the GEMV's `a` is not read).
+  const float* attn_partial = nullptr;
+  int32_t attn_splits = 0;
 };
 constexpr int64_t kGemvPrologueMaxK = 4096;
+constexpr int64_t kGemvAttnMaxPairs = 2048;  // heads x splits of GemvPrologue::attn_partial
 
 // C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV). With b.grouped (and no zero
 // points or per-row scale, k % 32 == 0, A 8-byte aligned) the split-bf16 MFMA kernel runs;
@@ -324,10 +331,28 @@ bool LaunchDecodeAttention(const float* q, const float* k, const float* v, float
                            int64_t heads, int64_t kv_heads, int64_t head_dim, hipStream_t stream,
                            const int32_t* position_dev, int64_t max_position, float* work, size_t work_bytes,
                            uint32_t* arrivals);
+// Fast mode, a decode row (seq 1) with head_dim 64: RoPE of q and k and the KV append as
+// LaunchDecodeAttention does, then per-split softmax partials into `partial`
+// [heads][splits][2 + 64] (m, l, acc) with no combine: the input prologue of the o-projection
+// GEMV (GemvPrologue::attn_partial) combines them. Returns the split count (a power of two
+// from 8 to 64, each split at most 256 positions; DecodeAttentionSplits(max position)), or 0,
+// launching nothing, when the sizes or the alignment do not fit.
+int LaunchDecodeSplitAttention(const float* q, const float* k, const float* v, float* k_cache, float* v_cache,
+                               const float* cos_table, const float* sin_table, int64_t position, int64_t heads,
+                               int64_t kv_heads, int64_t head_dim, hipStream_t stream, const int32_t* position_dev,
+                               int64_t max_position, float* partial, size_t partial_bytes);
+int DecodeAttentionSplits(int64_t max_position);
+// Partial bytes per head of the largest split count (64 splits of 2 + 64 floats).
+constexpr size_t kDecodeSplitMaxBytesPerHead = 64 * (2 + 64) * sizeof(float);
 // Scratch bytes LaunchAttention needs for these sizes (0 when none).
 size_t AttentionWorkBytes(int64_t seq, int64_t heads, int64_t max_position, int64_t head_dim);
 // rng_inout is a device word holding the xorshift32 state; index_dev offsets `chosen`.
+// greedy_work (at least GreedyWorkBytes(vocab) bytes, its first word zero and left zero by
+// each launch; launches sharing it must not overlap) lets a greedy pick run over many
+// workgroups; without it one workgroup scans the row.
 void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
-                       int32_t top_k, hipStream_t stream, const int32_t* index_dev = nullptr);
+                       int32_t top_k, hipStream_t stream, const int32_t* index_dev = nullptr,
+                       void* greedy_work = nullptr, size_t greedy_bytes = 0);
+size_t GreedyWorkBytes(int64_t vocab);
 
 }  // namespace accel_hip

@@ -102,4 +102,45 @@ __device__ __forceinline__ float ByteToFloat(uint32_t word, int b) {
   return static_cast<float>(static_cast<int32_t>(word << (24 - 8 * b)) >> 24);
 }
 
+__device__ __forceinline__ unsigned FloatBits(float x) { return __builtin_bit_cast(unsigned, x); }
+__device__ __forceinline__ float BitsFloat(unsigned x) { return __builtin_bit_cast(float, x); }
+// x from lane l ^ 8 (row_ror:8 inside each 16-lane row), l + 7 - 2 (l % 8) (row_half_mirror),
+// l ^ 2 and l ^ 1 (quad_perm).
+template <int kCtrl>
+__device__ __forceinline__ float Dpp(float x) {
+  return BitsFloat(static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(FloatBits(x)), kCtrl, 0xf, 0xf,
+                                                                     false)));
+}
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppQuadXor2 = 0x4e;  // quad_perm [2, 3, 0, 1]
+constexpr int kDppQuadXor1 = 0xb1;  // quad_perm [1, 0, 3, 2]
+
+// Sums one value per column over the 64 lanes of a wave: three halving exchanges leave lane l
+// with column (l >> 3) & 7 summed over its 8-lane group, three more finish the sum. The
+// exchanges are VALU lane moves (v_permlane32_swap between wave halves, v_permlane16_swap
+// between 16-lane rows, DPP inside a row), not LDS round trips. With A = column i and
+// B = column i + 4, the 32-lane swap leaves [A.lo, B.lo] and [A.hi, B.hi], whose sum holds
+// column i in the low half and column i + 4 in the high half; the 16-lane swap does the same
+// between rows 0/1 and 2/3.
+__device__ __forceinline__ float WaveColumnSum8(const float (&v8)[8], int lane) {
+  float v4[4], v2[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(FloatBits(v8[i]), FloatBits(v8[i + 4]), false, false);
+    v4[i] = BitsFloat(r[0]) + BitsFloat(r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(FloatBits(v4[i]), FloatBits(v4[i + 2]), false, false);
+    v2[i] = BitsFloat(r[0]) + BitsFloat(r[1]);
+  }
+  const bool h3 = lane & 8;
+  float v = (h3 ? v2[1] : v2[0]) + Dpp<kDppRowRor8>(h3 ? v2[0] : v2[1]);
+  v = v + Dpp<kDppRowHalfMirror>(v);
+  v = v + Dpp<kDppQuadXor2>(v);
+  v = v + Dpp<kDppQuadXor1>(v);
+  return v;
+}
+
 }  // namespace accel_hip

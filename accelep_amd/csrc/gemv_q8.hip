@@ -242,46 +242,6 @@ __device__ __forceinline__ void ComputeNarrowBatch(const NarrowBatch<M, U>& b, i
   }
 }
 
-__device__ __forceinline__ unsigned FloatBits(float x) { return __builtin_bit_cast(unsigned, x); }
-__device__ __forceinline__ float BitsFloat(unsigned x) { return __builtin_bit_cast(float, x); }
-// x from lane l ^ 8 (row_ror:8 inside each 16-lane row), l + 7 - 2 (l % 8) (row_half_mirror),
-// l ^ 2 and l ^ 1 (quad_perm).
-template <int kCtrl>
-__device__ __forceinline__ float Dpp(float x) {
-  return BitsFloat(static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(FloatBits(x)), kCtrl, 0xf, 0xf,
-                                                                     false)));
-}
-constexpr int kDppRowRor8 = 0x128;
-constexpr int kDppRowHalfMirror = 0x141;
-constexpr int kDppQuadXor2 = 0x4e;  // quad_perm [2, 3, 0, 1]
-constexpr int kDppQuadXor1 = 0xb1;  // quad_perm [1, 0, 3, 2]
-
-// Sums one value per column over the 64 lanes of a wave: three halving exchanges leave lane l
-// with column (l >> 3) & 7 summed over its 8-lane group, three more finish the sum. The
-// exchanges are VALU lane moves (v_permlane32_swap between wave halves, v_permlane16_swap
-// between 16-lane rows, DPP inside a row), not LDS round trips. With A = column i and
-// B = column i + 4, the 32-lane swap leaves [A.lo, B.lo] and [A.hi, B.hi], whose sum holds
-// column i in the low half and column i + 4 in the high half; the 16-lane swap does the same
-// between rows 0/1 and 2/3.
-__device__ __forceinline__ float WaveColumnSum8(const float (&v8)[kNarrowTile], int lane) {
-  float v4[4], v2[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const auto r = __builtin_amdgcn_permlane32_swap(FloatBits(v8[i]), FloatBits(v8[i + 4]), false, false);
-    v4[i] = BitsFloat(r[0]) + BitsFloat(r[1]);
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const auto r = __builtin_amdgcn_permlane16_swap(FloatBits(v4[i]), FloatBits(v4[i + 2]), false, false);
-    v2[i] = BitsFloat(r[0]) + BitsFloat(r[1]);
-  }
-  const bool h3 = lane & 8;
-  float v = (h3 ? v2[1] : v2[0]) + Dpp<kDppRowRor8>(h3 ? v2[0] : v2[1]);
-  v = v + Dpp<kDppRowHalfMirror>(v);
-  v = v + Dpp<kDppQuadXor2>(v);
-  v = v + Dpp<kDppQuadXor1>(v);
-  return v;
-}
 
 // Waves per SIMD the register budget must allow. For m = 1 with a per-column or whole-tensor
 // scale, no zero points and no input prologue, 7 (<= 72 VGPRs): the 1792 tiles of a 4096 x
@@ -300,6 +260,12 @@ constexpr int kAOpSiluUp = 2;
 // at once and the row's sum of squares is reduced beside them; each output is scaled by
 // 1/rms at the store. Rounding differs from the normalize-first order (fast mode only).
 constexpr int kAOpRmsAfter = 3;
+// The decode attention's split partials combined into the row (GemvPrologue::attn_partial).
+constexpr int kAOpAttn = 4;
+constexpr int kAttnDim = 64;
+constexpr int kAttnMaxPairs = static_cast<int>(kGemvAttnMaxPairs);  // the LDS weight table
+constexpr int kAttnRegSplits = 8;    // splits whose columns are loaded before the weights are known
+constexpr int kAttnRegRows = 4;      // rows per thread loaded that way (k <= 4 x threads)
 
 // Writes the transformed input row (kAOp) into a_stage; every thread of the workgroup takes
 // part and the row is complete when this returns.
@@ -307,7 +273,70 @@ template <int kAOp, int kThreads>
 __device__ __forceinline__ void StageInputRow(const GemvArgs& p, float* a_stage, double* part) {
   const int tid = threadIdx.x;
   const int k32 = static_cast<int>(p.k);
-  if (kAOp == kAOpRms) {
+  if (kAOp == kAOpAttn) {
+    // Row i = 64 h + d is sum_s w_hs acc_hs[d] / sum_s w_hs l_hs, with
+    // w_hs = e^(m_hs - max_s m_hs) (0 for an empty split); the acc sum runs over the splits in
+    // order, the l sum as a butterfly. The first kAttnRegSplits columns of this thread's first
+    // kAttnRegRows rows are loaded with the (m, l) pairs, in the same round.
+    __shared__ float wts[kAttnMaxPairs];
+    __shared__ float total_l[kGemvPrologueMaxK / kAttnDim];
+    const int splits = p.pro.attn_splits;
+    const int heads = k32 / kAttnDim;
+    const float* part_base = p.pro.attn_partial;
+    constexpr int kStride = 2 + kAttnDim;
+    float xs[kAttnRegRows][kAttnRegSplits];
+#pragma unroll
+    for (int r = 0; r < kAttnRegRows; ++r) {
+      // Rows past k read the last row (unused): the loads need no branches.
+      const int i = min(tid + r * kThreads, k32 - 1);
+      const int hh = i / kAttnDim;
+      const int d = i % kAttnDim;
+#pragma unroll
+      for (int sp = 0; sp < kAttnRegSplits; ++sp)  // splits >= kAttnRegSplits (launcher)
+        xs[r][sp] = part_base[(hh * splits + sp) * kStride + 2 + d];
+    }
+    // Lane pr = h * splits + s holds split s of head h; splits is a power of two <= 64
+    // (launcher), so a head's splits are whole lane groups of one wave and its max and sum
+    // are butterflies over them (every lane of the group gets the same bits).
+    for (int pr0 = 0; pr0 < heads * splits; pr0 += kThreads) {  // uniform over the workgroup
+      const int pr = pr0 + tid;
+      const bool live = pr < heads * splits;
+      const float mv = live ? part_base[pr * kStride] : -INFINITY;
+      const float lv = live ? part_base[pr * kStride + 1] : 0.f;
+      float big = mv;
+      for (int off = 1; off < splits; off <<= 1) big = fmaxf(big, __shfl_xor(big, off));
+      const float w = mv == -INFINITY ? 0.f : expf(__fsub_rn(mv, big));
+      float l = __fmul_rn(w, lv);
+      for (int off = 1; off < splits; off <<= 1) l = __fadd_rn(l, __shfl_xor(l, off));
+      if (live) {
+        wts[pr] = w;
+        if (pr % splits == 0) total_l[pr / splits] = l;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kAttnRegRows; ++r) {
+      const int i = tid + r * kThreads;
+      if (i < k32) {
+        const int hh = i / kAttnDim;
+        const float* w = wts + hh * splits;
+        float o = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < kAttnRegSplits; ++sp) o = __fadd_rn(o, __fmul_rn(w[sp], xs[r][sp]));
+        for (int sp = kAttnRegSplits; sp < splits; ++sp)
+          o = __fadd_rn(o, __fmul_rn(w[sp], part_base[(hh * splits + sp) * kStride + 2 + i % kAttnDim]));
+        a_stage[i] = __fdiv_rn(o, total_l[hh]);
+      }
+    }
+    for (int i = tid + kAttnRegRows * kThreads; i < k32; i += kThreads) {
+      const int hh = i / kAttnDim;
+      const float* w = wts + hh * splits;
+      float o = 0.f;
+      for (int sp = 0; sp < splits; ++sp)
+        o = __fadd_rn(o, __fmul_rn(w[sp], part_base[(hh * splits + sp) * kStride + 2 + i % kAttnDim]));
+      a_stage[i] = __fdiv_rn(o, total_l[hh]);
+    }
+  } else if (kAOp == kAOpRms) {
     double ss = 0.0;
     for (int i = tid; i < k32; i += kThreads) {
       const double v = static_cast<double>(p.a[i]);
@@ -470,7 +499,8 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   using S = NarrowShape<1>;
   static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
   __shared__ float red[S::kWaves][kNarrowTile];
-  __shared__ __align__(16) float a_stage[kAOp == kAOpRms ? kGemvPrologueMaxK : 1];  // the staged row
+  // The staged input row.
+  __shared__ __align__(16) float a_stage[kAOp == kAOpRms || kAOp == kAOpAttn ? kGemvPrologueMaxK : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -1033,6 +1063,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                   hipStream_t stream, const GemvPrologue* prologue) {
   if (m < 1 || m > 16 || k < 1 || n < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV shape out of range");
   int a_op = prologue == nullptr                                        ? kAOpNone
+                   : prologue->attn_partial != nullptr                     ? kAOpAttn
                    : prologue->rms_weight != nullptr && prologue->rms_after ? kAOpRmsAfter
                    : prologue->rms_weight != nullptr                       ? kAOpRms
                    : prologue->silu_up != nullptr                          ? kAOpSiluUp
@@ -1041,6 +1072,11 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   if (a_op != kAOpNone && (m != 1 || b.tiled == nullptr || b.zero != nullptr || b.mode == kScalePerRow ||
                            k > kGemvPrologueMaxK))
     Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV input prologue needs m = 1, staged tiles, no zero points, k <= 4096");
+  if (a_op == kAOpAttn && (k % kAttnDim != 0 || prologue->attn_splits < kAttnRegSplits ||
+                           prologue->attn_splits > 64 || (prologue->attn_splits & (prologue->attn_splits - 1)) != 0 ||
+                           (k / kAttnDim) * prologue->attn_splits > kAttnMaxPairs))
+    Fail(ACCEL_HIP_INVALID_ARGUMENT,
+         "GEMV attention prologue needs k = 64 x heads, 8 .. 64 splits (a power of two), heads x splits <= 2048");
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // The narrow kernel reads the staged column tiles (and indexes rows in 32 bits); without
@@ -1126,11 +1162,13 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                           : a_op == kAOpRmsAfter
                               ? pair_a && reinterpret_cast<uintptr_t>(prologue->rms_weight) % 8 == 0
                           : a_op == kAOpSiluUp ? pair_a && reinterpret_cast<uintptr_t>(prologue->silu_up) % 8 == 0
-                                               : k % 2 == 0;
+                                               : k % 2 == 0;  // kAOpRms, kAOpAttn: the row is staged in LDS
     const bool m1 = m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
                     n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
                     epi.rms_weight == nullptr;
     if (!m1 && a_op == kAOpRmsAfter) a_op = kAOpRms;  // the general kernel normalizes first
+    if (!m1 && a_op == kAOpAttn)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV attention prologue needs the m = 1 kernel (per-column or tensor scale)");
     if (m1) {
       const int steps = static_cast<int>((k + NarrowShape<1>::kStepRows - 1) / NarrowShape<1>::kStepRows);
       const bool clamp = k != steps * NarrowShape<1>::kStepRows;
@@ -1146,6 +1184,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
 #define ACCEL_GEMV_M1(ST, CL)                                                               \
   do {                                                                                      \
     if (a_op == kAOpRms) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRms);                           \
+    else if (a_op == kAOpAttn) ACCEL_GEMV_M1_K(ST, CL, false, kAOpAttn);                    \
     else if (a_op == kAOpRmsAfter) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRmsAfter);            \
     else if (a_op == kAOpSiluUp) ACCEL_GEMV_M1_K(ST, CL, false, kAOpSiluUp);                \
     else if (plain) ACCEL_GEMV_M1_K(ST, CL, true, kAOpNone);                                \

@@ -125,12 +125,14 @@ struct Model {
   bool decode_graph_exact = false;
   bool decode_warm = false;
   // Decode-row fusions (accel_llama_set_fused_inputs): bit 0, RMSNorm and SiLU*up inside the
-  // next GEMV; bit 1, RoPE + KV append + attention + combine as one kernel.
-  int32_t fuse = 3;
+  // next GEMV; bit 1, RoPE + KV append + attention + combine as one kernel; bit 2 (fast mode,
+  // over bit 1), the attention in fixed splits whose partials the o-projection GEMV combines.
+  int32_t fuse = 7;
   // Attention partials of a decode step ([heads][context / 64 chunks][2 + head_dim]): owned
   // here so a captured step never points into a workspace that later grows.
   DevBuf attn_work;
   DevBuf attn_arrivals;  // uint32 per head, zero between decode attention launches
+  DevBuf greedy_work;    // the greedy pick's count (zero between launches) and keys
 
   void DropDecodeGraph() {
     if (decode_graph != nullptr) accel_hip_graph_destroy(decode_graph);
@@ -180,6 +182,12 @@ struct Model {
   static constexpr int64_t kFusedNormMaxOut = 8192;
   bool Fusable(const Linear& w, int64_t m) const {
     return (fuse & 1) != 0 && m == 1 && !w.q.empty() && !Ctx().exact_products && w.in <= kGemvPrologueMaxK;
+  }
+  // The o-projection may read the split attention's partials (fuse bit 2).
+  bool SplitAttention(const Linear& o) const {
+    return (fuse & 4) != 0 && !o.q.empty() && !Ctx().exact_products && o.in <= kGemvPrologueMaxK &&
+           o.in == static_cast<int64_t>(cfg.heads) * head_dim &&
+           static_cast<int64_t>(cfg.heads) * DecodeAttentionSplits(cfg.context - 1) <= kGemvAttnMaxPairs;
   }
   void ApplyPrologue(const Linear& w, const float* x, float* c, const Epilogue& e, const GemvPrologue& pro) {
     Context& ctx = Ctx();
@@ -255,6 +263,22 @@ struct Model {
       float* kc = k_cache[static_cast<size_t>(li)].as<float>();
       float* vc = v_cache[static_cast<size_t>(li)].as<float>();
       ApplyNormed(l.qkv, hidden.as<float>(), l.attn_norm, query.as<float>(), seq, qkv);
+      const int splits =
+          seq == 1 && SplitAttention(l.o)
+              ? LaunchDecodeSplitAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
+                                           rope_cos.as<float>(), rope_sin.as<float>(), pos, cfg.heads, cfg.kv_heads,
+                                           hd, s, state, cfg.context - 1, attn_work.as<float>(),
+                                           attn_work.buffer().bytes)
+              : 0;
+      if (splits > 0) {
+        GemvPrologue pro;
+        pro.attn_partial = attn_work.as<float>();
+        pro.attn_splits = splits;
+        ApplyPrologue(l.o, attn_work.as<float>(), hidden.as<float>(), residual, pro);
+        ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
+        ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
+        continue;
+      }
       if (seq != 1 || (fuse & 2) == 0 || !LaunchDecodeAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
                                              rope_cos.as<float>(), rope_sin.as<float>(), mixed.as<float>(), pos,
                                              cfg.heads, cfg.kv_heads, hd, s, state, cfg.context - 1,
@@ -330,7 +354,7 @@ struct Model {
     for (int32_t step = 0; step < max_new; ++step) {
       if (produced >= cfg.context) Fail(ACCEL_HIP_INVALID_ARGUMENT, "generation exceeded the token buffer");
       LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
-                        state + 1);
+                        state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
       produced += 1;
       if (eos_id >= 0) {
         // Only an eos id needs the chosen id on the host before the next step.
@@ -556,8 +580,11 @@ ACCEL_LLAMA_API AccelLlama* accel_llama_create(const AccelLlamaConfig* config) {
     m->chosen = DevBuf(ctx * sizeof(int32_t));
     m->prompt_ids = DevBuf(ctx * sizeof(int32_t));
     m->words = DevBuf(64);
-    m->attn_work = DevBuf(AttentionWorkBytes(1, config->heads, config->context - 1, dim));
+    // Room for the chunk partials and for the fixed-split partials of the decode attention.
+    m->attn_work = DevBuf(std::max(AttentionWorkBytes(1, config->heads, config->context - 1, dim),
+                                   static_cast<size_t>(config->heads) * kDecodeSplitMaxBytesPerHead));
     m->attn_arrivals = DevBuf(static_cast<size_t>(config->heads) * sizeof(uint32_t));
+    m->greedy_work = DevBuf(GreedyWorkBytes(config->vocab));
     for (int32_t l = 0; l < config->layers; ++l) {
       m->k_cache.emplace_back(k_n * f);
       m->v_cache.emplace_back(k_n * f);
@@ -711,7 +738,7 @@ ACCEL_LLAMA_API int accel_llama_set_fused_inputs(AccelLlama* handle, int32_t ena
     return 1;
   }
   return Run([&] {
-    if (enable < 0 || enable > 3) Fail(ACCEL_HIP_INVALID_ARGUMENT, "fused inputs: enable must be 0 .. 3");
+    if (enable < 0 || enable > 7) Fail(ACCEL_HIP_INVALID_ARGUMENT, "fused inputs: enable must be 0 .. 7");
     std::lock_guard<std::mutex> lock(m->mu);
     if (m->fuse != enable) m->DropDecodeGraph();  // the graph holds the other kernels
     m->fuse = enable;

@@ -292,10 +292,101 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* logits, in
   if (tid == 0) *chosen = static_cast<int32_t>(pick);
 }
 
+// ---- greedy over many workgroups ----------------------------------------------------------
+// Each workgroup takes 2048 ids (two 16-byte pieces per thread) and keeps the largest key
+//   key(v, i) = OrderKey(v == 0 ? +0 : v) << 32 | (2^32 - 1 - i),   0 for a NaN,
+// so the largest key is the largest value, the earliest id among equal values (-0 equals +0),
+// and NaNs never win: the reference's strict > scan, whose answer is 0 when id 0 holds a NaN
+// (checked by the last workgroup). Thread 0 of each workgroup stores its key to part[b]
+// (device scope), then counts its arrival with a device-scope acquire-release add: the
+// release orders the key before the count, and in the workgroup whose add completes the
+// grid the acquire, followed by the workgroup barrier, orders every thread's device-scope
+// reads of part[] after all the keys. That workgroup picks the largest key, writes the id and
+// sets the count back to zero for the next launch (launches on one stream are ordered).
+constexpr int kGreedyThreads = 256;
+constexpr int kGreedyIds = 2048;  // ids per workgroup
+constexpr int kGreedyMaxBlocks = 1024;
+
+__device__ __forceinline__ uint64_t GreedyKey(float v, uint32_t i) {
+  if (isnan(v)) return 0;
+  const float c = v == 0.f ? 0.f : v;
+  return (static_cast<uint64_t>(OrderKey(c)) << 32) | static_cast<uint64_t>(0xffffffffu - i);
+}
+
+__device__ uint64_t BlockMaxKey(uint64_t k, uint64_t* sk) {
+  k = max(k, XorLane<32>(k));
+  k = max(k, XorLane<16>(k));
+  k = max(k, XorLane<8>(k));
+  k = max(k, XorLane<4>(k));
+  k = max(k, XorLane<2>(k));
+  k = max(k, XorLane<1>(k));
+  if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = k;
+  __syncthreads();
+  uint64_t r = sk[0];
+  for (int w = 1; w < kGreedyThreads / 64; ++w) r = max(r, sk[w]);
+  return r;
+}
+
+__global__ __launch_bounds__(kGreedyThreads) void GreedyKernel(const float* logits, int32_t* chosen, int32_t vocab,
+                                                               const int32_t* index_dev, uint64_t* part,
+                                                               uint32_t* count) {
+  __shared__ uint64_t sk[kGreedyThreads / 64];
+  __shared__ int is_last;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const float4* l4 = reinterpret_cast<const float4*>(logits);
+  const int n4 = vocab / 4;  // vocab % 4 == 0 (launcher)
+  uint64_t best = 0;
+#pragma unroll
+  for (int j = 0; j < kGreedyIds / 4 / kGreedyThreads; ++j) {
+    const int i4 = b * (kGreedyIds / 4) + j * kGreedyThreads + tid;
+    if (i4 < n4) {
+      const float4 v = l4[i4];
+      const uint32_t i0 = 4u * static_cast<uint32_t>(i4);
+      best = max(best, GreedyKey(v.x, i0));
+      best = max(best, GreedyKey(v.y, i0 + 1));
+      best = max(best, GreedyKey(v.z, i0 + 2));
+      best = max(best, GreedyKey(v.w, i0 + 3));
+    }
+  }
+  best = BlockMaxKey(best, sk);
+  if (tid == 0) {
+    __hip_atomic_store(&part[b], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  uint64_t k = 0;
+  for (int i = tid; i < static_cast<int>(gridDim.x); i += kGreedyThreads)
+    k = max(k, __hip_atomic_load(&part[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  __syncthreads();  // sk is reused
+  k = BlockMaxKey(k, sk);
+  if (tid == 0) {
+    const int32_t id = (k == 0 || isnan(logits[0])) ? 0 : static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k));
+    chosen[index_dev != nullptr ? *index_dev : 0] = id;
+    __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 }  // namespace
 
+size_t GreedyWorkBytes(int64_t vocab) {
+  return 64 + static_cast<size_t>((vocab + kGreedyIds - 1) / kGreedyIds) * sizeof(uint64_t);
+}
+
 void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, float temperature, uint32_t* rng_inout,
-                       int32_t top_k, hipStream_t stream, const int32_t* index_dev) {
+                       int32_t top_k, hipStream_t stream, const int32_t* index_dev, void* greedy_work,
+                       size_t greedy_bytes) {
+  const int64_t blocks = (vocab + kGreedyIds - 1) / kGreedyIds;
+  if (!(temperature > 0.f) && greedy_work != nullptr && greedy_bytes >= GreedyWorkBytes(vocab) && blocks > 1 &&
+      blocks <= kGreedyMaxBlocks && vocab % 4 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0) {
+    uint32_t* count = static_cast<uint32_t*>(greedy_work);
+    uint64_t* part = reinterpret_cast<uint64_t*>(static_cast<char*>(greedy_work) + 64);
+    hipLaunchKernelGGL(GreedyKernel, dim3(static_cast<uint32_t>(blocks)), dim3(kGreedyThreads), 0, stream, logits,
+                       chosen, static_cast<int32_t>(vocab), index_dev, part, count);
+    Check(hipGetLastError(), "GreedyKernel launch");
+    return;
+  }
   hipLaunchKernelGGL(SampleKernel, dim3(1), dim3(kThreads), 0, stream, logits, chosen, vocab, temperature, rng_inout,
                      top_k, index_dev);
   Check(hipGetLastError(), "SampleKernel launch");

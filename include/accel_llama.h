@@ -77,10 +77,13 @@ ACCEL_LLAMA_API int accel_llama_logit_max_abs(AccelLlama* model, const float* re
 /* Uncounted read of the logit row (no reference counterpart; for tests). */
 ACCEL_LLAMA_API int accel_llama_logits(AccelLlama* model, float* out, int32_t count);
 /* No reference counterpart (a test seam) for a one-row (decode) forward. enable is a bit
- * mask, default 3. Bit 0: the RMSNorms and SiLU*up run inside the next int8 GEMV (the norm is
+ * mask, default 7. Bit 0: the RMSNorms and SiLU*up run inside the next int8 GEMV (the norm is
  * applied to the product's sums, which rounds differently from normalizing first) instead of
  * as separate kernels. Bit 1: RoPE + KV append, attention and chunk combine run as one kernel
- * instead of three (same bits). Values outside 0 .. 3 are an invalid argument. */
+ * instead of three (same bits). Bit 2 (not in exact-products mode; over bit 1): the attention
+ * runs in a fixed number of position splits and the o-projection GEMV combines their partials
+ * in its input prologue (softmax sums in another order: rounding only). Values outside
+ * 0 .. 7 are an invalid argument. */
 ACCEL_LLAMA_API int accel_llama_set_fused_inputs(AccelLlama* model, int32_t enable);
 ACCEL_LLAMA_API void accel_llama_reset(AccelLlama* model);
 ACCEL_LLAMA_API const char* accel_llama_last_error(void);

@@ -152,13 +152,16 @@ def test_matmul_probes_and_zero_k():
 
 
 @pytest.mark.parametrize("m,k,n", [(256, 1024, 4096), (256, 4096, 1024), (77, 300, 129), (1, 576, 49), (64, 64, 64),
-                                   (128, 4096, 256), (64, 512, 64), (64, 2048, 192), (128, 1536, 128), (64, 1088, 704)])
+                                   (128, 4096, 256), (64, 512, 64), (64, 2048, 192), (128, 1536, 128), (64, 1088, 704),
+                                   (1024, 2048, 1024)])
 def test_matmul_against_oracle(m, k, n):
-    """fp32 GEMM. The 64 x 64 wave-split kernel takes small full-tile grids: 16 groups per wave
-    unrolled (256 x 1024 x 4096), with K also split over workgroups and combined by the last to
-    arrive (256 x 4096 x 1024: 4 splits; 128 x 4096 x 256: 4; 64 x 2048 x 192: 2), and the
-    looped form (64 x 512 x 64: 8 groups; 128 x 1536 x 128: 24). The LDS kernel takes the rest.
-    Every element within 2 gamma_K of the float64 product."""
+    """fp32 GEMM. The 64 x 64 wave-split kernel (4 waves, each over a quarter of the
+    workgroup's K) takes small full-tile grids: 16 groups per wave unrolled (256 x 1024 x 4096;
+    and, with K also split over workgroups and summed by SplitReduceKernel, 256 x 4096 x 1024
+    and 128 x 4096 x 256 in 4 splits, 64 x 2048 x 192 in 2), and the looped form
+    (64 x 512 x 64: 8 groups; 128 x 1536 x 128: 24; 1024 x 2048 x 1024: 32). The LDS kernel
+    takes the rest (ragged shapes, K not a multiple of 256). Every element within 2 gamma_K of
+    the float64 product."""
     r = np.random.default_rng(m * 7 + k)
     a = r.standard_normal((m, k)).astype(np.float32)
     b = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
@@ -715,3 +718,49 @@ def test_sampling_reference_fixtures(gold):
     want_states = gold["sample_rng_after"]
     mism = [i for i in range(len(ids)) if ids[i] != want_ids[i] or states[i] != want_states[i]]
     assert not mism, f"{len(mism)} sampling cases differ, first {mism[:5]}"
+
+
+def _greedy_cases():
+    r = np.random.default_rng(77)
+    v = 49152
+    base = lambda: r.standard_normal(v).astype(np.float32)
+    x = base()
+    yield "random", x
+    x = base(); top = float(x.max()) + 1.0
+    x[[40000, 3001, 3000, 17000]] = top  # equal maxima in three workgroups: the earliest id wins
+    yield "ties", x
+    x = -np.abs(base()) - 1.0
+    x[30000], x[5000] = 0.0, -0.0  # -0 equals +0: the earlier id wins
+    yield "signed_zero", x
+    x = base(); x[0] = np.nan
+    yield "nan_at_0", x
+    x = base(); x[[1, 2048, 40000]] = np.nan; x[9999] = 50.0
+    yield "nan_elsewhere", x
+    x = np.full(v, np.nan, np.float32); x[0] = -3.0
+    yield "all_nan_but_0", x
+    yield "all_neg_inf", np.full(v, -np.inf, np.float32)
+    x = base(); x[-1] = np.inf
+    yield "inf_last", x
+    x = r.standard_normal(49156).astype(np.float32)  # a partial last workgroup
+    x[49155] = 99.0
+    yield "ragged_tail", x
+    yield "odd_vocab", r.standard_normal(4097).astype(np.float32)  # one-workgroup path
+
+
+@pytest.mark.parametrize("name", [n for n, _ in _greedy_cases()])
+def test_greedy_pick_matches_oracle(name):
+    """Greedy SampleToken (temperature 0) over a 49152-id row runs on many workgroups, each
+    reducing 2048 ids to an order-preserving key, the last to arrive picking the largest. Its
+    id must equal the reference's strict > scan (the oracle's orc_sample_token): the earliest
+    id among equal maxima, -0 equal to +0, NaNs never chosen, 0 when id 0 holds a NaN. Two
+    launches in a row check that the arrival count is left at zero."""
+    x = dict(_greedy_cases())[name]
+    want, _ = oracle().sample_token(x, 0.0, 1, 0)
+    lg = dev(x)
+    chosen = dev(np.full(2, -1, np.int32))
+    for _ in range(2):
+        st = C.c_uint32(1)
+        check(lib().accel_hip_sample_token(lg.buffer, chosen.buffer, 1, x.size, 0.0, C.byref(st), 0))
+        got = int(chosen.numpy()[1])
+        print(f"greedy {name}: gpu {got} oracle {want}", flush=True)
+        assert got == want

@@ -188,23 +188,28 @@ def _decode_row_logits(eng, cfg, prompt, fuse):
 @pytest.mark.parametrize("count", [9, 64, 65, 150, 8250])
 def test_decode_row_fused_kernels_match_separate_passes(count):
     """A one-row forward runs RoPE, the KV append, the chunked attention and its combine as one
-    kernel: the logits must carry exactly the bits of the three-kernel forward. With the
-    RMSNorms and SiLU*up inside the GEMVs as well (the norm applied to the sums) they agree to
-    rounding and pick the same id. The prompt lengths put the new position inside the first
-    64-position chunk, at its last slot, at the first slot of the second, in a third chunk,
-    and in the 129th."""
+    kernel (mask 2): the logits must carry exactly the bits of the three-kernel forward (mask 0).
+    With the RMSNorms and SiLU*up inside the GEMVs as well (mask 3, the norm applied to the
+    sums), and with the attention in fixed splits combined inside the o-projection GEMV (mask 4
+    alone, and 7, the default), they agree to rounding and pick the same id. The prompt
+    lengths put the new position inside the first 64-position chunk (and leave three of the
+    eight splits empty), at its last slot, at the first slot of the second, in a third chunk,
+    and in the 129th (64 splits of 129 positions)."""
     cfg = dict(llama_config("smol3"), layers=2, context=max(160, count + 16))
     w, q = llama_weights(cfg, 103)
     prompt = np.random.default_rng(5).integers(0, cfg["vocab"], size=count).astype(np.int32)
     eng = Engine(cfg, w, q)
     try:
-        rows = {fuse: _decode_row_logits(eng, cfg, prompt, fuse) for fuse in (0, 2, 3)}
-        assert np.isfinite(rows[3]).all()
+        rows = {fuse: _decode_row_logits(eng, cfg, prompt, fuse) for fuse in (0, 2, 3, 4, 7)}
         np.testing.assert_array_equal(rows[2].view(np.uint32), rows[0].view(np.uint32))
-        np.testing.assert_allclose(rows[3], rows[0], rtol=1e-4, atol=1e-4)
-        assert int(np.argmax(rows[3])) == int(np.argmax(rows[0]))
-        assert eng.L.accel_llama_set_fused_inputs(eng.h, 4) == 1
-        assert b"enable must be 0 .. 3" in eng.L.accel_llama_last_error()
+        for fuse in (3, 4, 7):
+            assert np.isfinite(rows[fuse]).all()
+            err = float(np.abs(rows[fuse] - rows[0]).max())
+            print(f"count {count} mask {fuse}: max|logit - separate passes| = {err:.3g}", flush=True)
+            np.testing.assert_allclose(rows[fuse], rows[0], rtol=1e-4, atol=1e-4)
+            assert int(np.argmax(rows[fuse])) == int(np.argmax(rows[0]))
+        assert eng.L.accel_llama_set_fused_inputs(eng.h, 8) == 1
+        assert b"enable must be 0 .. 7" in eng.L.accel_llama_last_error()
     finally:
         eng.close()
 
