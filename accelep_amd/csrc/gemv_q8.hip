@@ -263,9 +263,42 @@ constexpr int kAOpRmsAfter = 3;
 // The decode attention's split partials combined into the row (GemvPrologue::attn_partial).
 constexpr int kAOpAttn = 4;
 constexpr int kAttnDim = 64;
-constexpr int kAttnMaxPairs = static_cast<int>(kGemvAttnMaxPairs);  // the LDS weight table
-constexpr int kAttnRegSplits = 8;    // splits whose columns are loaded before the weights are known
-constexpr int kAttnRegRows = 4;      // rows per thread loaded that way (k <= 4 x threads)
+constexpr int kAttnMaxPairs = static_cast<int>(kGemvAttnMaxPairs);
+constexpr int kAttnRegSplits = 8;  // splits loaded with the weights; more are read after them
+
+// Rows (d, d + 1) of head hh from the split partials [heads][splits][2 + 64]: with ml[s] =
+// (m_s, l_s) and ac[s] = (acc_s[d], acc_s[d + 1]) of the first kAttnRegSplits splits already
+// loaded, w_s = e^(m_s - max m) (0 for an empty split, m_s = -inf), and the pair is
+// (sum_s w_s acc_s) / (sum_s w_s l_s), every sum in split order. Each lane forms the weights
+// of its own head; all lanes of all workgroups form them alike, so they agree bit for bit.
+__device__ __forceinline__ void AttnCombinePair(const float* part, int splits, int hh, int d,
+                                                const float2 (&ml)[kAttnRegSplits],
+                                                const float2 (&ac)[kAttnRegSplits], float& a0, float& a1) {
+  constexpr int kStride = 2 + kAttnDim;
+  const float* head = part + hh * splits * kStride;
+  float big = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < kAttnRegSplits; ++sp) big = fmaxf(big, ml[sp].x);
+  for (int sp = kAttnRegSplits; sp < splits; ++sp) big = fmaxf(big, head[sp * kStride]);
+  float l = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < kAttnRegSplits; ++sp) {
+    const float w = ml[sp].x == -INFINITY ? 0.f : expf(__fsub_rn(ml[sp].x, big));
+    l = __fadd_rn(l, __fmul_rn(w, ml[sp].y));
+    o0 = __fadd_rn(o0, __fmul_rn(w, ac[sp].x));
+    o1 = __fadd_rn(o1, __fmul_rn(w, ac[sp].y));
+  }
+  for (int sp = kAttnRegSplits; sp < splits; ++sp) {
+    const float2 m2 = *reinterpret_cast<const float2*>(head + sp * kStride);
+    const float2 x2 = *reinterpret_cast<const float2*>(head + sp * kStride + 2 + d);
+    const float w = m2.x == -INFINITY ? 0.f : expf(__fsub_rn(m2.x, big));
+    l = __fadd_rn(l, __fmul_rn(w, m2.y));
+    o0 = __fadd_rn(o0, __fmul_rn(w, x2.x));
+    o1 = __fadd_rn(o1, __fmul_rn(w, x2.y));
+  }
+  a0 = __fdiv_rn(o0, l);
+  a1 = __fdiv_rn(o1, l);
+}
 
 // Writes the transformed input row (kAOp) into a_stage; every thread of the workgroup takes
 // part and the row is complete when this returns.
@@ -273,70 +306,7 @@ template <int kAOp, int kThreads>
 __device__ __forceinline__ void StageInputRow(const GemvArgs& p, float* a_stage, double* part) {
   const int tid = threadIdx.x;
   const int k32 = static_cast<int>(p.k);
-  if (kAOp == kAOpAttn) {
-    // Row i = 64 h + d is sum_s w_hs acc_hs[d] / sum_s w_hs l_hs, with
-    // w_hs = e^(m_hs - max_s m_hs) (0 for an empty split); the acc sum runs over the splits in
-    // order, the l sum as a butterfly. The first kAttnRegSplits columns of this thread's first
-    // kAttnRegRows rows are loaded with the (m, l) pairs, in the same round.
-    __shared__ float wts[kAttnMaxPairs];
-    __shared__ float total_l[kGemvPrologueMaxK / kAttnDim];
-    const int splits = p.pro.attn_splits;
-    const int heads = k32 / kAttnDim;
-    const float* part_base = p.pro.attn_partial;
-    constexpr int kStride = 2 + kAttnDim;
-    float xs[kAttnRegRows][kAttnRegSplits];
-#pragma unroll
-    for (int r = 0; r < kAttnRegRows; ++r) {
-      // Rows past k read the last row (unused): the loads need no branches.
-      const int i = min(tid + r * kThreads, k32 - 1);
-      const int hh = i / kAttnDim;
-      const int d = i % kAttnDim;
-#pragma unroll
-      for (int sp = 0; sp < kAttnRegSplits; ++sp)  // splits >= kAttnRegSplits (launcher)
-        xs[r][sp] = part_base[(hh * splits + sp) * kStride + 2 + d];
-    }
-    // Lane pr = h * splits + s holds split s of head h; splits is a power of two <= 64
-    // (launcher), so a head's splits are whole lane groups of one wave and its max and sum
-    // are butterflies over them (every lane of the group gets the same bits).
-    for (int pr0 = 0; pr0 < heads * splits; pr0 += kThreads) {  // uniform over the workgroup
-      const int pr = pr0 + tid;
-      const bool live = pr < heads * splits;
-      const float mv = live ? part_base[pr * kStride] : -INFINITY;
-      const float lv = live ? part_base[pr * kStride + 1] : 0.f;
-      float big = mv;
-      for (int off = 1; off < splits; off <<= 1) big = fmaxf(big, __shfl_xor(big, off));
-      const float w = mv == -INFINITY ? 0.f : expf(__fsub_rn(mv, big));
-      float l = __fmul_rn(w, lv);
-      for (int off = 1; off < splits; off <<= 1) l = __fadd_rn(l, __shfl_xor(l, off));
-      if (live) {
-        wts[pr] = w;
-        if (pr % splits == 0) total_l[pr / splits] = l;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kAttnRegRows; ++r) {
-      const int i = tid + r * kThreads;
-      if (i < k32) {
-        const int hh = i / kAttnDim;
-        const float* w = wts + hh * splits;
-        float o = 0.f;
-#pragma unroll
-        for (int sp = 0; sp < kAttnRegSplits; ++sp) o = __fadd_rn(o, __fmul_rn(w[sp], xs[r][sp]));
-        for (int sp = kAttnRegSplits; sp < splits; ++sp)
-          o = __fadd_rn(o, __fmul_rn(w[sp], part_base[(hh * splits + sp) * kStride + 2 + i % kAttnDim]));
-        a_stage[i] = __fdiv_rn(o, total_l[hh]);
-      }
-    }
-    for (int i = tid + kAttnRegRows * kThreads; i < k32; i += kThreads) {
-      const int hh = i / kAttnDim;
-      const float* w = wts + hh * splits;
-      float o = 0.f;
-      for (int sp = 0; sp < splits; ++sp)
-        o = __fadd_rn(o, __fmul_rn(w[sp], part_base[(hh * splits + sp) * kStride + 2 + i % kAttnDim]));
-      a_stage[i] = __fdiv_rn(o, total_l[hh]);
-    }
-  } else if (kAOp == kAOpRms) {
+  if (kAOp == kAOpRms) {
     double ss = 0.0;
     for (int i = tid; i < k32; i += kThreads) {
       const double v = static_cast<double>(p.a[i]);
@@ -499,8 +469,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   using S = NarrowShape<1>;
   static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
   __shared__ float red[S::kWaves][kNarrowTile];
-  // The staged input row.
-  __shared__ __align__(16) float a_stage[kAOp == kAOpRms || kAOp == kAOpAttn ? kGemvPrologueMaxK : 1];
+  __shared__ __align__(16) float a_stage[kAOp == kAOpRms ? kGemvPrologueMaxK : 1];  // the staged row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -546,6 +515,32 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
         b.a[u][0][0] = __fmul_rn(__fdiv_rn(xv[u].x, __fadd_rn(1.f, expf(-xv[u].x))), wv[u].x);
         b.a[u][0][1] = __fmul_rn(__fdiv_rn(xv[u].y, __fadd_rn(1.f, expf(-xv[u].y))), wv[u].y);
       }
+    }
+  } else if (kAOp == kAOpAttn) {
+    // The attention combine per lane (AttnCombinePair): its pairs' partials are loaded with
+    // the weights, so the row costs no extra memory round and no barrier.
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    constexpr int kStride = 2 + kAttnDim;
+    const int splits = pro.attn_splits;
+    float2 ml[kSteps][kAttnRegSplits], ac[kSteps][kAttnRegSplits];
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+      const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole, in one head
+      const float* head = pro.attn_partial + (rp / kAttnDim) * splits * kStride;
+#pragma unroll
+      for (int sp = 0; sp < kAttnRegSplits; ++sp) {
+        ml[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride);
+        ac[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride + 2 + rp % kAttnDim);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+      const int rp = !kClamp || r < k - 2 ? r : k - 2;
+      AttnCombinePair(pro.attn_partial, splits, rp / kAttnDim, rp % kAttnDim, ml[u], ac[u], b.a[u][0][0],
+                      b.a[u][0][1]);
     }
   } else {
 #pragma unroll
@@ -1073,10 +1068,9 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                            k > kGemvPrologueMaxK))
     Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV input prologue needs m = 1, staged tiles, no zero points, k <= 4096");
   if (a_op == kAOpAttn && (k % kAttnDim != 0 || prologue->attn_splits < kAttnRegSplits ||
-                           prologue->attn_splits > 64 || (prologue->attn_splits & (prologue->attn_splits - 1)) != 0 ||
                            (k / kAttnDim) * prologue->attn_splits > kAttnMaxPairs))
     Fail(ACCEL_HIP_INVALID_ARGUMENT,
-         "GEMV attention prologue needs k = 64 x heads, 8 .. 64 splits (a power of two), heads x splits <= 2048");
+         "GEMV attention prologue needs k = 64 x heads, at least 8 splits and heads x splits <= 2048");
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // The narrow kernel reads the staged column tiles (and indexes rows in 32 bits); without
@@ -1162,7 +1156,9 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                           : a_op == kAOpRmsAfter
                               ? pair_a && reinterpret_cast<uintptr_t>(prologue->rms_weight) % 8 == 0
                           : a_op == kAOpSiluUp ? pair_a && reinterpret_cast<uintptr_t>(prologue->silu_up) % 8 == 0
-                                               : k % 2 == 0;  // kAOpRms, kAOpAttn: the row is staged in LDS
+                          : a_op == kAOpAttn
+                              ? k % 2 == 0 && reinterpret_cast<uintptr_t>(prologue->attn_partial) % 8 == 0
+                              : k % 2 == 0;  // kAOpRms: the row is staged in LDS
     const bool m1 = m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
                     n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
                     epi.rms_weight == nullptr;
