@@ -393,7 +393,7 @@ void Launch(const GemmArgs& args, bool q8, dim3 grid, hipStream_t stream) {
 //    B[kb + 4q + s][4(lane % 16) .. + 3], whose element j is its B operand for column tile j,
 //    so MFMA column c of tile j is the tile's column 4c + j. The product sums every k of the
 //    group once, in another order; 8 loads feed 64 MFMAs;
-//  * operands of the next two groups are in flight while one group's 64 MFMAs run;
+//  * operands of the next three groups are in flight while one group's 64 MFMAs run;
 //  * the four wave partials meet in LDS and are added in wave order; a K split across
 //    workgroups (for grids with fewer tiles than CUs) goes through the workspace and
 //    SplitReduceKernel, as above. (Combining the splits in the last workgroup to arrive, with

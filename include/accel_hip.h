@@ -128,8 +128,12 @@ ACCEL_HIP_API int accel_hip_matmul(AccelHipBuffer a, AccelHipBuffer b, AccelHipB
                                    int64_t n);
 /* accel::MatMulQuantized (include/accel/runtime.h:124-125; src/sim_device.cc:541-602).
  * Device pointers; a NULL plane reads the float pointer. Either side may be quantized.
- * w = (float(q) - float(zero)) * scale at the plane's coordinate. int8 GEMV for m <= 16,
- * fp32 MFMA GEMM with the int8 panel dequantized in LDS above that. */
+ * w = (float(q) - float(zero)) * scale at the plane's coordinate. m <= 16: the int8 GEMV
+ * (VALU for m <= 2, exact bf16-split products on the matrix cores for 3 <= m <= 16). Above
+ * that, an int8 weight with per-column or whole-tensor scale, no zero points and k % 32 == 0
+ * runs on the bf16 matrix cores with the activation split exactly into three bf16 parts (the
+ * weight staged once as bf16); other planes on the fp32 MFMA GEMM with the int8 panel
+ * dequantized in LDS. */
 ACCEL_HIP_API int accel_hip_matmul_quantized(const float* a, const AccelHipQuantPlane* a_quant, const float* b,
                                              const AccelHipQuantPlane* b_quant, float* c, int64_t m, int64_t k,
                                              int64_t n);
@@ -137,8 +141,8 @@ ACCEL_HIP_API int accel_hip_matmul_quantized(const float* a, const AccelHipQuant
  * arithmetic). When on, every matmul entry point sums each output in k order from zero with
  * each product rounded before its add, and dequantizes an int8 operand per element as
  * (float(q) - float(zero)) * scale: the bits of ReferenceMatMul / MatMulQuantized
- * (src/sim_device.cc:387-402,541-602). When off (the default) the MFMA GEMM and the VALU
- * GEMV add in their own order: within 2*gamma_K*(|A|@|B|) of the exact product. Process-wide;
+ * (src/sim_device.cc:387-402,541-602). When off (the default) the GEMMs and GEMVs add in
+ * their own order: within 2*gamma_K*(|A|@|B|) of the exact product. Process-wide;
  * accel_hip_exact_products() reads the setting (1 on, 0 off). */
 ACCEL_HIP_API int accel_hip_set_exact_products(int32_t on);
 ACCEL_HIP_API int32_t accel_hip_exact_products(void);
