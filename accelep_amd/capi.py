@@ -80,6 +80,8 @@ SIGNATURES = {
     "accel_hip_matmul_quantized_fused_noalloc": (C.c_int, [C.c_void_p, C.POINTER(QuantPlane), C.c_void_p,
                                                            C.POINTER(QuantPlane), C.c_void_p, i64, i64, i64,
                                                            C.POINTER(Epilogue)]),
+    "accel_hip_prepare_quantized": (C.c_int, [C.POINTER(QuantPlane), i64, i64, C.c_uint32,
+                                              C.POINTER(C.c_uint32)]),
     "accel_hip_transpose": (C.c_int, [Buffer, Buffer, i64, i64]),
     "accel_hip_gemm_epilogue": (C.c_int, [Buffer, i64, i64, C.c_float, C.POINTER(Buffer), C.c_int32, I64P,
                                           C.c_float, C.c_int32]),

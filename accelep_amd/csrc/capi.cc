@@ -225,6 +225,56 @@ ACCEL_HIP_API int accel_hip_matmul_quantized_fused(const float* a, const AccelHi
   });
 }
 
+// Weight preparation: the staged copies of an int8 weight built now instead of at first use.
+ACCEL_HIP_API int accel_hip_prepare_quantized(const AccelHipQuantPlane* b_quant, int64_t k, int64_t n,
+                                              uint32_t layouts, uint32_t* staged) {
+  return Guard([&] {
+    if (staged != nullptr) *staged = 0;
+    if (b_quant == nullptr || k < 0 || n < 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare needs a quant plane and k, n >= 0");
+    if ((layouts & ~static_cast<uint32_t>(ACCEL_HIP_STAGE_ALL)) != 0)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: unknown layout bits");
+    CheckPlane(b_quant, "B");
+    RefuseInCapture("preparing staged weight copies");
+    if (k * n == 0) return;
+    Q8View view;
+    if (!PlaneView(*b_quant, k, n, &view)) {
+      if (layouts != 0)
+        Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: this plane's scale coordinates fit no staged form (it is dequantized per call)");
+      return;
+    }
+    const bool groups_ok = k % kGemvGroupRows == 0 && view.zero == nullptr &&
+                           (view.mode == kScalePerCol || view.mode == kScaleConst);
+    const bool bf16_ok = GemmBf16Stageable(k, n, view);
+    const uint32_t want = layouts != 0 ? layouts
+                                       : ACCEL_HIP_STAGE_GEMV_TILES | (groups_ok ? ACCEL_HIP_STAGE_GEMV_GROUPS : 0u) |
+                                             (bf16_ok ? ACCEL_HIP_STAGE_GEMM_BF16 : 0u);
+    if ((want & ACCEL_HIP_STAGE_GEMV_GROUPS) != 0 && !groups_ok)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the group-interleaved copy needs k % 32 == 0, no zero points and a "
+                                       "per-column or whole-tensor scale");
+    if ((want & ACCEL_HIP_STAGE_GEMM_BF16) != 0 && !bf16_ok)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the bf16 copy needs k % 32 == 0, k >= 64, n % 8 == 0, no zero points "
+                                       "and a per-column or whole-tensor scale");
+    const hipStream_t s = Ctx().stream;
+    const auto built = [](const void* p) {
+      if (p == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the weight is not inside a live allocation of this library");
+    };
+    uint32_t done = 0;
+    if ((want & ACCEL_HIP_STAGE_GEMV_TILES) != 0) {
+      built(StagedColumnTiles(view.q, k, n, s));
+      done |= ACCEL_HIP_STAGE_GEMV_TILES;
+    }
+    if ((want & ACCEL_HIP_STAGE_GEMV_GROUPS) != 0) {
+      built(StagedGroupTiles(view.q, k, n, s));
+      done |= ACCEL_HIP_STAGE_GEMV_GROUPS;
+    }
+    if ((want & ACCEL_HIP_STAGE_GEMM_BF16) != 0) {
+      built(StagedBf16Image(view.q, k, n, s));
+      done |= ACCEL_HIP_STAGE_GEMM_BF16;
+    }
+    if (staged != nullptr) *staged = done;
+  });
+}
+
 // Device::Transpose (src/sim_device.cc:198-209).
 ACCEL_HIP_API int accel_hip_transpose(AccelHipBuffer src, AccelHipBuffer dst, int64_t rows, int64_t cols) {
   return Guard([&] {

@@ -179,6 +179,9 @@ const void* StagedBf16Image(const int8_t* q, int64_t k, int64_t n, hipStream_t s
 void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream);
 // Whether the int8-weight GEMM runs this product from a staged bf16 copy (the caller stages it).
 bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v);
+// Whether a weight of this form can have the staged bf16 copy at all (GemmWantsBf16Image
+// without the grid condition on m).
+bool GemmBf16Stageable(int64_t k, int64_t n, const Q8View& v);
 // Whether LaunchGemvQ8 takes an m-row product with this k and weight view from the
 // group-interleaved copy (the caller stages that copy instead of the 8-column tiles).
 constexpr int64_t kGemvGroupMinM = 3;

@@ -635,9 +635,13 @@ void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_
   Check(hipGetLastError(), "TileBf16Kernel launch");
 }
 
-bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v) {
+bool GemmBf16Stageable(int64_t k, int64_t n, const Q8View& v) {
   if (v.q == nullptr || v.zero != nullptr || (v.mode != kScalePerCol && v.mode != kScaleConst)) return false;
-  if (m < 1 || k < 2 * kBK || n < 8 || k % kBK != 0 || n % 8 != 0 || k / kBK > 0x7fffffff) return false;
+  return k >= 2 * kBK && n >= 8 && k % kBK == 0 && n % 8 == 0 && k / kBK <= 0x7fffffff;
+}
+
+bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v) {
+  if (m < 1 || !GemmBf16Stageable(k, n, v)) return false;
   Context& ctx = Ctx();
   const int64_t cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
   return ((m + 127) / 128) * ((n + 127) / 128) >= cus;  // the 128-tile grid, no K split

@@ -495,6 +495,9 @@ void UploadPart(const Part& p, bool int8, const void* block, const float* scale)
   NoteBytesToDevice(static_cast<size_t>(p.in * p.width) * elem);
   if (int8) NoteBytesToDevice(static_cast<size_t>(p.width) * sizeof(float));
   w.filled |= 1u << p.index;
+  // A complete int8 projection gets its decode GEMV tiles now, at load, not in the first step.
+  if (int8 && w.ready() && StagedColumnTiles(w.q.as<int8_t>(), w.in, w.out, s) == nullptr)
+    Fail(ACCEL_HIP_RUNTIME_ERROR, "staging a projection's GEMV tiles failed");
 }
 
 DevBuf* NormSlot(Model& m, int32_t kind, int32_t layer) {

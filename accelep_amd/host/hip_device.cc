@@ -226,6 +226,19 @@ void HipMatMulQuantizedFused(const float* a, const QuantPlane* a_quant, const fl
   NoteKernelMatmul();
 }
 
+void HipPrepareQuantized(const QuantPlane& weight) {
+  if (weight.shape.size() < 2) throw std::invalid_argument("prepare needs a matrix weight");
+  const int64_t k = weight.shape[weight.shape.size() - 2];
+  const int64_t n = weight.shape.back();
+  int64_t batches = 1;
+  for (size_t d = 0; d + 2 < weight.shape.size(); ++d) batches *= weight.shape[d];
+  AccelHipQuantPlane plane = ToHip(weight);
+  for (int64_t b = 0; b < batches; ++b) {
+    plane.offset = weight.offset + b * k * n;
+    Check(accel_hip_prepare_quantized(&plane, k, n, 0, nullptr));
+  }
+}
+
 void HipSynchronize() { Check(accel_hip_synchronize()); }
 
 void HipSetExactProducts(bool on) { Check(accel_hip_set_exact_products(on ? 1 : 0)); }

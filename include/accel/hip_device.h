@@ -40,6 +40,11 @@ void HipMatMulFused(Device& device, DeviceBuffer a, DeviceBuffer b, DeviceBuffer
 void HipMatMulQuantizedFused(const float* a, const QuantPlane* a_quant, const float* b, const QuantPlane* b_quant,
                              float* c, int64_t m, int64_t k, int64_t n, const FusedEpilogue& epilogue);
 
+// Builds the staged copies MatMulQuantized reads for this int8 weight now (every layout its
+// form allows; each batch matrix of a plane of rank > 2), instead of at the weight's first
+// use: for BindConstant (src/ep.cc:1430-1463), outside any graph capture.
+void HipPrepareQuantized(const QuantPlane& weight);
+
 // Waits until every kernel the library has launched has finished.
 void HipSynchronize();
 

@@ -137,6 +137,21 @@ ACCEL_HIP_API int accel_hip_matmul(AccelHipBuffer a, AccelHipBuffer b, AccelHipB
 ACCEL_HIP_API int accel_hip_matmul_quantized(const float* a, const AccelHipQuantPlane* a_quant, const float* b,
                                              const AccelHipQuantPlane* b_quant, float* c, int64_t m, int64_t k,
                                              int64_t n);
+/* Weight preparation. No counterpart in the reference, whose MatMulQuantized dequantizes each
+ * panel on the fly (src/sim_device.cc:541-602); it belongs where the reference uploads and
+ * binds the weight (UploadDequantized and BindConstant, src/ep.cc:843-900,1430-1463). Builds
+ * now, on the library stream, the staged copies of the int8 weight b_quant ([k, n] at its
+ * offset) that the matmuls otherwise build at the weight's first use: layouts is a mask of
+ * ACCEL_HIP_STAGE_*, 0 for every layout this plane's form allows. A copy lasts until the
+ * weight's allocation is freed or written. Refused (ACCEL_HIP_RUNTIME_ERROR) during a graph
+ * capture; ACCEL_HIP_INVALID_ARGUMENT for a layout the plane cannot take or a weight outside
+ * this library's heap. *staged (if not NULL) receives the layouts built. */
+#define ACCEL_HIP_STAGE_GEMV_TILES 1u  /* 8-column tiles: the int8 GEMV at m <= 2 (m <= 4 otherwise) */
+#define ACCEL_HIP_STAGE_GEMV_GROUPS 2u /* group-interleaved tiles: the bf16-split GEMV, 3 <= m <= 16 */
+#define ACCEL_HIP_STAGE_GEMM_BF16 4u   /* bf16 in MFMA operand order: the int8-weight GEMM, m > 16 */
+#define ACCEL_HIP_STAGE_ALL 7u
+ACCEL_HIP_API int accel_hip_prepare_quantized(const AccelHipQuantPlane* b_quant, int64_t k, int64_t n,
+                                              uint32_t layouts, uint32_t* staged);
 /* Exact products (no reference counterpart as a switch; it selects the reference's own
  * arithmetic). When on, every matmul entry point sums each output in k order from zero with
  * each product rounded before its add, and dequantizes an int8 operand per element as

@@ -77,6 +77,7 @@ CPP_API = [
     "accel::ResetAcceleratorStats()", "accel::NoteConstantTouch(", "accel::ConstantTouchCount()",
     "accel::AppendProfileRecord(", "accel::WriteProfile(", "accel::KvTableStore::Create(", "accel::OwnedBuffer::Reset()",
     "accel::ActivationName(", "accel::HipMatMulFused(", "accel::HipMatMulQuantizedFused(", "accel::IsHipDevice(",
+    "accel::HipPrepareQuantized(",
 ]
 
 

@@ -182,3 +182,85 @@ def test_capture_inside_capture_is_refused():
     assert rc == RUNTIME_ERROR and "already" in msg
     with pytest.raises(HipError):
         check(L.accel_hip_graph_launch(None, 1))
+
+
+INVALID_ARGUMENT = 1
+STAGE_TILES, STAGE_GROUPS, STAGE_BF16 = 1, 2, 4
+
+
+def _prepare(plane, k, n, layouts=0):
+    staged = C.c_uint32(0xFFFF)
+    rc = lib().accel_hip_prepare_quantized(C.byref(plane), k, n, layouts, C.byref(staged))
+    return rc, staged.value
+
+
+def test_prepared_weight_can_be_captured():
+    """accel_hip_prepare_quantized builds a weight's staged copies before any use. A capture
+    of GEMVs on it (m = 1 on the 8-column tiles, m = 4 on the group-interleaved copy) then
+    records, and three replays, each after eager work of its own, store the eager call's
+    bits."""
+    L = lib()
+    k, n = 576, 1536
+    g1 = _gemv(1, k, n, 31)
+    g4 = dict(_gemv(4, k, n, 31))
+    g4["qd"], g4["sd"], g4["plane"] = g1["qd"], g1["sd"], g1["plane"]  # the same weight
+    rc, staged = _prepare(g1["plane"], k, n)
+    assert rc == 0, L.accel_hip_last_error()
+    assert staged == STAGE_TILES | STAGE_GROUPS | STAGE_BF16
+    check(_call(g1))
+    check(_call(g4))
+    eager1, eager4 = g1["out"].numpy().copy(), g4["out"].numpy().copy()
+    assert_gamma_bound(eager1, g1["a"], g1["w"])
+    assert_gamma_bound(eager4, g4["a"], g1["w"])
+    g1["out"].upload(np.zeros((1, n), np.float32))
+    g4["out"].upload(np.zeros((4, n), np.float32))
+    print("capture after prepare", flush=True)
+    check(L.accel_hip_capture_begin())
+    try:
+        rc1, rc4 = _call(g1), _call(g4)
+    finally:
+        graph = _end_capture()
+    try:
+        assert (rc1, rc4) == (0, 0), L.accel_hip_last_error()
+        scratch = dev(np.zeros(1024, np.float32))
+        for rep in range(3):
+            g1["out"].upload(np.zeros((1, n), np.float32))
+            g4["out"].upload(np.zeros((4, n), np.float32))
+            check(L.accel_hip_graph_launch(graph, 1))
+            check(L.accel_hip_residual_add(scratch.buffer, scratch.buffer, 1024))  # eager work between replays
+            same_bits(g1["out"].numpy(), eager1)
+            same_bits(g4["out"].numpy(), eager4)
+    finally:
+        check(L.accel_hip_graph_destroy(graph))
+
+
+def test_prepare_reports_and_refuses():
+    """Layouts a plane cannot take are refused by name; a plane with zero points still gets
+    its 8-column tiles; inside a capture the call is refused and enqueues nothing."""
+    L = lib()
+    k, n = 64, 96
+    r = np.random.default_rng(5)
+    q = dev(r.integers(-127, 128, size=k * n, dtype=np.int8))
+    s = dev(r.uniform(1e-3, 1e-2, size=n).astype(np.float32))
+    z = dev(r.integers(-3, 4, size=n, dtype=np.int8))
+    plain = quant_plane(q, s, None, [k, n], 1)
+    zero = quant_plane(q, s, z, [k, n], 1)
+    assert _prepare(plain, k, n, STAGE_TILES) == (0, STAGE_TILES)
+    assert _prepare(zero, k, n) == (0, STAGE_TILES)
+    rc, _ = _prepare(zero, k, n, STAGE_GROUPS)
+    assert rc == INVALID_ARGUMENT and b"group-interleaved" in L.accel_hip_last_error()
+    rc, _ = _prepare(zero, k, n, STAGE_BF16)
+    assert rc == INVALID_ARGUMENT and b"bf16 copy" in L.accel_hip_last_error()
+    rc, _ = _prepare(plain, k, n, 8)
+    assert rc == INVALID_ARGUMENT and b"unknown layout" in L.accel_hip_last_error()
+    rc, _ = _prepare(plain, 60, n, STAGE_GROUPS)  # k % 32 != 0
+    assert rc == INVALID_ARGUMENT
+    check(L.accel_hip_capture_begin())
+    try:
+        rc, staged = _prepare(plain, k, n)
+        msg = L.accel_hip_last_error()
+    finally:
+        graph = _end_capture()
+        check(L.accel_hip_graph_destroy(graph))
+    assert rc == RUNTIME_ERROR and staged == 0, msg
+    assert _prepare(plain, k, n) == (0, STAGE_TILES | STAGE_GROUPS | STAGE_BF16)
