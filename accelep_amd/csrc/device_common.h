@@ -98,6 +98,16 @@ __device__ __forceinline__ T WaveButterfly(T x, Op op) {
 }
 
 // Signed byte b of a dword to float, exact.
+// Workgroup barrier that orders LDS only: each wave's LDS reads and writes before it are
+// complete and visible to the workgroup after it. Unlike __syncthreads (whose workgroup
+// release also waits for the wave's global loads), loads issued for later iterations stay in
+// flight across it. For loops whose waves exchange data through LDS alone.
+__device__ __forceinline__ void LdsBarrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float ByteToFloat(uint32_t word, int b) {
   return static_cast<float>(static_cast<int32_t>(word << (24 - 8 * b)) >> 24);
 }

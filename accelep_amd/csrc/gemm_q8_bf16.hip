@@ -266,7 +266,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 
           __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
         }
       }
-      __syncthreads();
+      LdsBarrier();  // the panels in flight for later chunks stay in flight
     }
   }
 
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       ComputeImageChunk<kSwz>(lds + (u % 2) * kImgBlockWords, breg[u % kNB], lane, wm, acc, acc_ml);
       StoreImageA(lds + ((u + 1) % 2) * kImgBlockWords, tid, areg[(u + 1) % 2]);
       LoadImageB(p, cb0, min(ch + kNB, chunks - 1), lane, breg[u % kNB]);
-      __syncthreads();
+      LdsBarrier();  // the A blocks and B operands in flight for later chunks stay in flight
     }
   }
 
