@@ -9,9 +9,12 @@
 // constant float weight as an on-device OwnedBuffer, runtime inputs as host pointers. The step
 // sequences are RunKernel's (src/ep.cc:1602-1650): plain, has_rms (ExecuteMatMul retaining the
 // pre-norm sum, RmsNorm into the next input) and has_skip (ExecuteMatMul, then ResidualAdd of
-// the held sum and NoteAddEpilogue). Every input is small integers or halves, so every product
-// and sum is exact in fp32 and the expected values are exact; the one full-size product (the
-// decode GEMV shape) is checked against Higham's gamma_K bound.
+// the held sum and NoteAddEpilogue), and a leading-dynamic MatMul's runtime batch (src/ep.cc:
+// 418-486,1546-1593) with float and int8 weights, batched B and FusedMatMul's transposes. Every
+// input is small integers or halves, so every product and sum is exact in fp32 and the expected
+// values are exact; the one full-size product (the decode GEMV shape) is checked against
+// Higham's gamma_K bound.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -307,6 +310,88 @@ void TestDecodeGemvShape(accel::Device& device) {
   }
 }
 
+// A leading-dynamic MatMul (src/ep.cc:418-486): RunKernel checks the runtime shapes against the
+// compiled contract (:1546-1593) and hands the runtime batch to ExecuteMatMul as the leading
+// dimension of A. The same constant weight serves three batch sizes, as an on-device float
+// weight and as an int8 plane with power-of-two column scales; then a batched B (one matrix per
+// batch) and FusedMatMul's trans_a / trans_b / alpha on batched operands. Small integers and
+// halves keep every product and sum exact.
+void TestLeadingBatchAndTrans(accel::Device& device) {
+  const int64_t k = 48, n = 20, rows = 5;
+  std::vector<float> wf(static_cast<size_t>(k * n));
+  std::vector<int8_t> w8(static_cast<size_t>(k * n));
+  std::vector<float> scale(static_cast<size_t>(n));
+  for (int64_t i = 0; i < k * n; ++i) {
+    wf[i] = static_cast<float>((i * 7 + 3) % 7 - 3);
+    w8[i] = static_cast<int8_t>((i * 5 + 1) % 17 - 8);
+  }
+  for (int64_t j = 0; j < n; ++j) scale[j] = (j % 2 == 0) ? 0.5f : 0.25f;
+  std::vector<float> wq(static_cast<size_t>(k * n));
+  for (int64_t i = 0; i < k * n; ++i) wq[i] = static_cast<float>(w8[i]) * scale[i % n];
+  accel::OwnedBuffer wd = Upload(device, wf.data(), wf.size() * sizeof(float), {k, n});
+  accel::OwnedBuffer q = Upload(device, w8.data(), w8.size(), {k, n});
+  accel::OwnedBuffer s = Upload(device, scale.data(), scale.size() * sizeof(float), {n});
+  accel::Operand bq;
+  bq.quant = true;
+  bq.shape = {k, n};
+  bq.quant_plane.q = static_cast<const int8_t*>(q.buffer.data);
+  bq.quant_plane.scale = static_cast<const float*>(s.buffer.data);
+  bq.quant_plane.shape = {k, n};
+  bq.quant_plane.axis = 1;
+  for (const int64_t batch : {3, 1, 2}) {
+    std::vector<float> a(static_cast<size_t>(batch * rows * k));
+    for (size_t i = 0; i < a.size(); ++i) a[i] = 0.5f * static_cast<float>(static_cast<int64_t>(i * 11 + batch) % 9 - 4);
+    std::vector<float> y(static_cast<size_t>(batch * rows * n), 7.f);
+    accel::ExecuteMatMul(device, Host(a, {batch, rows, k}), OnDevice(wd), y.data());
+    EXPECT_EXACT(y, HostMatMul(a, wf, batch * rows, k, n));
+    std::fill(y.begin(), y.end(), 7.f);
+    accel::ExecuteMatMul(device, Host(a, {batch, rows, k}), bq, y.data());
+    EXPECT_EXACT(y, HostMatMul(a, wq, batch * rows, k, n));
+  }
+  // Batched B: [2, 4, 16] @ [2, 16, 8], one matrix per batch.
+  {
+    const int64_t bb = 2, m = 4, kk = 16, nn = 8;
+    std::vector<float> a(static_cast<size_t>(bb * m * kk)), b(static_cast<size_t>(bb * kk * nn));
+    for (size_t i = 0; i < a.size(); ++i) a[i] = static_cast<float>(static_cast<int64_t>(i * 3) % 7 - 3);
+    for (size_t i = 0; i < b.size(); ++i) b[i] = static_cast<float>(static_cast<int64_t>(i * 5) % 9 - 4);
+    std::vector<float> y(static_cast<size_t>(bb * m * nn), 7.f), want;
+    accel::ExecuteMatMul(device, Host(a, {bb, m, kk}), Host(b, {bb, kk, nn}), y.data());
+    for (int64_t t = 0; t < bb; ++t) {
+      const std::vector<float> at(a.begin() + t * m * kk, a.begin() + (t + 1) * m * kk);
+      const std::vector<float> bt(b.begin() + t * kk * nn, b.begin() + (t + 1) * kk * nn);
+      const std::vector<float> c = HostMatMul(at, bt, m, kk, nn);
+      want.insert(want.end(), c.begin(), c.end());
+    }
+    EXPECT_EXACT(y, want);
+  }
+  // FusedMatMul, batched A stored [2, k, m] with trans_a, B stored [n, k] with trans_b,
+  // alpha 0.5: Y[t] = 0.5 * A[t]^T @ B^T.
+  {
+    const int64_t bb = 2, m = 6, kk = 12, nn = 10;
+    std::vector<float> a(static_cast<size_t>(bb * kk * m)), b(static_cast<size_t>(nn * kk));
+    for (size_t i = 0; i < a.size(); ++i) a[i] = static_cast<float>(static_cast<int64_t>(i * 7) % 11 - 5);
+    for (size_t i = 0; i < b.size(); ++i) b[i] = static_cast<float>(static_cast<int64_t>(i * 3) % 5 - 2);
+    accel::FusedMatMulConfig cfg;
+    cfg.trans_a = true;
+    cfg.trans_b = true;
+    cfg.alpha = 0.5f;
+    std::vector<float> y(static_cast<size_t>(bb * m * nn), 7.f), want;
+    accel::ExecuteFusedMatMul(device, Host(a, {bb, kk, m}), Host(b, {nn, kk}), cfg, accel::Activation::None, y.data());
+    std::vector<float> bt(static_cast<size_t>(kk * nn));
+    for (int64_t r = 0; r < nn; ++r)
+      for (int64_t c = 0; c < kk; ++c) bt[c * nn + r] = b[r * kk + c];
+    for (int64_t t = 0; t < bb; ++t) {
+      std::vector<float> at(static_cast<size_t>(m * kk));
+      for (int64_t r = 0; r < kk; ++r)
+        for (int64_t c = 0; c < m; ++c) at[c * kk + r] = a[t * kk * m + r * m + c];
+      std::vector<float> c = HostMatMul(at, bt, m, kk, nn);
+      for (float& v : c) v *= 0.5f;
+      want.insert(want.end(), c.begin(), c.end());
+    }
+    EXPECT_EXACT(y, want);
+  }
+}
+
 }  // namespace
 
 int main() {
@@ -317,6 +402,7 @@ int main() {
     TestStepSequences(*device);
     TestGemmAndFused(*device);
     TestDecodeGemvShape(*device);
+    TestLeadingBatchAndTrans(*device);
     EXPECT(accel::LiveDeviceAllocs() == live);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "FAIL: exception %s\n", e.what());
