@@ -526,14 +526,17 @@ def main():
         per, gbs = bench_gemv(hip, 1, args.steps, args.warmup, 1, rng)
         secondary["gemv_m1_cache_warm"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
                                            "note": "one weight copy, L2/MALL may serve it; not HBM-honest"}
-        steps2 = max(10, args.steps // 4)
-        per, tf = bench_mlp(hip, steps2, max(1, args.warmup // 4), rng)
+        # The GEMM legs time at least 20 launches after at least 5 untimed ones, whatever
+        # --steps is: a leg that follows the memory-bound GEMV legs runs its first launches
+        # while the clocks settle.
+        steps2 = max(20, args.steps // 4)
+        per, tf = bench_mlp(hip, steps2, max(5, args.warmup // 4), rng)
         secondary["mlp_fp32"] = {"ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
                                  "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "steps": steps2,
                                  "config": "X[256,1024] Gemm1024x4096+bias+gelu, Gemm4096x1024+bias+residual"}
         log(f"mlp fp32: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
-        steps4 = max(10, args.steps // 20)
-        per, tf = bench_prefill(hip, steps4, max(1, args.warmup // 20), rng)
+        steps4 = max(20, args.steps // 20)
+        per, tf = bench_prefill(hip, steps4, max(5, args.warmup // 20), rng)
         secondary["prefill_int8_rmsnorm"] = {
             "ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
             "vs_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
