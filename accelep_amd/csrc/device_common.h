@@ -20,9 +20,11 @@ __device__ __forceinline__ int64_t BiasIndex(const Epilogue& e, int64_t i, int64
 // The reference's epilogue steps with their roundings (src/sim_device.cc:229-241,
 // src/runtime.cc:332-344): v = alpha*acc; v = v + beta*bias; relu keeps NaN and -0
 // (replaces only v < 0); gelu = (0.5*v) * (1 + erf(v*0.70710678)); then the residual.
-__device__ __forceinline__ float ApplyEpilogue(float acc, int64_t i, int64_t j, int64_t n, const Epilogue& e) {
+// bias_v and res_v are the element's bias and residual values, already loaded (read only
+// when the epilogue has a bias or residual).
+__device__ __forceinline__ float ApplyEpilogueLoaded(float acc, const Epilogue& e, float bias_v, float res_v) {
   float v = __fmul_rn(e.alpha, acc);
-  if (e.bias != nullptr) v = __fadd_rn(v, __fmul_rn(e.beta, e.bias[BiasIndex(e, i, j)]));
+  if (e.bias != nullptr) v = __fadd_rn(v, __fmul_rn(e.beta, bias_v));
   if (e.activation == ACCEL_HIP_ACT_RELU) {
     if (v < 0.f) v = 0.f;
   } else if (e.activation == ACCEL_HIP_ACT_GELU) {
@@ -30,8 +32,14 @@ __device__ __forceinline__ float ApplyEpilogue(float acc, int64_t i, int64_t j, 
     const float arg = __fmul_rn(v, 0.7071067811865476f);
     v = __fmul_rn(half, __fadd_rn(1.f, erff(arg)));
   }
-  if (e.residual != nullptr) v = __fadd_rn(v, e.residual[i * n + j]);
+  if (e.residual != nullptr) v = __fadd_rn(v, res_v);
   return v;
+}
+
+__device__ __forceinline__ float ApplyEpilogue(float acc, int64_t i, int64_t j, int64_t n, const Epilogue& e) {
+  const float bias_v = e.bias != nullptr ? e.bias[BiasIndex(e, i, j)] : 0.f;
+  const float res_v = e.residual != nullptr ? e.residual[i * n + j] : 0.f;
+  return ApplyEpilogueLoaded(acc, e, bias_v, res_v);
 }
 
 // Stores output element (i, j) of an [m, n] product, following the epilogue's column split.

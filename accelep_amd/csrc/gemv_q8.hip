@@ -595,18 +595,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     if (kPlain) {
       c[col] = x;
     } else {
-      // ApplyEpilogue's steps and roundings, with the bias and residual already loaded.
-      float y = __fmul_rn(epi.alpha, x);
-      if (epi.bias != nullptr) y = __fadd_rn(y, __fmul_rn(epi.beta, bias_v));
-      if (epi.activation == ACCEL_HIP_ACT_RELU) {
-        if (y < 0.f) y = 0.f;
-      } else if (epi.activation == ACCEL_HIP_ACT_GELU) {
-        const float half = __fmul_rn(0.5f, y);
-        const float arg = __fmul_rn(y, 0.7071067811865476f);
-        y = __fmul_rn(half, __fadd_rn(1.f, erff(arg)));
-      }
-      if (epi.residual != nullptr) y = __fadd_rn(y, res_v);
-      StoreC(c, 0, col, n, epi, y);
+      StoreC(c, 0, col, n, epi, ApplyEpilogueLoaded(x, epi, bias_v, res_v));
     }
   }
 }
