@@ -414,27 +414,32 @@ struct ImageArgs {
   Epilogue epi;
 };
 
-__device__ __forceinline__ void LoadImageA(const ImageArgs& p, int64_t a_block, int ch, int tid, u32x4 (&r)[6]) {
+// One chunk's image block, copied by kNT threads (kImgBlockVecs / kNT 16-byte pieces each).
+template <int kNT>
+__device__ __forceinline__ void LoadImageA(const ImageArgs& p, int64_t a_block, int ch, int tid,
+                                           u32x4 (&r)[kImgBlockVecs / kNT]) {
   const u32x4* src = p.a_img + (a_block + ch) * kImgBlockVecs;
 #pragma unroll
-  for (int i = 0; i < 6; ++i) r[i] = src[i * kThreads + tid];
+  for (int i = 0; i < kImgBlockVecs / kNT; ++i) r[i] = src[i * kNT + tid];
 }
 
-// B operands of one chunk for this wave: k steps 2ch, 2ch + 1 of its two 32-column blocks
+// B operands of one chunk for this wave: k steps 2ch, 2ch + 1 of its kCB 32-column blocks
 // (blocks past the weight repeat the last one; their columns are never stored).
-__device__ __forceinline__ void LoadImageB(const ImageArgs& p, int cb0, int ch, int lane, u32x4 (&r)[2][2]) {
+template <int kCB>
+__device__ __forceinline__ void LoadImageB(const ImageArgs& p, int cb0, int ch, int lane, u32x4 (&r)[2][kCB]) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kCB; ++j) {
       const int64_t cb = min(cb0 + j, p.col_blocks - 1);
       r[ks][j] = p.w_img[(cb * p.k_steps + 2 * ch + ks) * 64 + lane];
     }
 }
 
-__device__ __forceinline__ void StoreImageA(uint32_t* buf, int tid, const u32x4 (&r)[6]) {
+template <int kNT>
+__device__ __forceinline__ void StoreImageA(uint32_t* buf, int tid, const u32x4 (&r)[kImgBlockVecs / kNT]) {
 #pragma unroll
-  for (int i = 0; i < 6; ++i) reinterpret_cast<u32x4*>(buf)[i * kThreads + tid] = r[i];
+  for (int i = 0; i < kImgBlockVecs / kNT; ++i) reinterpret_cast<u32x4*>(buf)[i * kNT + tid] = r[i];
 }
 
 // The chunk's six operand groups (2 k steps x 3 planes), each two 16-byte LDS reads of A and
@@ -449,9 +454,9 @@ __device__ __forceinline__ void ReadImageGroup(const uint32_t* buf, int lane, in
     av[i] = *reinterpret_cast<const u32x4*>(&buf[pl * kImgPlaneWords + ImageWord<kSwz>(wm * 64 + i * 32 + (lane & 31), g)]);
 }
 
-template <int kSwz>
-__device__ __forceinline__ void ComputeImageChunk(const uint32_t* buf, const u32x4 (&bv)[2][2], int lane, int wm,
-                                                  v16f (&acc_hi)[2][2], v16f (&acc_ml)[2][2]) {
+template <int kSwz, int kCB>
+__device__ __forceinline__ void ComputeImageChunk(const uint32_t* buf, const u32x4 (&bv)[2][kCB], int lane, int wm,
+                                                  v16f (&acc_hi)[2][kCB], v16f (&acc_ml)[2][kCB]) {
   u32x4 av[2][2];
   ReadImageGroup<kSwz>(buf, lane, wm, 0, av[0]);
 #pragma unroll
@@ -461,17 +466,17 @@ __device__ __forceinline__ void ComputeImageChunk(const uint32_t* buf, const u32
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kCB; ++j) {
         v16f& acc = pl == 0 ? acc_hi[i][j] : acc_ml[i][j];
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[grp & 1][i]),
                                                       __builtin_bit_cast(bf16x8, bv[ks][j]), acc, 0, 0, 0);
       }
   }
-  // Keep that order: group g + 1's two LDS reads, then group g's four MFMAs.
+  // Keep that order: group g + 1's two LDS reads, then group g's 2 * kCB MFMAs.
 #pragma unroll
   for (int grp = 0; grp < 6; ++grp) {
     if (grp + 1 < 6) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kCB, 0);            // MFMA
   }
 }
 
@@ -513,11 +518,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // next two chunks' loading. Loads past the last chunk repeat it (never used).
   u32x4 breg[kNB][2][2];
 #pragma unroll
-  for (int s = 0; s < kNB; ++s) LoadImageB(p, cb0, min(s, chunks - 1), lane, breg[s]);
-  u32x4 areg[2][6];
-  LoadImageA(p, a_block, 0, tid, areg[0]);
-  LoadImageA(p, a_block, min(1, chunks - 1), tid, areg[1]);
-  StoreImageA(lds, tid, areg[0]);
+  for (int s = 0; s < kNB; ++s) LoadImageB<2>(p, cb0, min(s, chunks - 1), lane, breg[s]);
+  u32x4 areg[2][kImgBlockVecs / kThreads];
+  LoadImageA<kThreads>(p, a_block, 0, tid, areg[0]);
+  LoadImageA<kThreads>(p, a_block, min(1, chunks - 1), tid, areg[1]);
+  StoreImageA<kThreads>(lds, tid, areg[0]);
   __syncthreads();
   constexpr int kUnroll = kNB == 3 ? 6 : 2 * kNB;  // a multiple of both rings, so every ring index is static
   for (int base = 0; base < chunks; base += kUnroll) {
@@ -525,10 +530,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int u = 0; u < kUnroll; ++u) {
       const int ch = base + u;
       if (ch >= chunks) break;  // workgroup-uniform
-      LoadImageA(p, a_block, min(ch + 2, chunks - 1), tid, areg[u % 2]);
-      ComputeImageChunk<kSwz>(lds + (u % 2) * kImgBlockWords, breg[u % kNB], lane, wm, acc, acc_ml);
-      StoreImageA(lds + ((u + 1) % 2) * kImgBlockWords, tid, areg[(u + 1) % 2]);
-      LoadImageB(p, cb0, min(ch + kNB, chunks - 1), lane, breg[u % kNB]);
+      LoadImageA<kThreads>(p, a_block, min(ch + 2, chunks - 1), tid, areg[u % 2]);
+      ComputeImageChunk<kSwz, 2>(lds + (u % 2) * kImgBlockWords, breg[u % kNB], lane, wm, acc, acc_ml);
+      StoreImageA<kThreads>(lds + ((u + 1) % 2) * kImgBlockWords, tid, areg[(u + 1) % 2]);
+      LoadImageB<2>(p, cb0, min(ch + kNB, chunks - 1), lane, breg[u % kNB]);
       LdsBarrier();  // the A blocks and B operands in flight for later chunks stay in flight
     }
   }
@@ -581,6 +586,172 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     if (tid < kImgRows && m0 + tid < p.m)
       p.row_ss[static_cast<int64_t>(tn) * p.m + m0 + tid] = row_part[tid] + row_part[kImgRows + tid];
   }
+}
+
+// ---- the wide grid: 8 waves per workgroup, tiles of 128 x 256 and 128 x 128 --------------
+//
+// The image kernel's 128 x 128 tiles read 40 KB of operands per 32-k chunk from L2 (the
+// 24 KB A block, and 8 KB of B for each of the two wave rows) for 3.1 Mflop of MFMA work.
+// With realistic operands the chip holds the kernel at its power limit (about 1.75 GHz against
+// 2.37 with the matrix cores idle), so operand traffic costs clock as well as time. A
+// workgroup of 8 waves (2 rows x 4 columns of 64 x 64) over a 128 x 256 tile shares each A
+// block among four waves instead of two: 56 KB per chunk for 6.3 Mflop, 30 % less L2 traffic
+// per flop and 17 % less LDS traffic. Such a workgroup holds a CU alone (2 waves per SIMD),
+// so the tile count must divide evenly over the CUs: the grid mixes 128 x 256 tiles over
+// the first columns (a whole number of rounds) with one round of 128 x 128 tiles (each wave
+// 64 x 32) over the rest, which end together. WideGridFor picks the split.
+constexpr int kWideThreads = 512;
+
+struct WideGrid {
+  int32_t big;        // 128 x 256 tiles (workgroups [0, big))
+  int32_t big_tn;     // their column tiles per row tile
+  int32_t small_tn;   // 128 x 128 column tiles per row tile, over columns [big_cols, n)
+  int32_t big_cols;
+};
+
+// One tile of the wide grid: kCB 32-column blocks per wave (2: 128 x 256; 1: 128 x 128).
+// slot is the 128-column index of the tile's first column in row_ss.
+template <int kCB, int kNB>
+__device__ __forceinline__ void WideTile(const ImageArgs& p, uint32_t* lds, int tm, int64_t n0, int cb0, int slot) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;
+  const int wn = wave & 3;
+  const int64_t m0 = static_cast<int64_t>(tm) * kImgRows;
+  const int64_t a_block = static_cast<int64_t>(tm) * p.chunks;
+  const int chunks = p.chunks;
+  v16f acc[2][kCB], acc_ml[2][kCB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < kCB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.f;
+        acc_ml[i][j][r] = 0.f;
+      }
+  // The image kernel's pipeline: A chunk ch in LDS buffer ch % 2, ch + 1 in registers, ch + 2
+  // loading; B operands of chunks ch .. ch + kNB - 1 in the register ring.
+  u32x4 breg[kNB][2][kCB];
+#pragma unroll
+  for (int s = 0; s < kNB; ++s) LoadImageB<kCB>(p, cb0, min(s, chunks - 1), lane, breg[s]);
+  u32x4 areg[2][kImgBlockVecs / kWideThreads];
+  LoadImageA<kWideThreads>(p, a_block, 0, tid, areg[0]);
+  LoadImageA<kWideThreads>(p, a_block, min(1, chunks - 1), tid, areg[1]);
+  StoreImageA<kWideThreads>(lds, tid, areg[0]);
+  __syncthreads();
+  constexpr int kUnroll = kNB == 3 ? 6 : 2 * kNB;
+  for (int base = 0; base < chunks; base += kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int ch = base + u;
+      if (ch >= chunks) break;  // workgroup-uniform
+      LoadImageA<kWideThreads>(p, a_block, min(ch + 2, chunks - 1), tid, areg[u % 2]);
+      ComputeImageChunk<1, kCB>(lds + (u % 2) * kImgBlockWords, breg[u % kNB], lane, wm, acc, acc_ml);
+      StoreImageA<kWideThreads>(lds + ((u + 1) % 2) * kImgBlockWords, tid, areg[(u + 1) % 2]);
+      LoadImageB<kCB>(p, cb0, min(ch + kNB, chunks - 1), lane, breg[u % kNB]);
+      LdsBarrier();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < kCB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + acc_ml[i][j][r];
+
+  // Element r of a 32 x 32 tile sits at row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
+  float cs[kCB];
+#pragma unroll
+  for (int j = 0; j < kCB; ++j) {
+    const int64_t col = n0 + wn * 32 * kCB + j * 32 + (lane & 31);  // < n: the grid covers whole tiles
+    cs[j] = p.scale[p.mode == kScalePerCol ? col : p.const_index];
+  }
+  double* row_part = reinterpret_cast<double*>(lds);  // [4 wn][128 rows], after the last barrier
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rl = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int64_t row = m0 + rl;
+      double ss = 0.0;
+#pragma unroll
+      for (int j = 0; j < kCB; ++j) {
+        const int64_t col = n0 + wn * 32 * kCB + j * 32 + (lane & 31);
+        if (row < p.m) {  // the epilogue reads bias and residual only inside [m, n]
+          const float v = ApplyEpilogue(__fmul_rn(acc[i][j][r], cs[j]), row, col, p.n, p.epi);
+          StoreC(p.c, row, col, p.n, p.epi, v);
+          ss += static_cast<double>(v) * static_cast<double>(v);
+        }
+      }
+      if (p.row_ss != nullptr) {
+        ss += XorLane<1>(ss);
+        ss += XorLane<2>(ss);
+        ss += XorLane<4>(ss);
+        ss += XorLane<8>(ss);
+        ss += XorLane<16>(ss);
+        if ((lane & 31) == 0) row_part[wn * kImgRows + rl] = ss;
+      }
+    }
+  if (p.row_ss != nullptr) {
+    __syncthreads();
+    if (tid < kImgRows && m0 + tid < p.m) {
+      const double t = row_part[tid] + row_part[kImgRows + tid] + row_part[2 * kImgRows + tid] +
+                       row_part[3 * kImgRows + tid];
+      p.row_ss[static_cast<int64_t>(slot) * p.m + m0 + tid] = t;
+      // A 256-column tile fills its second slot with zero: RmsScaleKernel adds every slot.
+      if (kCB == 2) p.row_ss[static_cast<int64_t>(slot + 1) * p.m + m0 + tid] = 0.0;
+    }
+  }
+}
+
+// Tile index t of a run dealt to XCDs in contiguous runs and ordered in bands of kBand row
+// tiles (as in the image kernel), for a grid of `count` tiles with tn_count column tiles.
+__device__ __forceinline__ void WideTileIndex(int b, int count, int tiles_m, int tn_count, int& tm, int& tn) {
+  const int t = (b % kXcds) * (count / kXcds) + b / kXcds;
+  const int band_tiles = kBand * tn_count;
+  const int band = t / band_tiles;
+  const int in_band = t % band_tiles;
+  const int rows_in_band = min(kBand, tiles_m - band * kBand);
+  tm = band * kBand + in_band % rows_in_band;
+  tn = in_band / rows_in_band;
+}
+
+template <int kNB>
+__global__ __launch_bounds__(kWideThreads) __attribute__((amdgpu_waves_per_eu(2))) void GemmQ8Bf16WideKernel(
+    ImageArgs p, WideGrid g) {
+  __shared__ __align__(16) uint32_t lds[2 * kImgBlockWords];
+  const int wn = (threadIdx.x >> 6) & 3;
+  const int b = blockIdx.x;
+  int tm, tn;
+  if (b < g.big) {
+    WideTileIndex(b, g.big, p.tiles_m, g.big_tn, tm, tn);
+    WideTile<2, kNB>(p, lds, tm, static_cast<int64_t>(tn) * 256, tn * 8 + wn * 2, 2 * tn);
+  } else {
+    WideTileIndex(b - g.big, p.tiles_m * g.small_tn, p.tiles_m, g.small_tn, tm, tn);
+    WideTile<1, kNB>(p, lds, tm, g.big_cols + static_cast<int64_t>(tn) * 128, g.big_cols / 32 + tn * 4 + wn,
+                     g.big_cols / 128 + tn);
+  }
+}
+
+// The wide grid's split for an m x n product on `cus` CUs, or false: n a multiple of 128,
+// exactly one round of 128 x 128 tiles (one per CU) over the last columns and a whole number
+// (at least 2) of rounds of 128 x 256 tiles over the others.
+bool WideGridFor(int64_t m, int64_t n, int64_t cus, WideGrid* g) {
+  const int64_t tiles_m = (m + kImgRows - 1) / kImgRows;
+  if (n % 128 != 0 || cus <= 0 || cus % kXcds != 0 || cus % tiles_m != 0) return false;
+  const int64_t nb = n / 128;
+  const int64_t small_tn = cus / tiles_m;
+  if (small_tn > nb || (nb - small_tn) % 2 != 0) return false;
+  const int64_t big_tn = (nb - small_tn) / 2;
+  if (big_tn < 1 || (tiles_m * big_tn) % cus != 0 || tiles_m * big_tn / cus < 2) return false;
+  if (tiles_m * big_tn > 0x7fffffff / kBand) return false;
+  g->big = static_cast<int32_t>(tiles_m * big_tn);
+  g->big_tn = static_cast<int32_t>(big_tn);
+  g->small_tn = static_cast<int32_t>(small_tn);
+  g->big_cols = static_cast<int32_t>(big_tn * 256);
+  return true;
 }
 
 // out[row, :] = float(double(c[row, :]) * inv) * w with inv = 1/sqrt(ss/n + eps) and ss the
@@ -684,9 +855,17 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
       uint32_t* img = const_cast<uint32_t*>(reinterpret_cast<const uint32_t*>(ia.a_img));
       hipLaunchKernelGGL(SplitAImageKernel<1>, sgrid, dim3(kThreads), 0, stream, a, img, m, k, ia.chunks, items);
       Check(hipGetLastError(), "SplitAImageKernel launch");
-      hipLaunchKernelGGL((GemmQ8Bf16ImageKernel<1, kImgBStages>), dim3(static_cast<uint32_t>(ia.tiles_per_xcd * kXcds)),
-                         dim3(kThreads), 0, stream, ia);
-      Check(hipGetLastError(), "GemmQ8Bf16ImageKernel launch");
+      const int64_t cus = Ctx().cu_count > 0 ? Ctx().cu_count : 256;
+      WideGrid wg;
+      if (WideGridFor(m, n, cus, &wg)) {
+        const uint32_t blocks = static_cast<uint32_t>(wg.big + ia.tiles_m * wg.small_tn);
+        hipLaunchKernelGGL((GemmQ8Bf16WideKernel<kImgBStages>), dim3(blocks), dim3(kWideThreads), 0, stream, ia, wg);
+        Check(hipGetLastError(), "GemmQ8Bf16WideKernel launch");
+      } else {
+        hipLaunchKernelGGL((GemmQ8Bf16ImageKernel<1, kImgBStages>),
+                           dim3(static_cast<uint32_t>(ia.tiles_per_xcd * kXcds)), dim3(kThreads), 0, stream, ia);
+        Check(hipGetLastError(), "GemmQ8Bf16ImageKernel launch");
+      }
       if (rms != nullptr) {
         if (m > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "RmsNorm has too many rows");
         const bool vec = n % 4 == 0 && reinterpret_cast<uintptr_t>(c) % 16 == 0 &&

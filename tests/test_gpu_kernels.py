@@ -521,6 +521,43 @@ def test_gemm_image_path_fused_rmsnorm_ragged():
     np.testing.assert_allclose(y, o.rmsnorm(np.ascontiguousarray(got), gamma_w, m, n, 1e-5), rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("m, k, n, rms", [(4000, 256, 5120, True), (2048, 128, 10240, False)])
+def test_gemm_wide_grid(m, k, n, rms):
+    """Shapes whose tiles divide evenly over the 256 CUs of an MI355X take the wide grid
+    (128 x 256 tiles of 8 waves, then one round of 128 x 128 tiles): 4000 rows (32 row tiles,
+    the last one ragged) x 5120 columns with alpha, bias, Gelu and a fused RMSNormalization,
+    and 2048 x 10240 with bias and a residual. The stored product meets the gamma_K bound (plus
+    the epilogue's roundings) and the normalized rows equal the oracle's RMSNorm of the stored
+    rows."""
+    case = _split_case(m, k, n, 4400 + m)
+    r = np.random.default_rng(4401 + m)
+    bias = (0.1 * r.standard_normal(n)).astype(np.float32)
+    b_d = dev(bias)
+    w = dequant_host(case["bq"], k, n)
+    o = oracle()
+    prod = (case["a"].astype(np.float64) @ w.astype(np.float64)).astype(np.float32)
+    if rms:
+        gamma_w = (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+        g_d = dev(gamma_w)
+        out = dev(np.zeros((m, n), np.float32))
+        e = Epilogue(alpha=1.25, beta=1.0, bias=b_d.ptr, bias_rank=1, activation=2, rms_weight=g_d.ptr,
+                     rms_eps=1e-5, rms_out=out.ptr)
+        e.bias_shape[0] = n
+        got = matmul_quantized(case, e)
+        want = o.gemm_epilogue(prod, 1.25, bias, [n], 1.0, 2)
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+        np.testing.assert_allclose(out.numpy(), o.rmsnorm(np.ascontiguousarray(got), gamma_w, m, n, 1e-5), rtol=1e-6,
+                                   atol=1e-6)
+    else:
+        res = r.standard_normal((m, n)).astype(np.float32)
+        res_d = dev(res)
+        e = Epilogue(alpha=1.0, beta=1.0, bias=b_d.ptr, bias_rank=1, residual=res_d.ptr)
+        e.bias_shape[0] = n
+        got = matmul_quantized(case, e)
+        want = o.gemm_epilogue(prod, 1.0, bias, [n], 1.0, 0) + res
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
 @pytest.mark.parametrize("m", [2, 4])
 def test_staged_weight_follows_rewrites(m):
     """The GEMV reads a staged copy of W (8-column tiles at m = 2, the group-interleaved form
