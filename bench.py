@@ -93,9 +93,16 @@ class Hip:
             self.check(self.L.accel_hip_capture_end(C.byref(g)))
         return g
 
-    def time_graph(self, graphs_and_reps):
-        """Event-timed replay: list of (graph, reps); returns elapsed ms."""
+    def time_graph(self, graphs_and_reps, lead=None):
+        """Event-timed replay: list of (graph, reps); returns elapsed ms.
+
+        `lead`, a graph replayed once (untimed) just before the start event, keeps the GPU busy
+        while the host submits the start event, the timed graphs and the end event: the timed
+        interval then holds the steps and not the host's submission latency (about 12 us,
+        which over 20 steps of a 10.5 us GEMV would read as 0.6 us a step)."""
         self.sync()
+        if lead is not None:
+            self.check(self.L.accel_hip_graph_launch(lead, 1))
         self.check(self.L.accel_hip_event_record(0))
         for g, reps in graphs_and_reps:
             if reps:
@@ -111,38 +118,50 @@ GRAPHS = True  # --no-graph: launch every step directly (profiler counter runs s
 
 
 def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
-    """Warms up, captures the timed calls into graphs of up to `period` steps, times exactly `steps`.
+    """Warms up, captures the timed calls into HIP graphs, times exactly `steps` steps.
 
     Step i reads weight copy i % rotation. The warm-up calls every copy at least once, so
     each is staged (the GEMV's first use of a weight builds its tiled copy, which the library
     refuses inside a capture) and the workspaces have their final size before anything is
-    captured. The graph period is a whole number of rotations, so every replay walks the
-    copies in the same order and a copy is never read again before the other copies
-    (> 256 MB) have streamed through the cache. Inside a graph consecutive kernels start back
-    to back; graphs of a few hundred nodes keep the per-launch queue gap off the average, so
-    the event-timed step matches the profiler's per-kernel duration."""
+    captured. Up to 400 steps are one graph of exactly `steps` nodes; more are graphs of
+    `period` nodes (a whole number of rotations) plus one for the rest. Every graph is
+    replayed once untimed (its first replay uploads it). Then a lead-in graph of whole
+    rotations (at least 4 steps) is replayed untimed right before the start event, so the host
+    submits the timed graphs while the GPU is busy and no submission latency falls inside the
+    interval. The lead-in ends on the last copy, so the timed steps walk the copies in order and
+    a copy is never read again before the other copies (> 256 MB) have streamed through the
+    cache. What stays inside is each timed graph's launch on the GPU, about 5 us (the GEMV at
+    M = 1: 10.71 us per step over 20 steps in one graph, 10.50 over 2000 in graphs of 200;
+    events recorded inside a captured graph cannot be timed on this ROCm)."""
     for i in range(max(warmup, rotation, 1)):
         step(i)
     hip.sync()
+    lead_len = rotation * -(-4 // rotation)
     if not GRAPHS:
+        for i in range(lead_len):
+            step(i)
         hip.check(hip.L.accel_hip_event_record(0))
         for i in range(steps):
             step(i)
         hip.check(hip.L.accel_hip_event_record(1))
         return hip.L.accel_hip_event_elapsed_ms(0, 1)
-    period = min(period, steps)
-    if period > rotation:
-        period -= period % rotation
-    full = hip.graph(step, period)
-    rest = steps % period
-    tail = hip.graph(step, rest) if rest else None
-    plan = [(full, steps // period)] + ([(tail, 1)] if tail else [])
+    lead = hip.graph(step, lead_len)
+    if steps <= 400:
+        plan = [(hip.graph(step, steps), 1)]
+    else:
+        period = min(period, steps)
+        if period > rotation:
+            period -= period % rotation
+        plan = [(hip.graph(step, period), steps // period)]
+        if steps % period:
+            plan.append((hip.graph(step, steps % period), 1))
+    graphs = [lead] + [g for g, _ in plan]
     try:
-        for g, _ in plan:  # the first replay of a graph uploads it
+        for g in graphs:  # the first replay of a graph uploads it
             hip.check(hip.L.accel_hip_graph_launch(g, 1))
-        return hip.time_graph(plan)
+        return hip.time_graph(plan, lead=lead)
     finally:
-        for g, _ in plan:
+        for g in graphs:
             hip.L.accel_hip_graph_destroy(g)
 
 
@@ -541,7 +560,7 @@ def main():
             "ms_per_step": round(per, 4), "TFLOP/s": round(tf, 2),
             "vs_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
             "bf16x3_roofline_frac": round(tf / BF16X3_PEAK_TFLOPS, 4),
-            "kernel": "GemmQ8Bf16Kernel: exact fp32 products as 3 bf16 MFMA passes, roofline 833 TFLOP/s",
+            "kernel": "GemmQ8Bf16WideKernel (accelep_amd/csrc/gemm_q8_bf16.hip): exact fp32 products as 3 bf16 MFMA passes, roofline 833 TFLOP/s",
             "steps": steps4, "config": "X[2048,4096] @ int8 W[4096,14336] + RMSNorm(eps 1e-5)"}
         log(f"prefill int8+rms: {per:.3f} ms/step, {tf:.1f} TFLOP/s")
         llama = bench_llama(hip, np.random.default_rng(11))
