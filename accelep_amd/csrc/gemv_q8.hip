@@ -769,6 +769,9 @@ __device__ __forceinline__ uint32_t PackBf16(float x, float y) {
 __device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
+// kPlain: the epilogue is the identity and C one [m, n] matrix, so each sum is stored as
+// sum * scale with no epilogue code (which costs about 1 us of the m = 16 kernel's tail).
+template <bool kPlain>
 __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p) {
   __shared__ float red[kSplitWaves][32][65];  // [wave][4 * column + row of the MFMA tile][lane]
   __shared__ bool is_last;
@@ -870,13 +873,16 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
   const bool live_col = col < p.n;
   if (p.splits > 1) {
     // Partial sums out (agent scope: the last workgroup, on any XCD, reads them), then the
-    // arrival count of the group.
+    // arrival count of the group. Split sp's [m, n] block starts at the uniform (scalar)
+    // offset sp * m * n; rows within it are 32-bit offsets (the launcher checks m * n < 2^31).
+    const int n32 = static_cast<int>(p.n);
+    const int64_t split_stride = p.m * p.n;
     float* part = p.partials + col;
+    float* mine = part + split * split_stride;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       if (live_col && m0 + i < mend)
-        __hip_atomic_store(&part[(static_cast<int64_t>(split) * p.m + m0 + i) * p.n], sum[i], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&mine[(m0 + i) * n32], sum[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) is_last = atomicAdd(&p.arrivals[group], 1u) == static_cast<uint32_t>(p.splits - 1);
@@ -893,9 +899,9 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
       for (int t = 0; t < kChunk; ++t)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int64_t sp = min(sp0 + t, p.splits - 1);
-          const int64_t mm = min(m0 + i, mend - 1);
-          v[t][i] = __hip_atomic_load(&part[(sp * p.m + mm) * p.n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const int sp = min(sp0 + t, p.splits - 1);
+          const int mm = min(m0 + i, mend - 1);
+          v[t][i] = __hip_atomic_load(&part[sp * split_stride + mm * n32], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 #pragma unroll
       for (int t = 0; t < kChunk; ++t)
@@ -910,7 +916,8 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
   for (int i = 0; i < 8; ++i) {
     const int mm = m0 + i;
     if (mm >= mend) break;
-    StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(sum[i], cs), mm, col, p.n, p.epi));
+    if (kPlain) p.c[mm * static_cast<int>(p.n) + col] = __fmul_rn(sum[i], cs);
+    else StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(sum[i], cs), mm, col, p.n, p.epi));
   }
 }
 
@@ -1068,7 +1075,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   const bool row_scale = b.mode == kScalePerRow;
   // The split-bf16 MFMA kernel: group-interleaved copy, whole 32-row blocks, A 8-byte aligned.
   const bool split_bf16 = m > 1 && b.grouped != nullptr && !zero && !row_scale && a_op == kAOpNone &&
-                          k % kSplitBlockRows == 0 && k < (int64_t(1) << 28) &&
+                          k % kSplitBlockRows == 0 && k < (int64_t(1) << 28) && m * n <= 0x7fffffff &&
                           reinterpret_cast<uintptr_t>(a) % 8 == 0 && (b.mode == kScalePerCol || b.mode == kScaleConst);
   const bool narrow = !split_bf16 && m <= 4 && b.tiled != nullptr && k < (int64_t(1) << 28);
   const int64_t tile_cols = narrow || split_bf16 ? kNarrowTile : kWideTile;
@@ -1136,7 +1143,10 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     const int64_t groups = (tiles + kSplitTiles - 1) / kSplitTiles;
     if (splits > 1) args.arrivals = static_cast<uint32_t*>(Temp(kTempArrivals, static_cast<size_t>(groups) * 4));
     const dim3 sgrid(static_cast<uint32_t>(groups), static_cast<uint32_t>(splits));
-    hipLaunchKernelGGL(GemvSplitBf16Kernel, sgrid, dim3(kSplitThreads), 0, stream, args);
+    if (epi.Identity() && epi.split[0] == 0)
+      hipLaunchKernelGGL(GemvSplitBf16Kernel<true>, sgrid, dim3(kSplitThreads), 0, stream, args);
+    else
+      hipLaunchKernelGGL(GemvSplitBf16Kernel<false>, sgrid, dim3(kSplitThreads), 0, stream, args);
   } else if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
     // The staged prologue row lives in LDS (16-byte aligned), so only an even k is needed

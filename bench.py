@@ -535,15 +535,18 @@ def main():
     log(f"gemv M=1 (HBM, {COPIES} copies): {per1 * 1e3:.2f} us/step, {gbs1:.1f} GB/s")
     secondary = {}
     if not args.only_headline:
+        # The secondary GEMV legs time at least 400 steps (one graph; a few ms), so their lines
+        # carry the steady per-step time rather than one graph launch spread over a few steps.
+        steps_g = max(400, args.steps)
         for m in (4, 16):
-            per, gbs = bench_gemv(hip, m, args.steps, args.warmup, COPIES, rng)
+            per, gbs = bench_gemv(hip, m, steps_g, args.warmup, COPIES, rng)
             flops = 2 * m * K_DIM * N_DIM
             secondary[f"gemv_m{m}"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
                                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                                       "TFLOP/s": round(flops / (per * 1e-3) / 1e12, 2)}
+                                       "TFLOP/s": round(flops / (per * 1e-3) / 1e12, 2), "steps": steps_g}
             log(f"gemv M={m}: {per * 1e3:.2f} us/step, {gbs:.1f} GB/s")
-        per, gbs = bench_gemv(hip, 1, args.steps, args.warmup, 1, rng)
-        secondary["gemv_m1_cache_warm"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1),
+        per, gbs = bench_gemv(hip, 1, steps_g, args.warmup, 1, rng)
+        secondary["gemv_m1_cache_warm"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1), "steps": steps_g,
                                            "note": "one weight copy, L2/MALL may serve it; not HBM-honest"}
         # The GEMM legs time at least 20 launches after at least 5 untimed ones, whatever
         # --steps is: a leg that follows the memory-bound GEMV legs runs its first launches
