@@ -115,6 +115,7 @@ class Hip:
 
 
 GRAPHS = True  # --no-graph: launch every step directly (profiler counter runs see each dispatch)
+LEAD_STEPS = 4  # untimed steps replayed right before the start event (rounded up to whole rotations)
 
 
 def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
@@ -136,7 +137,7 @@ def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
     for i in range(max(warmup, rotation, 1)):
         step(i)
     hip.sync()
-    lead_len = rotation * -(-4 // rotation)
+    lead_len = rotation * -(-LEAD_STEPS // rotation)
     if not GRAPHS:
         for i in range(lead_len):
             step(i)
