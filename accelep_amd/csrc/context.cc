@@ -492,7 +492,12 @@ ACCEL_HIP_API double accel_hip_time_ms(AccelHipWorkFn fn, void* user, int32_t it
 ACCEL_HIP_API int accel_hip_event_record(int32_t slot) {
   return Guard([&] {
     if (slot < 0 || slot >= kEventSlots) Fail(ACCEL_HIP_INVALID_ARGUMENT, "event slot out of range");
-    Check(hipEventRecord(g_events[slot], Ctx().stream), "hipEventRecord");
+    // Inside a capture only an external record node can be timed afterwards: a plain record
+    // there leaves an event that hipEventElapsedTime refuses (invalid resource handle).
+    if (Capturing())
+      Check(hipEventRecordWithFlags(g_events[slot], Ctx().stream, hipEventRecordExternal), "hipEventRecordWithFlags");
+    else
+      Check(hipEventRecord(g_events[slot], Ctx().stream), "hipEventRecord");
   });
 }
 

@@ -93,6 +93,33 @@ class Hip:
             self.check(self.L.accel_hip_capture_end(C.byref(g)))
         return g
 
+    def time_in_graph(self, step, lead_len, steps):
+        """Times `steps` calls of step(i) between two event records captured in one graph after
+        `lead_len` untimed calls (whole weight rotations): the graph's launch and the lead-in
+        fall before the start event. Replayed once untimed (the first replay uploads it), then
+        once timed. Returns elapsed ms."""
+        self.check(self.L.accel_hip_capture_begin())
+        try:
+            for i in range(lead_len):
+                step(i)
+            self.check(self.L.accel_hip_event_record(0))
+            for i in range(steps):
+                step(i)
+            self.check(self.L.accel_hip_event_record(1))
+        finally:
+            g = C.c_void_p()
+            self.check(self.L.accel_hip_capture_end(C.byref(g)))
+        try:
+            self.check(self.L.accel_hip_graph_launch(g, 1))
+            self.sync()
+            self.check(self.L.accel_hip_graph_launch(g, 1))
+            ms = self.L.accel_hip_event_elapsed_ms(0, 1)
+            if ms < 0:
+                raise RuntimeError(self.L.accel_hip_last_error().decode())
+            return ms
+        finally:
+            self.L.accel_hip_graph_destroy(g)
+
     def time_graph(self, graphs_and_reps, lead=None):
         """Event-timed replay: list of (graph, reps); returns elapsed ms.
 
@@ -124,16 +151,17 @@ def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
     Step i reads weight copy i % rotation. The warm-up calls every copy at least once, so
     each is staged (the GEMV's first use of a weight builds its tiled copy, which the library
     refuses inside a capture) and the workspaces have their final size before anything is
-    captured. Up to 400 steps are one graph of exactly `steps` nodes; more are graphs of
-    `period` nodes (a whole number of rotations) plus one for the rest. Every graph is
-    replayed once untimed (its first replay uploads it). Then a lead-in graph of whole
-    rotations (at least 4 steps) is replayed untimed right before the start event, so the host
-    submits the timed graphs while the GPU is busy and no submission latency falls inside the
-    interval. The lead-in ends on the last copy, so the timed steps walk the copies in order and
-    a copy is never read again before the other copies (> 256 MB) have streamed through the
-    cache. What stays inside is each timed graph's launch on the GPU, about 5 us (the GEMV at
-    M = 1: 10.71 us per step over 20 steps in one graph, 10.50 over 2000 in graphs of 200;
-    events recorded inside a captured graph cannot be timed on this ROCm)."""
+    captured. A lead-in of whole rotations (at least 4 steps) runs untimed right before the
+    start event and ends on the last copy, so the timed steps walk the copies in order and a
+    copy is never read again before the other copies (> 256 MB) have streamed through the
+    cache.
+    - Up to 400 steps: one graph holds the lead-in, the start event record, exactly `steps`
+      steps and the end event record (records inside a capture become timeable event nodes),
+      replayed once untimed (its first replay uploads it) and once timed. Neither the host's
+      submission nor the graph's launch on the GPU (about 5 us) falls inside the interval.
+    - More steps: graphs of `period` nodes (a whole number of rotations) plus one for the
+      rest, each replayed once untimed; then the lead-in graph and the timed replays back to
+      back between two events on the stream (one graph launch per `period` steps stays in)."""
     for i in range(max(warmup, rotation, 1)):
         step(i)
     hip.sync()
@@ -146,16 +174,15 @@ def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
             step(i)
         hip.check(hip.L.accel_hip_event_record(1))
         return hip.L.accel_hip_event_elapsed_ms(0, 1)
-    lead = hip.graph(step, lead_len)
     if steps <= 400:
-        plan = [(hip.graph(step, steps), 1)]
-    else:
-        period = min(period, steps)
-        if period > rotation:
-            period -= period % rotation
-        plan = [(hip.graph(step, period), steps // period)]
-        if steps % period:
-            plan.append((hip.graph(step, steps % period), 1))
+        return hip.time_in_graph(step, lead_len, steps)
+    lead = hip.graph(step, lead_len)
+    period = min(period, steps)
+    if period > rotation:
+        period -= period % rotation
+    plan = [(hip.graph(step, period), steps // period)]
+    if steps % period:
+        plan.append((hip.graph(step, steps % period), 1))
     graphs = [lead] + [g for g, _ in plan]
     try:
         for g in graphs:  # the first replay of a graph uploads it

@@ -10,6 +10,9 @@ what a capture must refuse, and stale graphs.
   been dropped (W rewritten or freed): the launch returns ACCEL_HIP_RUNTIME_ERROR and the
   graph is never replayed. A graph that did not read the dropped copy still replays.
 
+* An event recorded during a capture becomes a node of the graph that every replay records,
+  and stays timeable (the bench times its steps between two such events).
+
 No test here replays a graph whose memory was released: every refusal is decided on the host
 before anything is launched.
 """
@@ -264,3 +267,37 @@ def test_prepare_reports_and_refuses():
         check(L.accel_hip_graph_destroy(graph))
     assert rc == RUNTIME_ERROR and staged == 0, msg
     assert _prepare(plain, k, n) == (0, STAGE_TILES | STAGE_GROUPS | STAGE_BF16)
+
+
+def test_event_records_inside_a_capture_are_timeable():
+    """accel_hip_event_record during a capture adds an event node that every replay records:
+    the elapsed time between two such events is readable after each replay (a plain record
+    inside a graph is refused by hipEventElapsedTime), positive, and no longer than the same
+    replay timed from outside the graph."""
+    L = lib()
+    g = _gemv(1, 1024, 4096, 91)
+    check(_call(g))  # stage the weight copy eagerly
+    check(L.accel_hip_synchronize())
+    check(L.accel_hip_capture_begin())
+    check(_call(g))
+    check(L.accel_hip_event_record(0))
+    for _ in range(5):
+        check(_call(g))
+    check(L.accel_hip_event_record(1))
+    handle = _end_capture()
+    try:
+        for _ in range(3):
+            check(L.accel_hip_graph_launch(handle, 1))
+            check(L.accel_hip_synchronize())
+            inner = L.accel_hip_event_elapsed_ms(0, 1)
+            assert inner > 0, L.accel_hip_last_error().decode()
+            check(L.accel_hip_event_record(2))
+            check(L.accel_hip_graph_launch(handle, 1))
+            check(L.accel_hip_event_record(3))
+            outer = L.accel_hip_event_elapsed_ms(2, 3)
+            assert outer > 0, L.accel_hip_last_error().decode()
+            assert inner <= outer
+        np.testing.assert_allclose(g["out"].numpy(), g["a"].astype(np.float64) @ g["w"].astype(np.float64),
+                                   rtol=1e-4, atol=1e-4)
+    finally:
+        check(L.accel_hip_graph_destroy(handle))
