@@ -5,7 +5,9 @@
   runtime headers; linked against libamdhip64 with -z defs.
 * accelep_amd/libaccel_runtime.so: the C++ accel:: device and runtime (include/accel/*.h,
   host/*.cc) over the C-ABI.
-* tests/cpp/bin/*: the C++ tests (tests/cpp/*.cc), linked against both.
+* tests/cpp/bin/*: the C++ tests (tests/cpp/*.cc), linked against both, and
+  libbpe_host.so (tests/cpp/lib/bpe_host.cc over csrc/tokenizer.cc, no HIP) for the CPU
+  tokenizer tests.
 
     python -m accelep_amd.build          # or: python accelep_amd/build.py
 """
@@ -85,6 +87,14 @@ def _build_cpp_test(src: Path) -> Path:
     return exe
 
 
+def _build_bpe_host() -> Path:
+    CPP_TEST_BIN.mkdir(exist_ok=True)
+    out = CPP_TEST_BIN / "libbpe_host.so"
+    _run(["g++", *HOST_FLAGS, "-shared", "-fvisibility=hidden", f"-I{CSRC}", "-o", str(out),
+          str(CPP_TESTS / "lib" / "bpe_host.cc"), str(CSRC / "tokenizer.cc")])
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     """Compiles every source and links the library. Always rebuilds."""
     BUILD.mkdir(exist_ok=True)
@@ -102,6 +112,7 @@ def build(verbose: bool = False) -> Path:
     tests = sorted(CPP_TESTS.glob("*.cc"))
     with ThreadPoolExecutor(max_workers=max(1, min(len(tests), jobs))) as pool:
         list(pool.map(_build_cpp_test, tests))
+    _build_bpe_host()
     if verbose:
         print(f"built {LIB}, {RUNTIME_LIB} and {len(tests)} C++ test programs")
     return LIB

@@ -130,6 +130,14 @@ LLAMA_SIGNATURES = {
     "accel_llama_weight_q8": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, I8P, F32P, i64, i64]),
     "accel_llama_generate": (C.c_int, [C.c_void_p, I32P, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_uint32,
                                        C.c_int32, I32P, I32P]),
+    "accel_llama_tokenizer": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "accel_llama_encode": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int32, I32P, C.c_int32, I32P]),
+    "accel_llama_decode": (C.c_int, [C.c_void_p, I32P, C.c_int32, C.c_int32, C.c_char_p, C.c_int32, I32P]),
+    "accel_llama_complete": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_uint32,
+                                       C.c_int32, C.c_char_p, C.c_int32, I32P, I32P, C.c_int32, I32P, I32P]),
+    "accel_llama_complete_stream": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                              C.c_uint32, C.c_int32, C.c_char_p, C.c_int32, I32P, I32P, C.c_int32,
+                                              I32P, I32P, C.c_void_p, C.c_void_p]),
     "accel_llama_forward_ids": (C.c_int, [C.c_void_p, I32P, C.c_int32, C.c_int32]),
     "accel_llama_logit_max_abs": (C.c_int, [C.c_void_p, F32P, C.c_int32, F32P]),
     "accel_llama_logits": (C.c_int, [C.c_void_p, F32P, C.c_int32]),
@@ -137,6 +145,10 @@ LLAMA_SIGNATURES = {
     "accel_llama_reset": (None, [C.c_void_p]),
     "accel_llama_last_error": (C.c_char_p, []),
 }
+
+
+# AccelLlamaTokenFn: void (*)(int32_t token_id, void* user)
+TOKEN_FN = C.CFUNCTYPE(None, C.c_int32, C.c_void_p)
 
 
 def lib() -> C.CDLL:

@@ -19,6 +19,8 @@
 //    call copies the ids back once and, with no eos id, never waits on the GPU in between;
 //  * the decode step reads its position and id index from device memory and is replayed
 //    from a HIP graph, so a token costs its kernels' time and not ~450 host launches.
+// The tokenizer calls (src/llama_model.cc:183-205, :449-560) encode and decode on the host
+// with ByteBpe (tokenizer.cc) around the same Generate.
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -31,6 +33,7 @@
 
 #include "accel_llama.h"
 #include "common.h"
+#include "tokenizer.h"
 
 namespace {
 
@@ -133,6 +136,8 @@ struct Model {
   DevBuf attn_work;
   DevBuf attn_arrivals;  // uint32 per head, zero between decode attention launches
   DevBuf greedy_work;    // the greedy pick's count (zero between launches) and keys
+  ByteBpe bpe;           // accel_llama_tokenizer
+  DevBuf text_out;       // a completion's UTF-8 text on its way back (grows to the longest)
 
   void DropDecodeGraph() {
     if (decode_graph != nullptr) accel_hip_graph_destroy(decode_graph);
@@ -333,9 +338,11 @@ struct Model {
     if (accel_hip_graph_launch(decode_graph, 1) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
   }
 
-  // src/llama_model.cc:101-131.
+  // src/llama_model.cc:101-131. on_token (may be null) receives each id after it is sampled
+  // and before the eos check.
   void Generate(const int32_t* prompt, int32_t prompt_count, int32_t max_new, int32_t eos_id, float temperature,
-                uint32_t seed, int32_t top_k, int32_t* out_ids, int32_t* out_count) {
+                uint32_t seed, int32_t top_k, int32_t* out_ids, int32_t* out_count, AccelLlamaTokenFn on_token,
+                void* user) {
     filled = 0;
     if (prompt == nullptr || prompt_count <= 0 || prompt_count > cfg.context)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
@@ -356,12 +363,14 @@ struct Model {
       LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
                         state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
       produced += 1;
-      if (eos_id >= 0) {
-        // Only an eos id needs the chosen id on the host before the next step.
+      if (eos_id >= 0 || on_token != nullptr) {
+        // Only an eos id or a token callback needs the chosen id on the host before the next
+        // step (an uncounted read, as the reference's host reads it through a raw pointer).
         int32_t id = -1;
         Check(hipMemcpyAsync(&id, chosen.as<int32_t>() + produced - 1, sizeof(id), hipMemcpyDeviceToHost, stream()),
               "hipMemcpyAsync");
         Check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+        if (on_token != nullptr) on_token(id, user);
         if (id == eos_id) break;
       }
       if (filled >= cfg.context) break;
@@ -372,6 +381,42 @@ struct Model {
                             ACCEL_HIP_OK)
       Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
     *out_count = produced;
+  }
+
+  // src/llama_model.cc:133-148: the text goes to the host through device memory, so its copy
+  // back is a counted one, like the ids'.
+  void CopyOutText(const std::string& text, char* out_text, int32_t cap, int32_t* out_len) {
+    if (out_text == nullptr || out_len == nullptr || cap < 0 || static_cast<int64_t>(text.size()) > cap)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "completion text buffer is too small");
+    *out_len = static_cast<int32_t>(text.size());
+    if (text.empty()) return;
+    if (text_out.buffer().bytes < text.size()) text_out = DevBuf(text.size());
+    Check(hipMemcpyAsync(text_out.as<char>(), text.data(), text.size(), hipMemcpyHostToDevice, stream()),
+          "hipMemcpyAsync");
+    if (accel_hip_copy_d2h(out_text, text_out.buffer(), text.size()) != ACCEL_HIP_OK)
+      Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+  }
+
+  // src/llama_model.cc:183-206: encode the prompt, generate, decode the ids without special
+  // tokens.
+  void Complete(const char* prompt, int32_t prompt_len, int32_t max_new, int32_t eos_id, float temperature,
+                uint32_t seed, int32_t top_k, char* out_text, int32_t out_text_cap, int32_t* out_text_len,
+                int32_t* out_ids, int32_t out_ids_cap, int32_t* out_count, int32_t* prompt_tokens,
+                AccelLlamaTokenFn on_token, void* user) {
+    if (!bpe.loaded()) Fail(ACCEL_HIP_INVALID_ARGUMENT, "tokenizer is not loaded");
+    if (prompt_len < 0 || (prompt_len > 0 && prompt == nullptr) || out_ids == nullptr || out_count == nullptr ||
+        prompt_tokens == nullptr || out_ids_cap < max_new)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "invalid complete");
+    const std::vector<int32_t> ids =
+        bpe.Encode(prompt_len == 0 ? std::string_view() : std::string_view(prompt, static_cast<size_t>(prompt_len)));
+    if (ids.empty()) Fail(ACCEL_HIP_INVALID_ARGUMENT, "prompt encoded to no tokens");
+    if (static_cast<int32_t>(ids.size()) > cfg.context) Fail(ACCEL_HIP_INVALID_ARGUMENT, "prompt exceeds context");
+    Generate(ids.data(), static_cast<int32_t>(ids.size()), max_new, eos_id, temperature, seed, top_k, out_ids,
+             out_count, on_token, user);
+    // out_ids holds what the device chose (copied back by Generate).
+    const std::string text = bpe.Decode(out_ids, *out_count, true);
+    CopyOutText(text, out_text, out_text_cap, out_text_len);
+    *prompt_tokens = static_cast<int32_t>(ids.size());
   }
 };
 
@@ -676,8 +721,84 @@ ACCEL_LLAMA_API int accel_llama_generate(AccelLlama* handle, const int32_t* prom
   return Run([&] {
     std::lock_guard<std::mutex> lock(m->mu);
     if (!m->Ready()) Fail(ACCEL_HIP_INVALID_ARGUMENT, "llama weights are incomplete");
-    m->Generate(prompt, prompt_count, max_new, eos_id, temperature, seed, top_k, out_ids, out_count);
+    m->Generate(prompt, prompt_count, max_new, eos_id, temperature, seed, top_k, out_ids, out_count, nullptr,
+                nullptr);
   });
+}
+
+ACCEL_LLAMA_API int accel_llama_tokenizer(AccelLlama* handle, const char* path) {
+  Model* m = Get(handle);
+  if (m == nullptr || path == nullptr || path[0] == '\0') {
+    g_llama_error = "invalid tokenizer";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    m->bpe.Load(path);
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_encode(AccelLlama* handle, const char* text, int32_t text_len, int32_t* out_ids,
+                                       int32_t out_cap, int32_t* out_count) {
+  Model* m = Get(handle);
+  if (m == nullptr || text_len < 0 || (text_len > 0 && text == nullptr) || out_ids == nullptr ||
+      out_count == nullptr || out_cap < 0) {
+    g_llama_error = "invalid encode";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    const std::vector<int32_t> ids =
+        m->bpe.Encode(text_len == 0 ? std::string_view() : std::string_view(text, static_cast<size_t>(text_len)));
+    if (static_cast<int64_t>(ids.size()) > out_cap) Fail(ACCEL_HIP_INVALID_ARGUMENT, "encode buffer is too small");
+    if (!ids.empty()) std::memcpy(out_ids, ids.data(), ids.size() * sizeof(int32_t));
+    *out_count = static_cast<int32_t>(ids.size());
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_decode(AccelLlama* handle, const int32_t* ids, int32_t count, int32_t skip_special,
+                                       char* out_text, int32_t out_cap, int32_t* out_len) {
+  Model* m = Get(handle);
+  if (m == nullptr || out_text == nullptr || out_len == nullptr || count < 0 || (count > 0 && ids == nullptr) ||
+      out_cap < 0) {
+    g_llama_error = "invalid decode";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    const std::string text = m->bpe.Decode(ids, count, skip_special != 0);
+    if (static_cast<int64_t>(text.size()) > out_cap) Fail(ACCEL_HIP_INVALID_ARGUMENT, "decode buffer is too small");
+    if (!text.empty()) std::memcpy(out_text, text.data(), text.size());
+    *out_len = static_cast<int32_t>(text.size());
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_complete_stream(AccelLlama* handle, const char* prompt, int32_t prompt_len,
+                                                int32_t max_new, int32_t eos_id, float temperature, uint32_t seed,
+                                                int32_t top_k, char* out_text, int32_t out_text_cap,
+                                                int32_t* out_text_len, int32_t* out_ids, int32_t out_ids_cap,
+                                                int32_t* out_count, int32_t* prompt_tokens, AccelLlamaTokenFn on_token,
+                                                void* user) {
+  Model* m = Get(handle);
+  if (m == nullptr || prompt_len < 0 || (prompt_len > 0 && prompt == nullptr) || max_new < 0) {
+    g_llama_error = "invalid complete";
+    return 1;
+  }
+  return Run([&] {
+    std::lock_guard<std::mutex> lock(m->mu);
+    if (!m->Ready()) Fail(ACCEL_HIP_INVALID_ARGUMENT, "llama weights are incomplete");
+    m->Complete(prompt, prompt_len, max_new, eos_id, temperature, seed, top_k, out_text, out_text_cap, out_text_len,
+                out_ids, out_ids_cap, out_count, prompt_tokens, on_token, user);
+  });
+}
+
+ACCEL_LLAMA_API int accel_llama_complete(AccelLlama* handle, const char* prompt, int32_t prompt_len, int32_t max_new,
+                                         int32_t eos_id, float temperature, uint32_t seed, int32_t top_k,
+                                         char* out_text, int32_t out_text_cap, int32_t* out_text_len, int32_t* out_ids,
+                                         int32_t out_ids_cap, int32_t* out_count, int32_t* prompt_tokens) {
+  return accel_llama_complete_stream(handle, prompt, prompt_len, max_new, eos_id, temperature, seed, top_k, out_text,
+                                     out_text_cap, out_text_len, out_ids, out_ids_cap, out_count, prompt_tokens,
+                                     nullptr, nullptr);
 }
 
 ACCEL_LLAMA_API int accel_llama_forward_ids(AccelLlama* handle, const int32_t* ids, int32_t count, int32_t reset) {

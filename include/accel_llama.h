@@ -3,12 +3,13 @@
  * state and the chosen ids stay in HBM; the host sends prompt ids and receives the chosen
  * ids. Replaces AccelEP's accel_llama_* (include/accel/sim_api.h:38-115, src/llama_model.cc)
  * with the same names, argument meaning and return convention (0 on success, 1 on failure
- * with the message in accel_llama_last_error(); create returns NULL on failure). The
- * tokenizer/complete/stream calls are not part of this library.
+ * with the message in accel_llama_last_error(); create returns NULL on failure).
  *
  * Every step runs as HIP kernels of libaccel_hip (the same kernels as the accel_hip_* entry
  * points): int8 or fp32 linear layers, RMSNorm, RoPE, KV append, attention, SiLU and the
- * residual adds (fused into the o and down projections' stores), and the sampler.
+ * residual adds (fused into the o and down projections' stores), and the sampler. The
+ * tokenizer calls encode and decode on the host (a byte-level BPE of a Hugging Face
+ * tokenizer.json in the SmolLM2 form, src/bpe.cc) around the same generate loop.
  */
 #ifndef ACCEL_LLAMA_H_
 #define ACCEL_LLAMA_H_
@@ -69,6 +70,40 @@ ACCEL_LLAMA_API int accel_llama_weight_q8(AccelLlama* model, int32_t kind, int32
 ACCEL_LLAMA_API int accel_llama_generate(AccelLlama* model, const int32_t* prompt, int32_t prompt_count,
                                          int32_t max_new, int32_t eos_id, float temperature, uint32_t seed,
                                          int32_t top_k, int32_t* out_ids, int32_t* out_count);
+/* accel_llama_tokenizer (sim_api.h:76-77, src/llama_model.cc:449-464): load a Hugging Face
+ * tokenizer.json (model BPE; no normalizer or post-processor; pre-tokenizer Digits with
+ * individual digits then ByteLevel without prefix space; ByteLevel decoder). */
+ACCEL_LLAMA_API int accel_llama_tokenizer(AccelLlama* model, const char* path);
+/* accel_llama_encode (sim_api.h:84-88, src/llama_model.cc:466-492): ids of text_len bytes
+ * (NUL allowed; not valid UTF-8 is an error); fails with "encode buffer is too small" when
+ * out_cap is below the count. */
+ACCEL_LLAMA_API int accel_llama_encode(AccelLlama* model, const char* text, int32_t text_len, int32_t* out_ids,
+                                       int32_t out_cap, int32_t* out_count);
+/* accel_llama_decode (sim_api.h:89-91, src/llama_model.cc:494-519): UTF-8 text of the ids
+ * (skip_special nonzero leaves out special tokens; invalid UTF-8 comes out as U+FFFD per
+ * byte), *out_len bytes with no trailing NUL; "decode buffer is too small" past out_cap. */
+ACCEL_LLAMA_API int accel_llama_decode(AccelLlama* model, const int32_t* ids, int32_t count, int32_t skip_special,
+                                       char* out_text, int32_t out_cap, int32_t* out_len);
+/* accel_llama_complete (sim_api.h:92-98, src/llama_model.cc:521-527, :183-206): encode the
+ * prompt (prompt_len bytes, NUL allowed), generate as accel_llama_generate does, and decode
+ * the chosen ids without special tokens. out_ids_cap must be at least max_new; the prompt
+ * must encode to 1 .. context ids. Counted copies: the prompt ids in, the ids and the text
+ * back. */
+ACCEL_LLAMA_API int accel_llama_complete(AccelLlama* model, const char* prompt, int32_t prompt_len, int32_t max_new,
+                                         int32_t eos_id, float temperature, uint32_t seed, int32_t top_k,
+                                         char* out_text, int32_t out_text_cap, int32_t* out_text_len, int32_t* out_ids,
+                                         int32_t out_ids_cap, int32_t* out_count, int32_t* prompt_tokens);
+/* AccelLlamaTokenFn (sim_api.h:99-101): called with each chosen id once it has been read
+ * back (an uncounted read), before the eos check; it must not call back into the model. */
+typedef void (*AccelLlamaTokenFn)(int32_t token_id, void* user);
+/* accel_llama_complete_stream (sim_api.h:102-108, src/llama_model.cc:530-551): the same result
+ * as accel_llama_complete, with on_token (may be NULL) called per id. */
+ACCEL_LLAMA_API int accel_llama_complete_stream(AccelLlama* model, const char* prompt, int32_t prompt_len,
+                                                int32_t max_new, int32_t eos_id, float temperature, uint32_t seed,
+                                                int32_t top_k, char* out_text, int32_t out_text_cap,
+                                                int32_t* out_text_len, int32_t* out_ids, int32_t out_ids_cap,
+                                                int32_t* out_count, int32_t* prompt_tokens, AccelLlamaTokenFn on_token,
+                                                void* user);
 /* Test seams (sim_api.h:106-112): a forward over ids (reset nonzero clears the cache) that
  * leaves the last row's logits on the device, and max |logits - reference|. */
 ACCEL_LLAMA_API int accel_llama_forward_ids(AccelLlama* model, const int32_t* ids, int32_t count, int32_t reset);

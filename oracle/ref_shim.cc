@@ -154,3 +154,23 @@ REF_API void ref_sample_token(const float* logits, int32_t* chosen, int64_t inde
                               uint32_t* rng, int32_t top_k) {
   accel::SimSampleToken(logits, chosen, index, vocab, temperature, rng, top_k);
 }
+
+// The reference's \p{L} and \p{N} tables (src/unicode_cats.inc, compiled where it lies), as
+// flat [first, last] pairs; which 0 = letters, 1 = numbers.
+namespace ref_unicode {
+#include "unicode_cats.inc"
+}  // namespace ref_unicode
+
+REF_API int ref_unicode_ranges(int32_t which, const uint32_t** pairs, int32_t* count) {
+  if (which == 0) {
+    *pairs = ref_unicode::k_letter_ranges;
+    *count = ref_unicode::k_letter_ranges_count;
+    return 0;
+  }
+  if (which == 1) {
+    *pairs = ref_unicode::k_number_ranges;
+    *count = ref_unicode::k_number_ranges_count;
+    return 0;
+  }
+  return 1;
+}

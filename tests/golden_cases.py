@@ -253,3 +253,13 @@ def llama_full_case(sampled=False):
                     temperature=0.8, seed=11, top_k=40)
     return dict(name="smol_full_greedy", config=cfg, weights=w, quant=q, prompt=prompt, max_new=128, eos=-1,
                 temperature=0.0, seed=0, top_k=0)
+
+
+def complete_config():
+    """The model of the completion cases: tiny widths, and the vocabulary of
+    tests/golden/tokenizer_small.json (1220 tokens), so that every id decodes."""
+    return dict(vocab=1220, hidden=64, layers=2, heads=4, kv_heads=2, intermediate=128, context=48, eps=1e-5,
+                rope_theta=100000.0)
+
+
+COMPLETE_WEIGHT_SEED = 107

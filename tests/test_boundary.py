@@ -65,7 +65,8 @@ def test_llama_api_mirrors_the_reference_names():
 
     names = set(declared_llama_entry_points())
     assert names == set(LLAMA_SIGNATURES)
-    for want in ["create", "destroy", "weight", "generate", "forward_ids", "logit_max_abs", "reset", "last_error"]:
+    for want in ["create", "destroy", "weight", "tokenizer", "generate", "encode", "decode", "complete",
+                 "complete_stream", "forward_ids", "logit_max_abs", "reset", "last_error"]:
         assert f"accel_llama_{want}" in names
 
 
