@@ -120,6 +120,10 @@ struct Q8View {
   const int8_t* tiled = nullptr;  // staged column-tiled copy of q (kGemvTileCols wide), or nullptr
   const int8_t* grouped = nullptr;  // staged group-interleaved copy of q, or nullptr
   const void* bf16 = nullptr;       // staged bf16 copy in the GEMM's MFMA operand order, or nullptr
+  // Load policy of the one-row GEMV: false streams the weight (nontemporal loads, the right
+  // choice for weights read once per pass over more than the 256 MB last-level cache); true
+  // uses plain loads, for a caller whose whole working set stays cached between passes.
+  bool cached = false;
 };
 
 // ---- weight staging (staging.cc) --------------------------------------------------------

@@ -151,13 +151,19 @@ struct NarrowBatch {
 // sends only k < 2^28 here.
 // kPairA: k even and A 8-byte aligned, so (a[r], a[r + 1]) is one aligned 8-byte load.
 // kClamp false: the caller has checked that every row of the batch lies below ke.
+// kCached: a plain load instead of a streaming (nontemporal) one, for a weight that later
+// calls read again while it can still sit in the last-level cache (Q8View::cached).
 // Load u of a batch: the W pair.
-template <int M, int U, bool kClamp>
+template <int M, int U, bool kClamp, bool kCached = false>
 __device__ __forceinline__ void LoadNarrowWAt(int u, int r0, int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
   using S = NarrowShape<M>;
   const int r = r0 + u * static_cast<int>(S::kStepRows);
   const int rw = !kClamp || r < kw - 2 ? r : kw - 2;
-  b.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u));
+  const u32x4* at = reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u);
+  if constexpr (kCached)
+    b.w[u] = *at;
+  else
+    b.w[u] = __builtin_nontemporal_load(at);
 }
 
 // Load u of a batch: the A rows (and per-row scale and zero).
@@ -196,12 +202,12 @@ __device__ __forceinline__ void LoadNarrowAAt(int u, const GemvArgs& p, const fl
 // The whole batch, each W load followed by its A loads: loads complete in issue order, so
 // load u's data is ready as soon as the first u loads are, and the products of u start while
 // the later loads are still in flight.
-template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp>
+template <int M, int U, bool kZero, bool kRowScale, bool kPairA, bool kClamp, bool kCached = false>
 __device__ __forceinline__ void LoadNarrowBatch(const GemvArgs& p, const float* const (&arow)[M], int r0, int ke,
                                                 int kw, const int8_t* tbase, NarrowBatch<M, U>& b) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    LoadNarrowWAt<M, U, kClamp>(u, r0, kw, tbase, b);
+    LoadNarrowWAt<M, U, kClamp, kCached>(u, r0, kw, tbase, b);
     LoadNarrowAAt<M, U, kZero, kRowScale, kPairA, kClamp>(u, p, arow, r0, ke, b);
   }
 }
@@ -461,7 +467,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
 // flight instead of after the sums, so the last workgroup's store waits for no memory. With
 // an input prologue (kAOp) the weight loads are issued first, the transformed row is staged
 // in LDS (StageInputRow) while they are in flight, and A is read from there.
-template <int kSteps, bool kClamp, bool kPlain, int kAOp>
+template <int kSteps, bool kClamp, bool kPlain, int kAOp, bool kCached>
 __global__ __launch_bounds__(NarrowShape<1>::kThreads)
 __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) void GemvM1Kernel(
     const int8_t* tiled, const float* a, const float* scale, float* c, int32_t k, int32_t n, int32_t tiles,
@@ -486,12 +492,12 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   double ss = 0.0;  // kAOpRmsAfter: this lane's share of sum(double(x)^2)
   if (kAOp == kAOpNone) {
     const float* const arow[1] = {a};
-    LoadNarrowBatch<1, kSteps, false, false, true, kClamp>(unused, arow, 2 * tid, k, k, tbase, b);
+    LoadNarrowBatch<1, kSteps, false, false, true, kClamp, kCached>(unused, arow, 2 * tid, k, k, tbase, b);
   } else if (kAOp == kAOpRmsAfter || kAOp == kAOpSiluUp) {
     // Elementwise inputs: each lane forms its own A pairs from x and the second operand (the
     // norm weight, or up for SiLU*up), with no LDS stage and no barrier.
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp, kCached>(u, 2 * tid, k, tbase, b);
     const float* second = kAOp == kAOpRmsAfter ? pro.rms_weight : pro.silu_up;
     float2 xv[kSteps], wv[kSteps];
 #pragma unroll
@@ -520,7 +526,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     // The attention combine per lane (AttnCombinePair): its pairs' partials are loaded with
     // the weights, so the row costs no extra memory round and no barrier.
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp, kCached>(u, 2 * tid, k, tbase, b);
     constexpr int kStride = 2 + kAttnDim;
     const int splits = pro.attn_splits;
     float2 ml[kSteps][kAttnRegSplits], ac[kSteps][kAttnRegSplits];
@@ -544,7 +550,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp>(u, 2 * tid, k, tbase, b);
+    for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp, kCached>(u, 2 * tid, k, tbase, b);
     __shared__ double part[S::kWaves];
     GemvArgs staged{};
     staged.a = a;
@@ -1172,10 +1178,17 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
       const int32_t mul = b.mode == kScalePerCol ? 1 : 0;
       const int32_t cidx = b.mode == kScalePerCol ? 0 : static_cast<int32_t>(b.const_index);
       const dim3 block(NarrowShape<1>::kThreads);
-#define ACCEL_GEMV_M1_K(ST, CL, PL, OP)                                                                        \
-  hipLaunchKernelGGL((GemvM1Kernel<ST, CL, PL, OP>), grid, block, 0, stream, b.tiled, a, b.scale, c,            \
+#define ACCEL_GEMV_M1_KC(ST, CL, PL, OP, CA)                                                                   \
+  hipLaunchKernelGGL((GemvM1Kernel<ST, CL, PL, OP, CA>), grid, block, 0, stream, b.tiled, a, b.scale, c,        \
                      static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),            \
                      static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi, pro)
+#define ACCEL_GEMV_M1_K(ST, CL, PL, OP)          \
+  do {                                           \
+    if (b.cached)                                \
+      ACCEL_GEMV_M1_KC(ST, CL, PL, OP, true);    \
+    else                                         \
+      ACCEL_GEMV_M1_KC(ST, CL, PL, OP, false);   \
+  } while (0)
 #define ACCEL_GEMV_M1(ST, CL)                                                               \
   do {                                                                                      \
     if (a_op == kAOpRms) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRms);                           \
@@ -1205,6 +1218,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
       }
 #undef ACCEL_GEMV_M1
 #undef ACCEL_GEMV_M1_K
+#undef ACCEL_GEMV_M1_KC
     } else if (a_op == kAOpRms) {
       // The staged row in LDS is 16-byte aligned and k is whole, so pairs load as one.
       if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpRms>), grid,

@@ -150,6 +150,21 @@ struct Model {
 
   hipStream_t stream() const { return Ctx().stream; }
 
+  // Whether a decode step's int8 weights and the KV cache fit in three quarters of MI355X's
+  // 256 MB last-level cache (MALL). Then the one-row GEMVs load their weights with plain
+  // loads, so the next token finds them cached (SmolLM2-135M: 106 MB of layers, 28 MB of LM
+  // head and 30 MB of KV cache at context 640; 0.558 -> 0.539 ms per token). A larger model
+  // streams them (nontemporal loads), which keeps other data cached and reads HBM faster.
+  bool cached_loads = false;
+  void SetLoadPolicy() {
+    const size_t h = static_cast<size_t>(cfg.hidden), inter = static_cast<size_t>(cfg.intermediate);
+    const size_t q = static_cast<size_t>(cfg.heads) * head_dim, kv = static_cast<size_t>(cfg.kv_heads) * head_dim;
+    const size_t layer = h * (q + 2 * kv) + q * h + h * 2 * inter + inter * h;
+    const size_t cache = 2 * static_cast<size_t>(cfg.context) * kv * sizeof(float);
+    const size_t total = static_cast<size_t>(cfg.layers) * (layer + cache) + static_cast<size_t>(cfg.vocab) * h;
+    cached_loads = total <= (size_t(192) << 20);
+  }
+
   bool Ready() const {
     if ((embed_f.empty() && embed_q.empty()) || final_norm.empty() || !lm_head.ready()) return false;
     for (const LayerWeights& l : layers)
@@ -167,6 +182,7 @@ struct Model {
       v.q = w.q.as<int8_t>();
       v.scale = w.scale.as<float>();
       v.mode = kScalePerCol;
+      v.cached = cached_loads;
       if (ctx.exact_products) {
         LaunchExactMatmul(a, nullptr, v, c, m, w.in, w.out, e, ctx.stream);
       } else if (m <= 16) {
@@ -200,6 +216,7 @@ struct Model {
     v.q = w.q.as<int8_t>();
     v.scale = w.scale.as<float>();
     v.mode = kScalePerCol;
+    v.cached = cached_loads;
     v.tiled = StagedColumnTiles(v.q, w.in, w.out, ctx.stream);
     LaunchGemvQ8(x, v, c, 1, w.in, w.out, e, ctx.stream, &pro);
   }
@@ -597,6 +614,7 @@ ACCEL_LLAMA_API AccelLlama* accel_llama_create(const AccelLlamaConfig* config) {
     m->cfg = *config;
     m->head_dim = config->hidden / config->heads;
     m->layers.resize(static_cast<size_t>(config->layers));
+    m->SetLoadPolicy();
     // RoPE tables in double, as src/llama_model.cc:333-349 builds them.
     const int32_t dim = m->head_dim, half = dim / 2;
     const size_t ctx = static_cast<size_t>(config->context);
