@@ -251,24 +251,33 @@ class JsonReader {
     if (i_ >= s_.size()) Error("unexpected end");
     Json v;
     const char c = s_[i_];
+    if ((c == '{' || c == '[') && ++depth_ > kMaxDepth) Error("nesting too deep");
     if (c == '{') {
       ++i_;
       v.kind = Json::kObject;
-      if (Take('}')) return v;
+      if (Take('}')) {
+        --depth_;
+        return v;
+      }
       do {
         std::string key = String();
         Need(':');
         v.members.emplace_back(std::move(key), Value());
       } while (Take(','));
       Need('}');
+      --depth_;
     } else if (c == '[') {
       ++i_;
       v.kind = Json::kArray;
-      if (Take(']')) return v;
+      if (Take(']')) {
+        --depth_;
+        return v;
+      }
       do {
         v.items.push_back(Value());
       } while (Take(','));
       Need(']');
+      --depth_;
     } else if (c == '"') {
       v.kind = Json::kString;
       v.text = String();
@@ -293,8 +302,10 @@ class JsonReader {
     return v;
   }
 
+  static constexpr int kMaxDepth = 64;  // tokenizer.json nests a few levels; bounds the recursion
   const std::string& s_;
   size_t i_ = 0;
+  int depth_ = 0;
 };
 
 // A non-negative integer id from a JSON number.

@@ -346,6 +346,10 @@ def test_loader_errors_on_unreadable_files(tmp_path):
         bad.write_text('{"model": {"vocab": {"a": 0}', encoding="utf-8")
         with pytest.raises(TokenizerError, match="json"):
             h.load(bad)
+        deep = tmp_path / "deep.json"
+        deep.write_text('{"model": ' + "[" * 100000 + "]" * 100000 + "}", encoding="utf-8")
+        with pytest.raises(TokenizerError, match="nesting too deep"):
+            h.load(deep)
     finally:
         h.close()
 
