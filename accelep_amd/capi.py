@@ -144,6 +144,10 @@ LLAMA_SIGNATURES = {
     "accel_llama_set_fused_inputs": (C.c_int, [C.c_void_p, C.c_int32]),
     "accel_llama_reset": (None, [C.c_void_p]),
     "accel_llama_last_error": (C.c_char_p, []),
+    "accel_sim_reset_stats": (None, []),
+    "accel_sim_matmuls": (C.c_int64, []),
+    "accel_sim_bytes_to_device": (C.c_int64, []),
+    "accel_sim_bytes_to_host": (C.c_int64, []),
 }
 
 

@@ -102,6 +102,8 @@ bool WorkspaceFits(size_t bytes);
 
 // Stats of include/accel/runtime.h (AcceleratorStats) and the packed-GEMM probes.
 void NoteKernelMatmul();
+// count kernel matmuls at once (a fused caller noting the reference's logical calls).
+void NoteKernelMatmuls(int64_t count);
 void NotePackedCall(int64_t k);
 void NoteBytesToDevice(size_t bytes);
 void NoteBytesToHost(size_t bytes);

@@ -262,6 +262,7 @@ bool FindAllocation(const void* ptr, uint64_t* id, const char** base, size_t* by
 }
 
 void NoteKernelMatmul() { g_stats.kernel_matmuls.fetch_add(1); }
+void NoteKernelMatmuls(int64_t count) { g_stats.kernel_matmuls.fetch_add(count); }
 void NotePackedCall(int64_t k) {
   g_packed_calls.fetch_add(1, std::memory_order_relaxed);
   g_packed_trips.fetch_add(k, std::memory_order_relaxed);

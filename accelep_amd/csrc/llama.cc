@@ -150,6 +150,13 @@ struct Model {
 
   hipStream_t stream() const { return Ctx().stream; }
 
+  // The reference's forward makes 7 MatMul calls per layer and one for the LM head, each
+  // noted as a kernel matmul (src/llama_model.cc:209-247, src/sim_device.cc:195,601). The
+  // fused kernels here do the same products in fewer launches; the counter keeps the
+  // reference's logical count, once per forward (prompt, forward_ids or decode step, also
+  // when the step is a graph replay).
+  void NoteForward() const { NoteKernelMatmuls(7 * static_cast<int64_t>(cfg.layers) + 1); }
+
   // Whether a decode step's int8 weights and the KV cache fit in three quarters of MI355X's
   // 256 MB last-level cache (MALL). Then the one-row GEMVs load their weights with plain
   // loads, so the next token finds them cached (SmolLM2-135M: 106 MB of layers, 28 MB of LM
@@ -365,6 +372,7 @@ struct Model {
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
     prompt_ids.Upload(prompt, static_cast<size_t>(prompt_count) * sizeof(int32_t));
     Forward(prompt_ids.as<int32_t>(), prompt_count, 0, true);
+    NoteForward();
     filled = prompt_count;
     const uint32_t rng0 = seed == 0 ? 0x6d2b79f5u : seed;
     uint32_t* rng = words.as<uint32_t>() + 1;
@@ -392,6 +400,7 @@ struct Model {
       }
       if (filled >= cfg.context) break;
       DecodeStep(state);
+      NoteForward();
       filled += 1;
     }
     if (produced > 0 && accel_hip_copy_d2h(out_ids, chosen.buffer(), static_cast<size_t>(produced) * sizeof(int32_t)) !=
@@ -833,6 +842,7 @@ ACCEL_LLAMA_API int accel_llama_forward_ids(AccelLlama* handle, const int32_t* i
     if (m->filled < 0 || count > m->cfg.context - m->filled) Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
     m->prompt_ids.Upload(ids, static_cast<size_t>(count) * sizeof(int32_t));
     m->Forward(m->prompt_ids.as<int32_t>(), count, 0, true);
+    m->NoteForward();
     m->filled += count;
   });
 }
@@ -895,5 +905,25 @@ ACCEL_LLAMA_API void accel_llama_reset(AccelLlama* handle) {
 }
 
 ACCEL_LLAMA_API const char* accel_llama_last_error(void) { return g_llama_error.c_str(); }
+
+ACCEL_LLAMA_API void accel_sim_reset_stats(void) { accel_hip_reset_stats(); }
+
+ACCEL_LLAMA_API int64_t accel_sim_matmuls(void) {
+  AccelHipStats s{};
+  accel_hip_get_stats(&s);
+  return s.kernel_matmuls;
+}
+
+ACCEL_LLAMA_API int64_t accel_sim_bytes_to_device(void) {
+  AccelHipStats s{};
+  accel_hip_get_stats(&s);
+  return s.bytes_to_device;
+}
+
+ACCEL_LLAMA_API int64_t accel_sim_bytes_to_host(void) {
+  AccelHipStats s{};
+  accel_hip_get_stats(&s);
+  return s.bytes_to_host;
+}
 
 }  // extern "C"

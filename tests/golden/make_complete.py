@@ -6,7 +6,8 @@ golden_cases.complete_config() / COMPLETE_WEIGHT_SEED.
     make -C oracle && python3 tests/golden/make_complete.py
 
 Each case keeps the prompt, the sampling arguments and what the reference returned: the ids,
-the ids its token callback saw, the completion text and the prompt's token count.
+the ids its token callback saw, the completion text, the prompt's token count, and the
+simulator's counters over the call (accel_sim_matmuls, bytes to the device and to the host).
 """
 
 from __future__ import annotations
@@ -41,6 +42,8 @@ def open_reference():
         C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_uint32, C.c_int32, C.c_char_p,
         C.c_int32, I32P, I32P, C.c_int32, I32P, I32P, TOKEN_FN, C.c_void_p]
     L.accel_llama_last_error.restype = C.c_char_p
+    for name in ("accel_sim_matmuls", "accel_sim_bytes_to_device", "accel_sim_bytes_to_host"):
+        getattr(L, name).restype = C.c_int64
     cfg = complete_config()
     h = L.accel_llama_create(C.byref(LlamaConfig(**cfg)))
     assert h, L.accel_llama_last_error()
@@ -64,12 +67,15 @@ def complete(L, h, prompt, max_new, eos, temperature, seed, top_k):
     prompt_tokens = C.c_int32(-1)
     seen = []
     cb = TOKEN_FN(lambda tok, user: seen.append(int(tok)))
+    L.accel_sim_reset_stats()
     rc = L.accel_llama_complete_stream(h, data, len(data), max_new, eos, temperature, seed, top_k, text, 1 << 16,
                                        C.byref(text_len), ids.ctypes.data_as(I32P), max_new, C.byref(count),
                                        C.byref(prompt_tokens), cb, None)
     assert rc == 0, L.accel_llama_last_error()
+    counters = dict(matmuls=L.accel_sim_matmuls(), bytes_to_device=L.accel_sim_bytes_to_device(),
+                    bytes_to_host=L.accel_sim_bytes_to_host())
     return dict(ids=ids[: count.value].tolist(), stream_ids=seen, text=text.raw[: text_len.value].decode("utf-8"),
-                prompt_tokens=prompt_tokens.value)
+                prompt_tokens=prompt_tokens.value, counters=counters)
 
 
 def main():

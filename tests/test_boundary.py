@@ -51,7 +51,7 @@ def test_python_mirror_binds_every_symbol():
 
 
 def declared_llama_entry_points():
-    return re.findall(r"ACCEL_LLAMA_API\s+[\w\s\*]+?\b(accel_llama_\w+)\s*\(", LLAMA_HEADER.read_text())
+    return re.findall(r"ACCEL_LLAMA_API\s+[\w\s\*]+?\b(accel_(?:llama|sim)_\w+)\s*\(", LLAMA_HEADER.read_text())
 
 
 def test_library_exports_nothing_else():
@@ -68,6 +68,9 @@ def test_llama_api_mirrors_the_reference_names():
     for want in ["create", "destroy", "weight", "tokenizer", "generate", "encode", "decode", "complete",
                  "complete_stream", "forward_ids", "logit_max_abs", "reset", "last_error"]:
         assert f"accel_llama_{want}" in names
+    # the stats calls serve/llama.py binds beside them (include/accel/sim_api.h:30-33)
+    for want in ["reset_stats", "matmuls", "bytes_to_device", "bytes_to_host"]:
+        assert f"accel_sim_{want}" in names
 
 
 CPP_API = [

@@ -9,7 +9,8 @@ tokenizer oracle (oracle/bpe.py, pinned in tests/test_tokenizer.py).
   count, for float and int8 weights in both product modes (the same ids as
   tests/test_gpu_llama.py requires of generate);
 * complete's ids equal generate's on the encoded prompt; the copy counters hold the prompt
-  ids in, the ids and the text out (AccelEP tests/test_serve.py:363-364);
+  ids in, the ids and the text out (AccelEP tests/test_serve.py:363-364), and accel_sim_matmuls
+  and the byte counters read what the reference's read over the same completion;
 * every error of src/llama_model.cc:183-206 and :449-551 is raised with its message.
 """
 
@@ -144,7 +145,11 @@ def test_complete_matches_the_reference(weights, products, orc):
     try:
         for c in _golden()["cases"]:
             print(f"complete {c['name']} weights={weights} exact={products}", flush=True)
+            m.L.accel_sim_reset_stats()
             got = m.complete(c["prompt"], c["max_new"], c["eos"], c["temperature"], c["seed"], c["top_k"])
+            counters = dict(matmuls=m.L.accel_sim_matmuls(), bytes_to_device=m.L.accel_sim_bytes_to_device(),
+                            bytes_to_host=m.L.accel_sim_bytes_to_host())
+            assert counters == c["counters"]  # the reference's accel_sim_* over the same call
             assert got["ids"] == c["ids"]
             assert got["stream_ids"] == c["stream_ids"] == c["ids"]
             assert got["text"] == c["text"] == orc.decode(c["ids"], True)
