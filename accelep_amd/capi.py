@@ -144,10 +144,20 @@ LLAMA_SIGNATURES = {
     "accel_llama_set_fused_inputs": (C.c_int, [C.c_void_p, C.c_int32]),
     "accel_llama_reset": (None, [C.c_void_p]),
     "accel_llama_last_error": (C.c_char_p, []),
+}
+
+# include/accel_sim.h
+SIM_SIGNATURES = {
+    "accel_sim_create": (C.c_void_p, []),
+    "accel_sim_destroy": (None, [C.c_void_p]),
+    "accel_sim_upload": (C.c_void_p, [C.c_void_p, F32P, i64]),
+    "accel_sim_release": (None, [C.c_void_p, C.c_void_p]),
+    "accel_sim_matmul": (C.c_int, [C.c_void_p, F32P, i64, i64, C.c_void_p, i64, F32P]),
     "accel_sim_reset_stats": (None, []),
     "accel_sim_matmuls": (C.c_int64, []),
     "accel_sim_bytes_to_device": (C.c_int64, []),
     "accel_sim_bytes_to_host": (C.c_int64, []),
+    "accel_sim_last_error": (C.c_char_p, []),
 }
 
 
@@ -162,7 +172,7 @@ def lib() -> C.CDLL:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m accelep_amd.build`")
         handle = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in {**SIGNATURES, **LLAMA_SIGNATURES}.items():
+        for name, (res, args) in {**SIGNATURES, **LLAMA_SIGNATURES, **SIM_SIGNATURES}.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args

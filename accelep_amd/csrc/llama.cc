@@ -906,24 +906,4 @@ ACCEL_LLAMA_API void accel_llama_reset(AccelLlama* handle) {
 
 ACCEL_LLAMA_API const char* accel_llama_last_error(void) { return g_llama_error.c_str(); }
 
-ACCEL_LLAMA_API void accel_sim_reset_stats(void) { accel_hip_reset_stats(); }
-
-ACCEL_LLAMA_API int64_t accel_sim_matmuls(void) {
-  AccelHipStats s{};
-  accel_hip_get_stats(&s);
-  return s.kernel_matmuls;
-}
-
-ACCEL_LLAMA_API int64_t accel_sim_bytes_to_device(void) {
-  AccelHipStats s{};
-  accel_hip_get_stats(&s);
-  return s.bytes_to_device;
-}
-
-ACCEL_LLAMA_API int64_t accel_sim_bytes_to_host(void) {
-  AccelHipStats s{};
-  accel_hip_get_stats(&s);
-  return s.bytes_to_host;
-}
-
 }  // extern "C"

@@ -122,16 +122,8 @@ ACCEL_LLAMA_API int accel_llama_logits(AccelLlama* model, float* out, int32_t co
 ACCEL_LLAMA_API int accel_llama_set_fused_inputs(AccelLlama* model, int32_t enable);
 ACCEL_LLAMA_API void accel_llama_reset(AccelLlama* model);
 ACCEL_LLAMA_API const char* accel_llama_last_error(void);
-
-/* The simulator's stats calls (include/accel/sim_api.h:30-33, src/sim_api.cc:109-115), which
- * serve/llama.py binds beside the accel_llama_* calls: reset, kernel matmuls, and counted bytes
- * to the device and to the host (the accel_hip_get_stats fields of the same names). A Llama
- * forward notes the reference's 7 MatMul calls per layer plus the LM head, though its fused
- * kernels make fewer launches. */
-ACCEL_LLAMA_API void accel_sim_reset_stats(void);
-ACCEL_LLAMA_API int64_t accel_sim_matmuls(void);
-ACCEL_LLAMA_API int64_t accel_sim_bytes_to_device(void);
-ACCEL_LLAMA_API int64_t accel_sim_bytes_to_host(void);
+/* The stats serve/llama.py reads beside these calls (accel_sim_reset_stats, accel_sim_matmuls,
+ * accel_sim_bytes_to_device / _to_host) are declared in accel_sim.h. */
 
 #ifdef __cplusplus
 }

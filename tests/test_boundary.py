@@ -15,6 +15,7 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "accel_hip.h"
 LLAMA_HEADER = ROOT / "include" / "accel_llama.h"
+SIM_HEADER = ROOT / "include" / "accel_sim.h"
 LIB = ROOT / "accelep_amd" / "libaccel_hip.so"
 RUNTIME_LIB = ROOT / "accelep_amd" / "libaccel_runtime.so"
 
@@ -51,13 +52,18 @@ def test_python_mirror_binds_every_symbol():
 
 
 def declared_llama_entry_points():
-    return re.findall(r"ACCEL_LLAMA_API\s+[\w\s\*]+?\b(accel_(?:llama|sim)_\w+)\s*\(", LLAMA_HEADER.read_text())
+    return re.findall(r"ACCEL_LLAMA_API\s+[\w\s\*]+?\b(accel_llama_\w+)\s*\(", LLAMA_HEADER.read_text())
+
+
+def declared_sim_entry_points():
+    return re.findall(r"ACCEL_SIM_API\s+[\w\s\*]+?\b(accel_sim_\w+)\s*\(", SIM_HEADER.read_text())
 
 
 def test_library_exports_nothing_else():
     out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout
     exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
-    assert exported == set(declared_entry_points()) | set(declared_llama_entry_points())
+    assert exported == set(declared_entry_points()) | set(declared_llama_entry_points()) | set(
+        declared_sim_entry_points())
 
 
 def test_llama_api_mirrors_the_reference_names():
@@ -68,9 +74,17 @@ def test_llama_api_mirrors_the_reference_names():
     for want in ["create", "destroy", "weight", "tokenizer", "generate", "encode", "decode", "complete",
                  "complete_stream", "forward_ids", "logit_max_abs", "reset", "last_error"]:
         assert f"accel_llama_{want}" in names
-    # the stats calls serve/llama.py binds beside them (include/accel/sim_api.h:30-33)
-    for want in ["reset_stats", "matmuls", "bytes_to_device", "bytes_to_host"]:
-        assert f"accel_sim_{want}" in names
+
+
+def test_sim_api_mirrors_the_reference_names():
+    """The standalone calls of include/accel/sim_api.h:16-37, which serve/sim.py and
+    serve/llama.py bind."""
+    from accelep_amd.capi import SIM_SIGNATURES
+
+    names = set(declared_sim_entry_points())
+    assert names == set(SIM_SIGNATURES)
+    assert names == {f"accel_sim_{n}" for n in ["create", "destroy", "upload", "release", "matmul", "reset_stats",
+                                                 "matmuls", "bytes_to_device", "bytes_to_host", "last_error"]}
 
 
 CPP_API = [
