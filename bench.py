@@ -641,7 +641,7 @@ def main():
             "frac": round(gbs1 / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
             "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
-            "kernel": "GemvM1Kernel<8,false,true,0> (accelep_amd/csrc/gemv_q8.hip)",
+            "kernel": "GemvM1Kernel<8,false,true,0,false> (accelep_amd/csrc/gemv_q8.hip)",
             "algorithmic_bytes_per_launch": gemv_bytes(1),
             "avg_launch_us_event_timed": round(per1 * 1e3, 3),
         },
