@@ -157,18 +157,19 @@ struct Model {
   // when the step is a graph replay).
   void NoteForward() const { NoteKernelMatmuls(7 * static_cast<int64_t>(cfg.layers) + 1); }
 
-  // Whether a decode step's int8 weights and the KV cache fit in three quarters of MI355X's
-  // 256 MB last-level cache (MALL). Then the one-row GEMVs load their weights with plain
-  // loads, so the next token finds them cached (SmolLM2-135M: 106 MB of layers, 28 MB of LM
-  // head and 30 MB of KV cache at context 640; 0.558 -> 0.539 ms per token). A larger model
-  // streams them (nontemporal loads), which keeps other data cached and reads HBM faster.
+  // Whether a decode step's int8 weights (the layers and the LM head) fit in three quarters of
+  // MI355X's 256 MB last-level cache (MALL). Then the one-row GEMVs load their weights with
+  // plain loads, so the next token finds them cached (SmolLM2-135M: 106 MB of layers and
+  // 28 MB of LM head; 0.558 -> 0.539 ms per token at context 640). The KV cache is not
+  // counted: a step reads its rows up to the position only, and the attention's plain loads
+  // share the cache either way. A larger model streams its weights (nontemporal loads), which
+  // keeps other data cached and reads HBM faster.
   bool cached_loads = false;
   void SetLoadPolicy() {
     const size_t h = static_cast<size_t>(cfg.hidden), inter = static_cast<size_t>(cfg.intermediate);
     const size_t q = static_cast<size_t>(cfg.heads) * head_dim, kv = static_cast<size_t>(cfg.kv_heads) * head_dim;
     const size_t layer = h * (q + 2 * kv) + q * h + h * 2 * inter + inter * h;
-    const size_t cache = 2 * static_cast<size_t>(cfg.context) * kv * sizeof(float);
-    const size_t total = static_cast<size_t>(cfg.layers) * (layer + cache) + static_cast<size_t>(cfg.vocab) * h;
+    const size_t total = static_cast<size_t>(cfg.layers) * layer + static_cast<size_t>(cfg.vocab) * h;
     cached_loads = total <= (size_t(192) << 20);
   }
 
