@@ -298,6 +298,32 @@ def llama_q8_weights(cfg, rng):
             yield kind, layer, q, sc
 
 
+# Kernels of one graph-replayed decode token: per layer the q/k/v GEMV, the split attention,
+# the o, gate/up and down GEMVs; then the embedding, the final RMSNorm, the LM head and the
+# position advance in the graph, and the greedy pick launched between replays.
+def decode_kernels_per_token(cfg):
+    return 5 * cfg["layers"] + 5
+
+
+def graph_node_floor_us(hip, nodes, reps=20):
+    """Microseconds per node of a graph of `nodes` dependent minimal kernels (ResidualAdd over 64
+    floats, each reading what the previous one wrote), replayed `reps` times after one untimed
+    replay: the launch and memory round trip that a decode token's dependent kernels each pay
+    before any of their own work."""
+    buf = hip.DeviceArray.from_numpy(np.zeros(64, np.float32))
+
+    def step(i):
+        hip.check(hip.L.accel_hip_residual_add(buf.buffer, buf.buffer, 64))
+
+    g = hip.graph(step, nodes)
+    try:
+        hip.check(hip.L.accel_hip_graph_launch(g, 1))
+        ms = hip.time_graph([(g, reps)])
+    finally:
+        hip.L.accel_hip_graph_destroy(g)
+    return ms * 1e3 / (nodes * reps)
+
+
 def bench_llama(hip, rng, reps=3):
     """SmolLM2-135M-shape Llama on the GPU (accel_llama_*): the int8 weights of
     llama_q8_weights, 512 random prompt ids, 128 greedy tokens. Prefill = generate with one
@@ -336,10 +362,16 @@ def bench_llama(hip, rng, reps=3):
         pre = min(generate(1) for _ in range(reps))
         full = min(generate(129) for _ in range(reps))
         decode = max(full - pre, 1e-9)
+        kernels = decode_kernels_per_token(cfg)
+        floor_us = graph_node_floor_us(hip, kernels)
+        token_ms = decode / 128 * 1e3
         return {"prefill_ms": round(pre * 1e3, 2), "prefill_tok_s": round(512 / pre, 1),
-                "decode_ms_per_token": round(decode / 128 * 1e3, 4), "decode_tok_s": round(128 / decode, 1),
+                "decode_ms_per_token": round(token_ms, 4), "decode_tok_s": round(128 / decode, 1),
                 "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / LLAMA_DECODE_BYTES, 1),
                 "decode_roofline_frac": round((128 / decode) / (HBM_PEAK_GBS * 1e9 / LLAMA_DECODE_BYTES), 4),
+                "decode_kernels_per_token": kernels, "graph_node_floor_us": round(floor_us, 3),
+                "decode_node_floor_ms": round(kernels * floor_us / 1e3, 4),
+                "decode_node_floor_frac": round(kernels * floor_us / 1e3 / token_ms, 4),
                 "config": "SmolLM2-135M shape (30 layers, hidden 576, 9/3 heads, inter 1536, vocab 49152), "
                           "linear weights and tied embedding/LM head N(0,0.02) quantized to int8 per output row, "
                           "norms N(1,0.1), 512 random prompt ids, 128 greedy tokens, wall clock, best of 3"}
