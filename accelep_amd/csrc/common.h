@@ -160,10 +160,10 @@ bool FindAllocation(const void* ptr, uint64_t* id, const char** base, size_t* by
 void DropStagedForAllocation(uint64_t id);
 void LaunchTileColumns(const int8_t* q, int64_t k, int64_t n, int8_t* dst, hipStream_t stream);
 // Group-interleaved copy for the m > 1 GEMV (k a multiple of kGemvGroupRows): the 8-column
-// tiles in groups of kGemvGroupTiles; for group G, row octet o (rows 8o .. 8o + 7) and tile
-// slot j, the 64 bytes of those rows of tile 16G + j (row-major, 8 bytes a row) sit at
-// ((G * k/8 + o) * 16 + j) * 64, so the 16 tiles' rows of one octet are 1 KB contiguous.
-// Tiles past the last column are zero.
+// tiles in groups of kGemvGroupTiles. For group G, slot o of the 32-row blocks (block
+// b = o / 4, h = o % 4) and tile slot j, the 64 bytes at ((G * k/8 + o) * 16 + j) * 64 are
+// four 16-byte pieces p = 0..3, each rows 32b + 8p + 2h and 32b + 8p + 2h + 1 of tile 16G + j
+// (row-major, 8 bytes a row); 1 KB contiguous per slot o. Tiles past the last column are zero.
 constexpr int64_t kGemvGroupTiles = 16;
 constexpr int64_t kGemvGroupRows = 32;
 inline size_t StagedGroupBytes(int64_t k, int64_t n) {
@@ -258,7 +258,7 @@ constexpr int64_t kGemvPrologueMaxK = 4096;
 constexpr int64_t kGemvAttnMaxPairs = 2048;  // heads x splits of GemvPrologue::attn_partial
 
 // C[m, n] = A[m, k] @ dequant(Bq)[k, n] for m <= 16 (int8 GEMV). With b.grouped (and no zero
-// points or per-row scale, k % 32 == 0, A 8-byte aligned) the split-bf16 MFMA kernel runs;
+// points or per-row scale, k % 32 == 0, A 16-byte aligned) the split-bf16 MFMA kernel runs;
 // with b.tiled the 8-column tile kernels; otherwise W is read in place. A prologue needs m == 1,
 // staged tiles, a per-column or whole-tensor scale without zero points and k <=
 // kGemvPrologueMaxK.

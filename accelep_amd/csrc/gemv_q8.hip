@@ -752,9 +752,10 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
 // A workgroup (4 waves) owns one group of 16 staged tiles (128 columns) over one split of K.
 // Lane l takes tile slot l % 16 as the B column of its MFMAs and, for the 8 columns c of that
 // tile, the operand of the c-th MFMA. A 32-row block is read as 4 loads of 16 bytes per lane:
-// load h of lane group g = l / 16 holds rows 8h + 2g and 8h + 2g + 1 of the tile, so one load
-// of the wave is the 1 KB octet of all 16 tiles; A lane (row l % 16, group g) loads the same
-// rows of A, so the k slots agree. The waves take interleaved blocks, and their sums are added
+// load h of lane group g = l / 16 holds rows 8g + 2h and 8g + 2h + 1 of the tile (one load of
+// the wave is 1 KB of the staged copy), so lane group g's four loads are rows 8g .. 8g + 7
+// and A lane (row l % 16, group g) reads those 8 activations as two 16-byte loads; the k
+// slots agree. The waves take interleaved blocks, and their sums are added
 // through LDS in wave order. With splits, each workgroup stores its partial sums and the last
 // one of a group to arrive adds them in split order and applies the scale and the epilogue.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -793,7 +794,7 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
   const int blocks = static_cast<int>((ke - kb) / kSplitBlockRows);
   const int8_t* tb = p.grouped + (static_cast<int64_t>(group) * p.k + kb) * kSplitGroupBytes + 64 * slot + 16 * g;
   const bool row_live = slot < p.m;
-  const float* ab = p.a + static_cast<int64_t>(row_live ? slot : p.m - 1) * p.k + kb + 2 * g;
+  const float* ab = p.a + static_cast<int64_t>(row_live ? slot : p.m - 1) * p.k + kb + 8 * g;
 
   v4f acc[kNarrowTile];
 #pragma unroll
@@ -807,12 +808,15 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
       const int blk = b0 + u * kSplitWaves;
       const int bc = blk < blocks ? blk : blocks - 1;  // a valid block; its A is zeroed below
       const u32x4* wb = reinterpret_cast<const u32x4*>(tb + static_cast<int64_t>(bc) * (kSplitBlockRows * kSplitGroupBytes));
-      const f32x2* xb = reinterpret_cast<const f32x2*>(ab + static_cast<int64_t>(bc) * kSplitBlockRows);
+      const v4f* xb = reinterpret_cast<const v4f*>(ab + static_cast<int64_t>(bc) * kSplitBlockRows);
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        w[u][h] = __builtin_nontemporal_load(wb + 64 * h);  // octet h: rows 8h + 2g, 8h + 2g + 1
-        x[u][h] = xb[4 * h];
-      }
+      for (int h = 0; h < 4; ++h) w[u][h] = __builtin_nontemporal_load(wb + 64 * h);  // rows 8g + 2h, 8g + 2h + 1
+      // This lane's 8 activations of the block, rows 8g .. 8g + 7: two 16-byte loads.
+      const v4f x0 = xb[0], x1 = xb[1];
+      x[u][0] = f32x2{x0[0], x0[1]};
+      x[u][1] = f32x2{x0[2], x0[3]};
+      x[u][2] = f32x2{x1[0], x1[1]};
+      x[u][3] = f32x2{x1[2], x1[3]};
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any is used
 #pragma unroll
@@ -829,7 +833,7 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
         am[h] = PackBf16(r0, r1);
         al[h] = PackBf16(r0 - Bf16Low(am[h]), r1 - Bf16High(am[h]));
       }
-      // Column c of the tile: row 8h + 2g in byte c of words 0..1 of load h, row 8h + 2g + 1
+      // Column c of the tile: row 8g + 2h in byte c of words 0..1 of load h, row 8g + 2h + 1
       // in words 2..3.
       u32x4 bw[kNarrowTile];
 #pragma unroll
@@ -942,7 +946,8 @@ __global__ void TileGroupsKernel(const int8_t* q, int64_t k, int64_t n, int8_t* 
     const int64_t col = (grp * kSplitTiles + j) * kNarrowTile;
     uint32_t w[4] = {0, 0, 0, 0};
     for (int h = 0; h < 2; ++h) {
-      const int64_t r = 8 * o + 2 * pair + h;
+      // Piece (octet o, pair) of a 32-row block holds rows 8 * pair + 2 * (o % 4) + h of it.
+      const int64_t r = 32 * (o >> 2) + 8 * pair + 2 * (o & 3) + h;
       if (vec && col + 7 < n) {
         const uint2 v = *reinterpret_cast<const uint2*>(q + r * n + col);
         w[2 * h] = v.x;
@@ -1079,10 +1084,10 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   // them the wide kernel, which reads W in place, takes any m <= 16.
   const bool zero = b.zero != nullptr;
   const bool row_scale = b.mode == kScalePerRow;
-  // The split-bf16 MFMA kernel: group-interleaved copy, whole 32-row blocks, A 8-byte aligned.
+  // The split-bf16 MFMA kernel: group-interleaved copy, whole 32-row blocks, A 16-byte aligned.
   const bool split_bf16 = m > 1 && b.grouped != nullptr && !zero && !row_scale && a_op == kAOpNone &&
                           k % kSplitBlockRows == 0 && k < (int64_t(1) << 28) && m * n <= 0x7fffffff &&
-                          reinterpret_cast<uintptr_t>(a) % 8 == 0 && (b.mode == kScalePerCol || b.mode == kScaleConst);
+                          reinterpret_cast<uintptr_t>(a) % 16 == 0 && (b.mode == kScalePerCol || b.mode == kScaleConst);
   const bool narrow = !split_bf16 && m <= 4 && b.tiled != nullptr && k < (int64_t(1) << 28);
   const int64_t tile_cols = narrow || split_bf16 ? kNarrowTile : kWideTile;
   const int64_t tiles = (n + tile_cols - 1) / tile_cols;
