@@ -39,6 +39,8 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16X3_PEAK_TFLOPS = 2500.0 / 3
 K_DIM, N_DIM = 4096, 14336
 COPIES = 8
+C1_SHAPE = (4, 576, 1536)  # X[4,576] @ int8 W[576,1536]
+MLP_SHAPE = (256, 1024, 4096)  # X[256,1024] -> 4096 -> 1024
 
 
 def gemv_bytes(m, k=K_DIM, n=N_DIM):
@@ -215,12 +217,8 @@ def bench_mlp(hip, steps, warmup, rng):
     """fp32 MLP X[256,1024] -> Gemm(1024x4096)+bias -> Gelu -> Gemm(4096x1024)+bias + X.
 
     Two fused calls per step (bias+gelu, bias+residual epilogues in registers)."""
-    m, d, h = 256, 1024, 4096
-    x = hip.DeviceArray.from_numpy(rng.standard_normal((m, d)).astype(np.float32))
-    w1 = hip.DeviceArray.from_numpy((rng.standard_normal((d, h)) * 0.02).astype(np.float32))
-    b1 = hip.DeviceArray.from_numpy((rng.standard_normal(h) * 0.02).astype(np.float32))
-    w2 = hip.DeviceArray.from_numpy((rng.standard_normal((h, d)) * 0.02).astype(np.float32))
-    b2 = hip.DeviceArray.from_numpy((rng.standard_normal(d) * 0.02).astype(np.float32))
+    m, d, h = MLP_SHAPE
+    x, w1, b1, w2, b2 = (hip.DeviceArray.from_numpy(v) for v in mlp_inputs(rng))
     hid = hip.DeviceArray((m, h))
     y = hip.DeviceArray((m, d))
     e1 = hip.Epilogue(alpha=1.0, beta=1.0, bias=b1.ptr, bias_rank=1, activation=2)
@@ -425,7 +423,10 @@ def _median_time(fn, runs):
     return float(np.median(times))
 
 
-def cpu_baseline(rng, runs=3):
+CPU_RUNS = 5  # every CPU leg: the median of this many timed runs after one warm-up
+
+
+def cpu_baseline(rng, runs=CPU_RUNS):
     """The reference's MatMulQuantized (compiled AccelEP sources) on the M=1 headline workload,
     pinned to one core; median of `runs` after one warm-up call."""
     sys.path.insert(0, str(ROOT / "tests"))
@@ -450,11 +451,12 @@ def cpu_baseline(rng, runs=3):
                    f"{'AccelEP MatMulQuantized (src/sim_device.cc:541-602) compiled -O2' if ref else 'oracle port'}, "
                    f"one thread pinned to CPU {core.cpu} ({cpu_model()}; host has {os.cpu_count()} logical CPUs), "
                    f"median of {runs} after a warm-up: {best:.2f} s/call"),
+        "cpu_model": cpu_model(),
         "seconds_per_call": round(best, 3),
     }
 
 
-def cpu_prefill_sample(rng, rows=64, cols=N_DIM // 8):
+def cpu_prefill_sample(rng, rows=64, cols=N_DIM // 8, runs=CPU_RUNS):
     """C4 on the reference path is hours, so it is timed on a block: X[rows,4096] @ int8
     W[4096,cols] (per-column scale) plus SimRmsNorm of the block's rows, pinned to one core, and
     extrapolated linearly to 2048 rows and 14336 columns (the reference blocks M by 64 and N by
@@ -474,17 +476,18 @@ def cpu_prefill_sample(rng, rows=64, cols=N_DIM // 8):
         def run():
             c = ref.matmul_quantized(a, None, None, plane, rows, K_DIM, cols)
             ref.rmsnorm(c, g, rows, cols, 1e-5, 0)
-        t = _median_time(run, 2)
+        run()
+        t = _median_time(run, runs)
     scale = (2048 / rows) * (N_DIM / cols)
     total = t * scale
     return {"seconds_extrapolated": round(total, 1), "TFLOP/s": round(2 * 2048 * K_DIM * N_DIM / total / 1e12, 6),
             "cores": 1, "kind": "reference", "extrapolated": True,
             "sample": (f"AccelEP MatMulQuantized + SimRmsNorm on X[{rows},4096] @ int8 W[4096,{cols}], one thread "
-                       f"pinned to CPU {core.cpu}, median of 2: {t:.2f} s, times {scale:.0f} for the full "
+                       f"pinned to CPU {core.cpu}, median of {runs} after a warm-up: {t:.2f} s, times {scale:.0f} for the full "
                        f"2048 x 4096 x 14336 workload (extrapolated)")}
 
 
-def cpu_llama_sample(rng, prompt_ids=32, new=16):
+def cpu_llama_sample(rng, prompt_ids=32, new=16, runs=CPU_RUNS):
     """C5 on the reference path (accel_llama_* of AccelEP's llama_model.cc through oracle/_ref)
     on a bounded sample: the SmolLM2-135M shape with the same weight generator (float weights
     fl(q*s), as the reference takes them), a `prompt_ids`-id prompt and `new` greedy tokens,
@@ -522,16 +525,100 @@ def cpu_llama_sample(rng, prompt_ids=32, new=16):
             return time.perf_counter() - t0
 
         with OneCore() as core:
-            pre = generate(1)
-            full = generate(new + 1)
+            generate(1)
+            pre = float(np.median([generate(1) for _ in range(runs)]))
+            full = float(np.median([generate(new + 1) for _ in range(runs)]))
         decode = max(full - pre, 1e-9) / new
         return {"prefill_tok_s": round(prompt_ids / pre, 2), "decode_s_per_token": round(decode, 4),
                 "decode_tok_s": round(1 / decode, 3), "cores": 1, "kind": "reference",
                 "sample": (f"AccelEP LlamaModel Generate (src/llama_model.cc) compiled -O2, SmolLM2-135M shape, "
                            f"{prompt_ids}-id prompt ({pre:.2f} s) + {new} greedy tokens ({full - pre:.2f} s), "
-                           f"one thread pinned to CPU {core.cpu}")}
+                           f"one thread pinned to CPU {core.cpu}, medians of {runs} after a warm-up")}
     finally:
         L.accel_llama_destroy(h)
+
+
+def mlp_inputs(rng):
+    """The C2 MLP's operands: X[256,1024] ~ N(0,1); W1[1024,4096], b1, W2[4096,1024], b2 ~ N(0,0.02)."""
+    m, d, h = MLP_SHAPE
+    x = rng.standard_normal((m, d)).astype(np.float32)
+    w1 = (rng.standard_normal((d, h)) * 0.02).astype(np.float32)
+    b1 = (rng.standard_normal(h) * 0.02).astype(np.float32)
+    w2 = (rng.standard_normal((h, d)) * 0.02).astype(np.float32)
+    b2 = (rng.standard_normal(d) * 0.02).astype(np.float32)
+    return x, w1, b1, w2, b2
+
+
+def cpu_mlp(rng, runs=CPU_RUNS):
+    """C2 on the reference path, the whole workload: SimDevice::MatMul (PackedMatMul,
+    src/sim_device.cc:185-196,331-369), GemmEpilogue with bias and exact Gelu (:211-245), the
+    second MatMul, GemmEpilogue with bias, and the residual as the runtime issues it
+    (GemmEpilogue over m = 1, n = count with X as the bias, src/runtime.cc:332-344), through the
+    compiled reference, pinned to one core; median of `runs` after one warm-up step."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ctypes import reference
+
+    ref = reference()
+    if ref is None:
+        return None
+    m, d, h = MLP_SHAPE
+    x, w1, b1, w2, b2 = mlp_inputs(rng)
+
+    def step():
+        hid = ref.gemm_epilogue(ref.device_matmul(x, w1), 1.0, b1, [h], 1.0, 2)
+        y = ref.gemm_epilogue(ref.device_matmul(hid, w2), 1.0, b2, [d], 1.0, 0)
+        return ref.gemm_epilogue(y.reshape(1, m * d), 1.0, x.reshape(-1), [m * d], 1.0, 0)
+
+    with OneCore() as core:
+        step()
+        t = _median_time(step, runs)
+    flops = 2 * m * d * h * 2
+    return {"seconds_per_step": round(t, 3), "TFLOP/s": round(flops / t / 1e12, 6), "cores": 1, "kind": "reference",
+            "sample": (f"the whole C2 step through AccelEP SimDevice (src/sim_device.cc MatMul + GemmEpilogue, "
+                       f"residual as src/runtime.cc:332-344 issues it) compiled -O2, one thread pinned to CPU "
+                       f"{core.cpu}, median of {runs} after a warm-up: {t:.2f} s/step")}
+
+
+def bench_c1(hip, steps, warmup, rng):
+    """C1: X fp32[4,576] @ DequantizeLinear(int8 W[576,1536], per-column scale, zero point 0) as
+    accel::MatMulQuantized, one call a step. Returns (ms_per_step, GB/s of algorithmic bytes)."""
+    m, k, n = C1_SHAPE
+    q = hip.DeviceArray.from_numpy(rng.integers(-127, 128, size=k * n, dtype=np.int8))
+    s = hip.DeviceArray.from_numpy(rng.uniform(1e-3, 1e-2, size=n).astype(np.float32))
+    plane = hip.quant_plane(q, s, None, [k, n], 1)
+    x = hip.DeviceArray.from_numpy(rng.standard_normal((m, k)).astype(np.float32))
+    out = hip.DeviceArray((m, n))
+
+    def step(i):
+        hip.check(hip.L.accel_hip_matmul_quantized(x.ptr, None, None, C.byref(plane), out.ptr, m, k, n))
+
+    ms = timed_steps(hip, step, steps, warmup)
+    per = ms / steps
+    return per, gemv_bytes(m, k, n) / (per * 1e-3) / 1e9
+
+
+def cpu_c1(rng, runs=CPU_RUNS):
+    """C1 on the reference path: AccelEP's MatMulQuantized (src/sim_device.cc:541-602) on
+    X[4,576] @ int8 W[576,1536] with a per-column scale, pinned to one core; median of `runs`
+    after one warm-up call."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ctypes import make_plane, reference
+
+    ref = reference()
+    if ref is None:
+        return None
+    m, k, n = C1_SHAPE
+    q = rng.integers(-127, 128, size=k * n, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    plane, keep = make_plane(q, s, None, [k, n], 1)
+    with OneCore() as core:
+        ref.matmul_quantized(a, None, None, plane, m, k, n)
+        t = _median_time(lambda: ref.matmul_quantized(a, None, None, plane, m, k, n), runs)
+    return {"seconds_per_call": round(t, 5), "GB/s": round(gemv_bytes(m, k, n) / t / 1e9, 5), "cores": 1,
+            "kind": "reference",
+            "sample": (f"the whole C1 call, AccelEP MatMulQuantized compiled -O2, one thread pinned to CPU {core.cpu}, "
+                       f"median of {runs} after a warm-up: {t * 1e3:.1f} ms/call")}
 
 
 def main():
@@ -605,6 +692,11 @@ def main():
                                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                                        "TFLOP/s": round(flops / (per * 1e-3) / 1e12, 2), "steps": steps_g}
             log(f"gemv M={m}: {per * 1e3:.2f} us/step, {gbs:.1f} GB/s")
+        per, gbs = bench_c1(hip, steps_g, args.warmup, rng)
+        secondary["c1_dequant_matmul"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1), "steps": steps_g,
+                                          "config": "X fp32[4,576] @ int8 W[576,1536], per-column scale (C1)",
+                                          "note": "latency-bound: 0.92 MB, one launch"}
+        log(f"c1 4x576x1536: {per * 1e3:.2f} us/step")
         per, gbs = bench_gemv(hip, 1, steps_g, args.warmup, 1, rng)
         secondary["gemv_m1_cache_warm"] = {"us_per_step": round(per * 1e3, 3), "GB/s": round(gbs, 1), "steps": steps_g,
                                            "note": "one weight copy, L2/MALL may serve it; not HBM-honest"}
@@ -641,6 +733,14 @@ def main():
             if pf is not None and "prefill_int8_rmsnorm" in secondary:
                 secondary["prefill_int8_rmsnorm"]["cpu_reference"] = pf
                 log(f"cpu prefill (extrapolated): {pf['seconds_extrapolated']} s")
+            c1 = cpu_c1(np.random.default_rng(10))
+            if c1 is not None and "c1_dequant_matmul" in secondary:
+                secondary["c1_dequant_matmul"]["cpu_reference"] = c1
+                log(f"cpu c1: {c1['seconds_per_call'] * 1e3:.1f} ms/call")
+            mlp = cpu_mlp(np.random.default_rng(12))
+            if mlp is not None and "mlp_fp32" in secondary:
+                secondary["mlp_fp32"]["cpu_reference"] = mlp
+                log(f"cpu mlp: {mlp['seconds_per_step']} s/step")
             ll = cpu_llama_sample(np.random.default_rng(9))
             if ll is not None and "llama_decode" in secondary:
                 secondary["llama_decode"]["cpu_reference"] = ll

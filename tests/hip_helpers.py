@@ -36,6 +36,19 @@ def assert_gamma_bound(got, a, w, extra_rel=0.0):
     return float(err.max()), float(np.max(err / bound))
 
 
+def assert_plugin_tolerance(got, a, w, rtol=1e-5, atol=1e-5):
+    """allclose(got, A@W, rtol, atol) against the float64 product: the plugin tests' tolerance
+    (AccelEP tests/test_ep.py:98-100) for fp32 products with K <= 1024. Returns the worst
+    |got - A@W| / (atol + rtol |A@W|)."""
+    exact = np.asarray(a, np.float64) @ np.asarray(w, np.float64)
+    got = np.asarray(got, np.float64)
+    ratio = np.abs(got - exact) / (atol + rtol * np.abs(exact))
+    bad = ratio > 1
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements beyond rtol={rtol}, atol={atol} of the float64 "
+                           f"product; worst ratio {float(ratio.max()):.3g} at {np.unravel_index(np.argmax(ratio), ratio.shape)}")
+    return float(ratio.max())
+
+
 def same_bits(got, want):
     got = np.asarray(got, np.float32)
     want = np.asarray(want, np.float32)
@@ -125,5 +138,6 @@ def dequant_host(spec, rows, cols):
     return w.reshape(rows, cols)
 
 
-__all__ = ["Buffer", "Epilogue", "HipError", "QuantPlane", "DeviceArray", "assert_gamma_bound", "check", "dev",
+__all__ = ["Buffer", "Epilogue", "HipError", "QuantPlane", "DeviceArray", "assert_gamma_bound", "assert_plugin_tolerance",
+           "check", "dev",
            "dequant_host", "gamma", "lib", "matmul_quantized", "plane_from_spec", "quant_plane", "same_bits", "stats"]

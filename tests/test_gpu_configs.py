@@ -5,8 +5,9 @@ CPU oracle (the C restatement of AccelEP's SimDevice, oracle/oracle.c).
   MatMul with fp32 X[4,576]; W uniform int8 in [-127,127], scales uniform [1e-3,1e-2],
   X ~ N(0,1). accel::MatMulQuantized (src/sim_device.cc:541-602) with the zero point given
   both as an explicit all-zero int8 tensor and as none, K = 576. Exact-products mode: the
-  reference's bits. Default mode: 2 gamma_K (|X| @ |W|) of the float64 product, with the share
-  within the plugin tolerance rtol = atol = 1e-5 (tests/test_ep.py:98-100) printed.
+  reference's bits. Default mode: within the plugin tolerance rtol = atol = 1e-5
+  (tests/test_ep.py:98-100) of the float64 product X @ fl(q * s), and within 2 gamma_K
+  (|X| @ |W|) of it.
 * C2: the fp32 MLP of bench.py, X[256,1024] -> Gemm(1024x4096)+bias -> exact Gelu ->
   Gemm(4096x1024)+bias + residual X, weights and biases ~ N(0,0.02), X ~ N(0,1), as the two
   fused calls the bench times. Oracle: ReferenceMatMul (src/sim_device.cc:387-402), then
@@ -15,9 +16,11 @@ CPU oracle (the C restatement of AccelEP's SimDevice, oracle/oracle.c).
   (K = 4096, split K with the split-reduce kernel): every element within 2 gamma_K (|H| @ |W2|)
   of the float64 product plus one rounding of each epilogue add, with H the GPU's own Gemm1
   output (so Gemm2's error is measured alone); the 1e-5 pass rate is printed beside it.
+  Gemm1 is also within 1e-5 of the float64 product with a float64 bias and Gelu.
 """
 
 import ctypes as C
+import math
 
 import numpy as np
 import pytest
@@ -50,12 +53,14 @@ def products(request):
 @pytest.mark.parametrize("zero", ["none", "explicit"])
 def test_c1_dequantize_matmul(zero, products):
     """In the exact-products mode the GPU stores the reference's bits. In the default mode it
-    adds in another order: every element within 2 gamma_K (|X| @ |W|) of the float64 product,
-    and the share within rtol = atol = 1e-5 of the reference printed. At this workload's
-    magnitudes (|C| up to 65, partial sums of tens) the reference's own k-ordered fp32 sum is
-    up to 4e-5 from the exact product, so 1e-5 of its bits is not a bound any other summation
-    order can promise element by element."""
-    from hip_helpers import assert_gamma_bound, same_bits
+    adds in another order, and every element is within rtol = atol = 1e-5 of the float64
+    product X @ fl(q * s) (the comparison the reference's plugin test makes against numpy,
+    tests/test_ep.py:98-100) and within 2 gamma_K (|X| @ |W|) of it. The reference's own
+    k-ordered fp32 sum is the less accurate one here: at this workload's magnitudes (|C| up to
+    65, partial sums of tens) its bits are up to 4e-5 from the float64 product, one element
+    beyond the 1e-5 tolerance, so the default path is checked against the float64 product
+    rather than against those bits."""
+    from hip_helpers import assert_gamma_bound, assert_plugin_tolerance, same_bits
     from oracle_ctypes import make_plane
 
     r = np.random.default_rng(2025)
@@ -75,10 +80,13 @@ def test_c1_dequantize_matmul(zero, products):
     want = oracle().matmul_quantized(x, None, None, oplane, m, k, n)
     w = (q.reshape(k, n).astype(np.float32) * s[None, :]).astype(np.float32)
     rate = float(np.isclose(got, want, rtol=1e-5, atol=1e-5).mean())
-    print(f"  max|gpu - oracle| = {float(np.abs(got - want).max()):.3g}, within 1e-5: {rate:.6f}", flush=True)
+    print(f"  max|gpu - oracle| = {float(np.abs(got - want).max()):.3g}, within 1e-5 of the oracle: {rate:.6f}",
+          flush=True)
     if products == "exact":
         same_bits(got, want)
     else:
+        worst = assert_plugin_tolerance(got, x, w)
+        print(f"  worst |gpu - X@W| / (1e-5 + 1e-5 |X@W|) = {worst:.3f}", flush=True)
         assert_gamma_bound(got, x, w)
         assert_gamma_bound(want, x, w)  # the reference's own result meets the same bound
 
@@ -112,6 +120,10 @@ def test_c2_fused_mlp():
     err1 = float(np.abs(h_gpu - h_ref).max())
     print(f"  Gemm1 (K=1024) max|gpu - oracle| = {err1:.3g}", flush=True)
     np.testing.assert_allclose(h_gpu, h_ref, rtol=1e-5, atol=1e-5)
+    # and against the float64 product with the float64 epilogue (exact Gelu through math.erf)
+    pre = x.astype(np.float64) @ w1.astype(np.float64) + b1.astype(np.float64)[None, :]
+    h64 = 0.5 * pre * (1.0 + np.vectorize(math.erf)(pre / math.sqrt(2.0)))
+    np.testing.assert_allclose(h_gpu, h64, rtol=1e-5, atol=1e-5)
 
     # Gemm2 on the GPU's H: oracle composition and the gamma_K bound.
     acc = o.reference_matmul(h_gpu, w2)
