@@ -7,6 +7,32 @@
 
 namespace accel_hip {
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats to one word of two bf16 (round to nearest even), x in the low half.
+__device__ __forceinline__ uint32_t PackBf16(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
+}
+// The low / high bf16 of a word as the fp32 value it holds exactly.
+__device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// x = hi + mid + lo for two floats at once, each part a bf16 (round to nearest even):
+// hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid). Both differences are exact in fp32,
+// and after two roundings to 8 significant bits at most 8 bits of x remain, so lo holds them
+// exactly and the three parts carry all 24 significand bits (for finite |x| >= 2^-110 and below
+// the bf16 overflow threshold 0x1.fep127), with |mid| about 2^-8 |x| at most and |lo| about
+// 2^-16 |x| at most.
+__device__ __forceinline__ void SplitBf16Pair(float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = PackBf16(x0, x1);
+  const float r0 = x0 - Bf16Low(hi);
+  const float r1 = x1 - Bf16High(hi);
+  mid = PackBf16(r0, r1);
+  lo = PackBf16(r0 - Bf16Low(mid), r1 - Bf16High(mid));
+}
+
 // Bias index of element (i, j) for a bias of rank 0..2 right-aligned against [m, n];
 // a dimension of size 1 broadcasts (BiasOffset, src/sim_device.cc:104-124).
 __device__ __forceinline__ int64_t BiasIndex(const Epilogue& e, int64_t i, int64_t j) {

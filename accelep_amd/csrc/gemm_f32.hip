@@ -22,6 +22,7 @@ namespace accel_hip {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kBK = 16;
@@ -384,32 +385,27 @@ void Launch(const GemmArgs& args, bool q8, dim3 grid, hipStream_t stream) {
 //
 // A product whose 64 x 64 tiles barely cover the CUs (the MLP's 256 x 1024 x 4096 and
 // 256 x 4096 x 1024) gives each SIMD one wave. In the LDS kernel above that wave runs one or
-// two dependent MFMA chains and meets a barrier every 16 k. Here each of the 4 waves takes the
-// whole 64 x 64 tile over a quarter of the workgroup's K range, as 4 x 4 independent
-// v_mfma_f32_16x16x4f32 chains, with no LDS and no barrier until the end:
-//  * the 16 k of one group are assigned to MFMA steps so that every load is a float4: lane
-//    group q = lane / 16 of row tile i loads A[16i + lane % 16][kb + 4q .. 4q + 3], whose
-//    element s is its A operand in step s (k = kb + 4q + s); in step s the lane loads
-//    B[kb + 4q + s][4(lane % 16) .. + 3], whose element j is its B operand for column tile j,
-//    so MFMA column c of tile j is the tile's column 4c + j. The product sums every k of the
-//    group once, in another order; 8 loads feed 64 MFMAs;
-//  * operands of the next three groups are in flight while one group's 64 MFMAs run;
-//  * the four wave partials meet in LDS and are added in wave order; a K split across
-//    workgroups (for grids with fewer tiles than CUs) goes through the workspace and
-//    SplitReduceKernel, as above. (Combining the splits in the last workgroup to arrive, with
-//    agent-scope stores and loads of the partial tiles, measured slower on the MLP's
-//    256 x 4096 x 1024: 73 against 55 us per MLP step; 60.6 against 55.3 with every partial
-//    load of a chunk of four splits requested at once.)
-// Full tiles only: m and n multiples of 64, K per wave a multiple of 4 groups of 16, A and B
-// 16-byte aligned.
-
-typedef float v4f __attribute__((ext_vector_type(4)));
+// two dependent MFMA chains and meets a barrier every 16 k. Here each of the 4 waves of a
+// workgroup takes the whole 64 x 64 tile over a quarter of the workgroup's K range, with no LDS
+// and no barrier until the end; the four wave partials meet in LDS and are added in wave order,
+// and a K split across workgroups (for grids with fewer tiles than CUs) goes through the
+// workspace and SplitReduceKernel, as above. Full tiles only: m and n multiples of 64, K per
+// wave a multiple of 64, A and B 16-byte aligned.
+//
+// Measured history on the MLP (X[256,1024] -> 4096 -> 1024, per step): the LDS kernel 64-66 us;
+// the same split of K on v_mfma_f32_16x16x4f32 (4 x 4 fp32 MFMA chains per wave, a pure MFMA
+// stream of 2 x 16.6 us) 54-56 us; the bf16 part products below 45.7-47 us. Summing the K splits
+// in the last workgroup of a tile to arrive (agent-scope stores, an arrival count, agent-scope
+// loads of the other partials) measured slower than SplitReduceKernel in both forms: on the
+// fp32 form 60.6 against 55.3 us per MLP step, on the bf16 form 48-49.6 against 46.5-47.1 us
+// (A/B/A/B on one box, graph replay). The same sum behind an acquire-release count (plain stores
+// and loads) is slower still (lab: 29.7 against 21.8 us per launch): the acquire invalidates the
+// XCD's L2 under the workgroups still streaming their operands.
 
 constexpr int kWsTile = 64;
-constexpr int kWsGroupK = 16;
-constexpr int kWsStages = 4;  // groups in flight (32 loads, below the 63 the load counter tracks)
 constexpr int kWsPad = kWsTile + 1;  // LDS row stride of the partial tiles (no bank conflicts)
 constexpr int kWsRowsPerThread = kWsTile * kWsTile / kThreads;  // output elements each thread stores
+constexpr int kWsUnitK = 256;  // K of a workgroup: whole multiples of 4 waves x 64
 static_assert(kThreads % kWsTile == 0 && kThreads / kWsTile == 4, "store loop: 4 tile rows per pass");
 
 struct WsArgs {
@@ -417,34 +413,143 @@ struct WsArgs {
   const float* b;
   float* c;
   int64_t m, k, n;
-  int64_t k_per_wg;    // K range of one workgroup (a multiple of 4 * kWsGroupK)
+  int64_t k_per_wg;    // K range of one workgroup (a multiple of kWsUnitK)
   float* partials;     // [splits][m][n] when K is split across workgroups, else nullptr
   Epilogue epi;
 };
 
-struct WsOperands {
-  float4 a[4];  // row tiles 0..3: 4 consecutive k of this lane's row
-  float4 b[4];  // steps 0..3: 4 consecutive columns (one per column tile) of this lane's k row
+// ---- the same small grids on the bf16 matrix cores: six exact part products per product ----
+//
+// Each fp32 operand x is split as hi + mid + lo (SplitBf16Pair: exact, |mid| about 2^-8 |x| at
+// most, |lo| about 2^-16 |x| at most), and a product a*b is formed from six part products,
+// hi*hi', hi*mid', mid*hi', mid*mid', hi*lo' and lo*hi', on v_mfma_f32_32x32x16_bf16. Each part
+// product is exact in fp32 (8 x 8 significand bits), so only the accumulation rounds. The three
+// left out, mid*lo' + lo*mid' + lo*lo', are below about 2^-23 |a b| together: less than two fp32
+// roundings of the product, which the reference's k-ordered loop rounds once. The hi*hi'
+// products accumulate apart from the five cross terms (together below about 2^-7 |a b|): the
+// large sum takes one rounding per MFMA step, as one fp32 accumulation would, and the cross
+// sum's roundings are 2^-7 as large; the two are added once at the end. Every output therefore
+// stays within Higham's 2 gamma_K bound of the exact product even if an MFMA added its products
+// one by one in fp32, for finite operands whose parts stay normal (|x| >= 2^-110) and below the
+// bf16 overflow threshold. (Measured on single MFMAs, one adds its 16 products and the
+// accumulator with about one fp32 rounding at the magnitude of the largest of them: 2^24 +
+// fourteen 1s - 2^24 gives 15, not the 0 of a sequential fp32 sum. One accumulator for all six
+// measured 0.3 us faster per MLP step, A/B on one box; not taken.)
+//
+// The bf16 matrix cores run 16 times the fp32 MFMA rate, so six passes are 2.7 times the
+// throughput of one fp32 pass. The grid and K split are the wave-split kernel's: a 64 x 64 tile
+// per workgroup, each of its 4 waves over a quarter of the workgroup's K, 2 x 2 MFMA tiles of
+// 32 x 32 per wave, K split across workgroups through SplitReduceKernel when the tiles leave CUs
+// idle. Operands load in groups of 32 k, two groups in flight; lane l (r = l % 32, h = l / 32)
+// loads per group:
+//  * A: row 32i + r of row tile i, k 16h .. 16h + 15, four float4 loads, so the two lanes of a
+//    row read its whole 128-byte line within one group (reading 16 k per group, half a line,
+//    measured about 1.5 us slower per launch on the MLP's products);
+//  * B: k rows 16h + 8s + t (MFMA step s < 2, t < 8), columns 2r and 2r + 1, one float2 load each:
+//    element j is the lane's B operand of column tile j, whose MFMA column c is the tile's
+//    column 2c + j.
+// MFMA step s of a group covers k 16h + 8s .. + 7 of lane (r, h), for A and B alike. The split of
+// the next step (VALU) is interleaved with the MFMAs of the current one.
+
+struct SbOperands {
+  float4 a[2][4];  // row tile i: k 16h .. 16h + 15 of the lane's row
+  float2 b[2][8];  // step s, row 16h + 8s + t: the lane's columns of column tiles 0 and 1
 };
 
-__device__ __forceinline__ void LoadWsGroup(const WsArgs& p, int64_t m0, int64_t n0, int64_t kb, int lane,
-                                            WsOperands& r) {
-  const int q = lane >> 4, l16 = lane & 15;
+struct SbParts {
+  u32x4 a[2][3];  // row tile i, part hi / mid / lo: 8 bf16, k ascending
+  u32x4 b[2][3];  // column tile j, part hi / mid / lo
+};
+
+__device__ __forceinline__ void LoadSbGroup(const WsArgs& p, int64_t m0, int64_t n0, int64_t kb, int lane,
+                                            SbOperands& r) {
+  const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r.a[i] = *reinterpret_cast<const float4*>(p.a + (m0 + 16 * i + l16) * p.k + kb + 4 * q);
+  for (int i = 0; i < 2; ++i) {
+    const float* src = p.a + (m0 + 32 * i + l32) * p.k + kb + 16 * h;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) r.b[s] = *reinterpret_cast<const float4*>(p.b + (kb + 4 * q + s) * p.n + n0 + 4 * l16);
+    for (int q = 0; q < 4; ++q) r.a[i][q] = *reinterpret_cast<const float4*>(src + 4 * q);
+  }
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      r.b[s][t] = *reinterpret_cast<const float2*>(p.b + (kb + 16 * h + 8 * s + t) * p.n + n0 + 2 * l32);
 }
 
-__device__ __forceinline__ float Lane4(const float4& v, int s) {
-  return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w;
+// Eight floats (k ascending) to the three part operands of one MFMA tile.
+__device__ __forceinline__ void SplitOperand(const float (&x)[8], u32x4 (&part)[3]) {
+  uint32_t w[3][4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) SplitBf16Pair(x[2 * v], x[2 * v + 1], w[0][v], w[1][v], w[2][v]);
+#pragma unroll
+  for (int q = 0; q < 3; ++q) part[q] = u32x4{w[q][0], w[q][1], w[q][2], w[q][3]};
 }
 
-// kGroups > 0: the K range of a wave is exactly kGroups groups (a trip count the compiler
-// knows). kGroups == 0: any multiple of kWsStages groups.
+// The part operands of MFMA step s of a loaded group.
+__device__ __forceinline__ void SplitSbStep(const SbOperands& r, int s, SbParts& q) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 u = r.a[i][2 * s], v = r.a[i][2 * s + 1];
+    const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+    SplitOperand(x, q.a[i]);
+  }
+  const float b0[8] = {r.b[s][0].x, r.b[s][1].x, r.b[s][2].x, r.b[s][3].x,
+                       r.b[s][4].x, r.b[s][5].x, r.b[s][6].x, r.b[s][7].x};
+  const float b1[8] = {r.b[s][0].y, r.b[s][1].y, r.b[s][2].y, r.b[s][3].y,
+                       r.b[s][4].y, r.b[s][5].y, r.b[s][6].y, r.b[s][7].y};
+  SplitOperand(b0, q.b[0]);
+  SplitOperand(b1, q.b[1]);
+}
+
+__device__ __forceinline__ v16f Mfma16(const u32x4& a, const u32x4& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+// The 24 MFMAs of one step, pass-major so that consecutive MFMAs feed different accumulators;
+// one MFMA, seven VALU instructions of the next step's split and one load of a group alternate
+// (pairs of MFMAs with 14 VALU measured 0.8 us slower per MLP step, quadruples 1.3 us).
+__device__ __forceinline__ void SbStepMfmas(const SbParts& cur, v16f (&hh)[2][2], v16f (&cross)[2][2]) {
+  // cross terms: lo*hi', hi*lo', mid*mid', mid*hi', hi*mid' (part 0 hi, 1 mid, 2 lo)
+  constexpr int kPa[5] = {2, 0, 1, 1, 0};
+  constexpr int kPb[5] = {0, 2, 1, 0, 1};
+#pragma unroll
+  for (int q = 0; q < 5; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) cross[i][j] = Mfma16(cur.a[i][kPa[q]], cur.b[j][kPb[q]], cross[i][j]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) hh[i][j] = Mfma16(cur.a[i][0], cur.b[j][0], hh[i][j]);
+#pragma unroll
+  for (int u = 0; u < 24; ++u) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// The epilogue steps of ApplyEpilogueLoaded for one known form, over a thread's 16 outputs
+// (rows 4u apart): the same operations in the same order, so the same bits.
+template <int kAct, bool kBias, bool kRes>
+__device__ __forceinline__ void StoreRows(const float (&v)[kWsRowsPerThread], const Epilogue& e, float bias_v,
+                                          const float (&res_v)[kWsRowsPerThread], float* out, int64_t n) {
+  Epilogue f = e;
+  f.activation = kAct;
+  f.bias = kBias ? e.bias : nullptr;
+  f.residual = kRes ? e.residual : nullptr;
+#pragma unroll
+  for (int u = 0; u < kWsRowsPerThread; ++u) out[4 * u * n] = ApplyEpilogueLoaded(v[u], f, bias_v, res_v[u]);
+}
+
+// kGroups > 0: the K range of a wave is exactly kGroups groups of 32. kGroups == 0: any even
+// number of groups.
 template <int kGroups>
-__global__ __launch_bounds__(kThreads) void GemmF32WaveSplitKernel(WsArgs p) {
+__global__ __launch_bounds__(kThreads) void GemmF32SplitBf16Kernel(WsArgs p) {
   __shared__ float red[4][kWsTile][kWsPad];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -455,13 +560,18 @@ __global__ __launch_bounds__(kThreads) void GemmF32WaveSplitKernel(WsArgs p) {
   const int64_t n0 = (tile % tiles_n) * kWsTile;
   const int64_t k_wave = p.k_per_wg / 4;
   const int64_t kbeg = static_cast<int64_t>(blockIdx.y) * p.k_per_wg + wave * k_wave;
-  const int groups = kGroups > 0 ? kGroups : static_cast<int>(k_wave / kWsGroupK);
+  const int groups = kGroups > 0 ? kGroups : static_cast<int>(k_wave / 32);
 
-  v4f acc[4][4];
+  v16f hh[2][2], cross[2][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        hh[i][j][r] = 0.f;
+        cross[i][j][r] = 0.f;
+      }
 
   // The store loop at the end gives thread tid column tid % 64 of tile rows 4u + tid / 64
   // (u < kWsRowsPerThread). Their bias and residual values are loaded here, so the loads
@@ -477,52 +587,71 @@ __global__ __launch_bounds__(kThreads) void GemmF32WaveSplitKernel(WsArgs p) {
   for (int u = 0; u < kWsRowsPerThread; ++u)
     res_v[u] = final_out && p.epi.residual != nullptr ? p.epi.residual[(m0 + 4 * u + erow) * p.n + n0 + ecol] : 0.f;
 
-  WsOperands ops[kWsStages];
+  // Group g sits in ops[g % 2]. Per group: split step 1 while step 0 multiplies, then split the
+  // next group's step 0 and request group g + 2 into the freed set while step 1 multiplies
+  // (requests past the end repeat the last group; never used).
+  SbOperands ops[2];
+  SbParts parts[2];
+  LoadSbGroup(p, m0, n0, kbeg, lane, ops[0]);
+  LoadSbGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(1, groups - 1)) * 32, lane, ops[1]);
+  SplitSbStep(ops[0], 0, parts[0]);
+#pragma unroll (kGroups > 0 ? kGroups / 2 : 1)
+  for (int g = 0; g < groups; g += 2) {
 #pragma unroll
-  for (int st = 0; st < kWsStages; ++st)
-    LoadWsGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(st, groups - 1)) * kWsGroupK, lane, ops[st]);
-  // groups is a multiple of kWsStages: the loop body is whole stage rings, so the loop head
-  // sees one pattern of loads in flight and waits only for the group it needs. With kGroups
-  // known the body is two rings (8 groups, 512 MFMAs): measured slightly faster than the
-  // whole range unrolled straight (Gemm1 of the MLP, 21.4 against 22.1 us per launch).
-#pragma unroll (kGroups > 0 ? 2 : 1)
-  for (int base = 0; base < groups; base += kWsStages) {
-#pragma unroll
-    for (int st = 0; st < kWsStages; ++st) {
-      const int g = base + st;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(Lane4(ops[st].a[i], s), Lane4(ops[st].b[s], j), acc[i][j], 0,
-                                                             0, 0);
-      // The group kWsStages ahead (repeating the last one past the end; never used), issued here:
-      // the barrier keeps the scheduler from sinking the loads to their use.
-      LoadWsGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(g + kWsStages, groups - 1)) * kWsGroupK, lane, ops[st]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int st = 0; st < 2; ++st) {
+      SplitSbStep(ops[st], 1, parts[1]);
+      SbStepMfmas(parts[0], hh, cross);
+      SplitSbStep(ops[st ^ 1], 0, parts[0]);
+      LoadSbGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(g + st + 2, groups - 1)) * 32, lane, ops[st]);
+      SbStepMfmas(parts[1], hh, cross);
     }
   }
-  // Element r of tile (i, j): row 16i + 4 * (lane / 16) + r, column 4 * (lane % 16) + j.
+  // Element r of MFMA tile (i, j): row 32i + 8(r / 4) + 4(lane / 32) + r % 4, column
+  // 2(lane % 32) + j.
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][16 * i + 4 * (lane >> 4) + r][4 * (lane & 15) + j] = acc[i][j][r];
+      for (int r = 0; r < 16; ++r)
+        red[wave][32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)][2 * (lane & 31) + j] = hh[i][j][r] + cross[i][j][r];
   __syncthreads();
+  float v[kWsRowsPerThread];
 #pragma unroll
   for (int u = 0; u < kWsRowsPerThread; ++u) {
-    const int row = 4 * u + erow, col = ecol;
-    const float v = red[0][row][col] + red[1][row][col] + red[2][row][col] + red[3][row][col];
-    const int64_t gr = m0 + row, gc = n0 + col;
-    if (!final_out) {
-      p.partials[(static_cast<int64_t>(blockIdx.y) * p.m + gr) * p.n + gc] = v;
-    } else {
-      const float b = bias_by_row && p.epi.bias != nullptr ? p.epi.bias[BiasIndex(p.epi, gr, gc)] : bias_v;
-      StoreC(p.c, gr, gc, p.n, p.epi, ApplyEpilogueLoaded(v, p.epi, b, res_v[u]));
+    const int row = 4 * u + erow;
+    v[u] = red[0][row][ecol] + red[1][row][ecol] + red[2][row][ecol] + red[3][row][ecol];
+  }
+  if (p.partials != nullptr) {  // SplitReduceKernel adds the splits in order and applies the epilogue
+#pragma unroll
+    for (int u = 0; u < kWsRowsPerThread; ++u)
+      p.partials[(static_cast<int64_t>(blockIdx.y) * p.m + m0 + 4 * u + erow) * p.n + n0 + ecol] = v[u];
+    return;
+  }
+  if (p.epi.split[0] == 0 && !bias_by_row) {
+    // One [m, n] output and a bias per column (or none): one straight run per form of the
+    // epilogue over the thread's 16 values, so their erf and stores overlap instead of
+    // following the epilogue's branches one value at a time.
+    float* out = p.c + (m0 + erow) * p.n + n0 + ecol;
+    const int form = (p.epi.activation == ACCEL_HIP_ACT_GELU ? 8 : p.epi.activation == ACCEL_HIP_ACT_RELU ? 4 : 0) |
+                     (p.epi.bias != nullptr ? 2 : 0) | (p.epi.residual != nullptr ? 1 : 0);
+    switch (form) {
+#define ACCEL_WS_FORM(F)                                                                             \
+  case F:                                                                                            \
+    StoreRows<(F & 12) == 8 ? ACCEL_HIP_ACT_GELU : (F & 12) == 4 ? ACCEL_HIP_ACT_RELU : ACCEL_HIP_ACT_NONE, \
+              (F & 2) != 0, (F & 1) != 0>(v, p.epi, bias_v, res_v, out, p.n);                           \
+    break;
+      ACCEL_WS_FORM(0) ACCEL_WS_FORM(1) ACCEL_WS_FORM(2) ACCEL_WS_FORM(3) ACCEL_WS_FORM(4) ACCEL_WS_FORM(5)
+      ACCEL_WS_FORM(6) ACCEL_WS_FORM(7) ACCEL_WS_FORM(8) ACCEL_WS_FORM(9) ACCEL_WS_FORM(10) ACCEL_WS_FORM(11)
+#undef ACCEL_WS_FORM
     }
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < kWsRowsPerThread; ++u) {
+    const int64_t gr = m0 + 4 * u + erow, gc = n0 + ecol;
+    const float b = bias_by_row && p.epi.bias != nullptr ? p.epi.bias[BiasIndex(p.epi, gr, gc)] : bias_v;
+    StoreC(p.c, gr, gc, p.n, p.epi, ApplyEpilogueLoaded(v[u], p.epi, b, res_v[u]));
   }
 }
 
@@ -541,10 +670,10 @@ bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
   auto tiles_for = [&](int tm, int tn) { return ((m + tm - 1) / tm) * ((n + tn - 1) / tn); };
   if (!q8 && tiles_for(128, 128) < 2 * cus && m % kWsTile == 0 && n % kWsTile == 0 &&
       reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 && m / kWsTile <= 65535) {
-    // Small fp32 grid: waves split K (GemmF32WaveSplitKernel); K split across workgroups too
+    // Small fp32 grid: waves split K (GemmF32SplitBf16Kernel); K split across workgroups too
     // when the tiles leave CUs idle, into ranges of whole 4-wave groups.
     const int64_t wtiles = (m / kWsTile) * (n / kWsTile);
-    const int64_t unit = 4 * kWsGroupK * kWsStages;  // per workgroup: 4 waves x whole stage rings
+    const int64_t unit = kWsUnitK;  // per workgroup: 4 waves x whole pairs of 32-k groups
     int64_t wsplits = wtiles < cus ? std::max<int64_t>(1, std::min<int64_t>((cus + wtiles - 1) / wtiles, k / (4 * unit)))
                                    : 1;
     while (wsplits > 1 && k % (wsplits * unit) != 0) --wsplits;
@@ -561,9 +690,9 @@ bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
                                 : nullptr;
       ws.epi = epi;
       const dim3 grid(static_cast<uint32_t>(wtiles), static_cast<uint32_t>(wsplits));
-      if (ws.k_per_wg / 4 == 16 * kWsGroupK) hipLaunchKernelGGL(GemmF32WaveSplitKernel<16>, grid, dim3(kThreads), 0, stream, ws);
-      else hipLaunchKernelGGL(GemmF32WaveSplitKernel<0>, grid, dim3(kThreads), 0, stream, ws);
-      Check(hipGetLastError(), "GemmF32WaveSplitKernel launch");
+      if (ws.k_per_wg / 4 == 256) hipLaunchKernelGGL(GemmF32SplitBf16Kernel<8>, grid, dim3(kThreads), 0, stream, ws);
+      else hipLaunchKernelGGL(GemmF32SplitBf16Kernel<0>, grid, dim3(kThreads), 0, stream, ws);
+      Check(hipGetLastError(), "GemmF32SplitBf16Kernel launch");
       if (wsplits > 1)
         LaunchSplitReduce(ws.partials, static_cast<int32_t>(wsplits), m, n, c, kScalePerRow, nullptr, 0, epi, stream);
       return false;

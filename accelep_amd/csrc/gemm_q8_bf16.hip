@@ -37,9 +37,6 @@
 namespace accel_hip {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -76,13 +73,6 @@ struct Q8GemmArgs {
   float* partials;      // [splits][m][n] raw sums when the K range is split, else nullptr
   Epilogue epi;
 };
-
-// Two floats to one word of two bf16 (round to nearest even).
-__device__ __forceinline__ uint32_t PackBf16(float x, float y) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
-}
-__device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
-__device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
 // The global part of one chunk, as loaded: A rows (tid / 8) + 32i, k quad tid % 8; W rows
 // 2 * kp and 2 * kp + 1 of column octet oct, kp = tid / octets < 16 (for BM = 64 the upper

@@ -758,23 +758,12 @@ __global__ __launch_bounds__(kWideThreads) void GemvWideKernel(GemvArgs p) {
 // slots agree. The waves take interleaved blocks, and their sums are added
 // through LDS in wave order. With splits, each workgroup stores its partial sums and the last
 // one of a group to arrive adds them in split order and applies the scale and the epilogue.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
 constexpr int kSplitWaves = 4;
 constexpr int kSplitThreads = kSplitWaves * 64;
 constexpr int kSplitTiles = static_cast<int>(kGemvGroupTiles);      // tiles of a group (128 columns)
 constexpr int kSplitBlockRows = static_cast<int>(kGemvGroupRows);  // K of one MFMA
 constexpr int kSplitBatch = 2;  // blocks a wave loads before using any
 constexpr int kSplitGroupBytes = kSplitTiles * kNarrowTile;  // bytes of one row of a group
-
-// Two floats to one word of two bf16 (round to nearest even; exact for the values used here).
-__device__ __forceinline__ uint32_t PackBf16(float x, float y) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
-}
-__device__ __forceinline__ float Bf16Low(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
-__device__ __forceinline__ float Bf16High(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
 // kPlain: the epilogue is the identity and C one [m, n] matrix, so each sum is stored as
 // sum * scale with no epilogue code (which costs about 1 us of the m = 16 kernel's tail).

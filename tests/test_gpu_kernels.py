@@ -156,13 +156,14 @@ def test_matmul_probes_and_zero_k():
                                    (128, 4096, 256), (64, 512, 64), (64, 2048, 192), (128, 1536, 128), (64, 1088, 704),
                                    (1024, 2048, 1024)])
 def test_matmul_against_oracle(m, k, n):
-    """fp32 GEMM. The 64 x 64 wave-split kernel (4 waves, each over a quarter of the
-    workgroup's K) takes small full-tile grids: 16 groups per wave unrolled (256 x 1024 x 4096;
-    and, with K also split over workgroups and summed by SplitReduceKernel, 256 x 4096 x 1024
-    and 128 x 4096 x 256 in 4 splits, 64 x 2048 x 192 in 2), and the looped form
-    (64 x 512 x 64: 8 groups; 128 x 1536 x 128: 24; 1024 x 2048 x 1024: 32). The LDS kernel
-    takes the rest (ragged shapes, K not a multiple of 256). Every element within 2 gamma_K of
-    the float64 product."""
+    """fp32 GEMM. The 64 x 64 wave-split kernel on the bf16 matrix cores (each fp32 operand as
+    three exact bf16 parts, six part products; 4 waves, each over a quarter of the workgroup's K)
+    takes small full-tile grids: 8 groups of 32 k per wave unrolled (256 x 1024 x 4096; and, with
+    K also split over workgroups and summed by SplitReduceKernel, 256 x 4096 x 1024 and
+    128 x 4096 x 256 in 4 splits, 64 x 2048 x 192 in 2), and the looped form (64 x 512 x 64: 4
+    groups; 128 x 1536 x 128: 12; 1024 x 2048 x 1024: 16). The LDS kernel on the fp32 matrix
+    cores takes the rest (ragged shapes, K not a multiple of 256). Every element within 2 gamma_K
+    of the float64 product, and within rtol = atol = 1e-5 of it for K <= 1024."""
     r = np.random.default_rng(m * 7 + k)
     a = r.standard_normal((m, k)).astype(np.float32)
     b = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
