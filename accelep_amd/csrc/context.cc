@@ -47,7 +47,7 @@ Context g_ctx;
 Error g_init_error{0, ""};
 std::mutex g_scratch_mu;
 
-constexpr int kEventSlots = 8;
+constexpr int kEventSlots = 16;
 hipEvent_t g_events[kEventSlots];
 
 // What accel_hip_capture_end hands out: the executable graph, the Generation() at the start

@@ -127,6 +127,14 @@ struct Model {
   void* decode_graph = nullptr;
   bool decode_graph_exact = false;
   bool decode_warm = false;
+  // Timing marks of the decode step (ACCEL_LLAMA_DECODE_MARKS=<layer>, read at each capture):
+  // the captured step records the event slots of accel_hip_event_record around the embedding,
+  // that layer's five kernels, all the layers, the LM head's norm and product and the advance
+  // (kMark*), and Generate records the sampler's start and end; the values left by the last
+  // step of a generate time its parts (bench.py --decode-marks). The marks are event nodes of
+  // the graph, so a marked step runs a little longer than an unmarked one. -1: no marks.
+  int32_t decode_marks = -1;
+  int32_t graph_marks = -1;  // the marks decode_graph was captured with
   // Decode-row fusions (accel_llama_set_fused_inputs): bit 0, RMSNorm and SiLU*up inside the
   // next GEMV; bit 1, RoPE + KV append + attention + combine as one kernel; bit 2 (fast mode,
   // over bit 1), the attention in fixed splits whose partials the o-projection GEMV combines.
@@ -138,6 +146,22 @@ struct Model {
   DevBuf greedy_work;    // the greedy pick's count (zero between launches) and keys
   ByteBpe bpe;           // accel_llama_tokenizer
   DevBuf text_out;       // a completion's UTF-8 text on its way back (grows to the longest)
+
+  enum MarkSlot : int32_t {
+    kMarkStart = 0, kMarkEmbedded = 1, kMarkLayer = 2, kMarkQkv = 3, kMarkAttention = 4, kMarkO = 5,
+    kMarkGateUp = 6, kMarkDown = 7, kMarkLayers = 8, kMarkHeadNorm = 9, kMarkHead = 10, kMarkAdvance = 11,
+    kMarkSampleStart = 12, kMarkSampleEnd = 13,
+    kMarkNode0 = 14, kMarkNode1 = 15  // two marks back to back: the cost of one event node
+  };
+  static int32_t MarksFromEnv() {
+    const char* v = std::getenv("ACCEL_LLAMA_DECODE_MARKS");
+    return v != nullptr && v[0] != 0 ? std::atoi(v) : -1;
+  }
+  // Records slot `slot` while the decode step is being captured with marks (`layer` -1: any).
+  void Mark(int32_t slot, int32_t layer = -1) {
+    if (decode_marks < 0 || !Capturing() || (layer >= 0 && layer != decode_marks)) return;
+    if (accel_hip_event_record(slot) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+  }
 
   void DropDecodeGraph() {
     if (decode_graph != nullptr) accel_hip_graph_destroy(decode_graph);
@@ -231,7 +255,8 @@ struct Model {
   // c = RMSNorm(x; norm) @ W: one kernel for a decode row, else the norm pass into `normed`.
   // A wide product (the LM head: 6144 workgroups) takes the separate pass too, rather than
   // every workgroup reading and normalizing the row again.
-  void ApplyNormed(const Linear& w, const float* x, const DevBuf& norm, float* c, int64_t m, const Epilogue& e) {
+  void ApplyNormed(const Linear& w, const float* x, const DevBuf& norm, float* c, int64_t m, const Epilogue& e,
+                   int32_t norm_mark = -1) {
     if (Fusable(w, m) && w.out <= kFusedNormMaxOut) {
       GemvPrologue pro;
       pro.rms_weight = norm.as<float>();
@@ -241,6 +266,7 @@ struct Model {
       return;
     }
     LaunchRmsNormRows(x, norm.as<float>(), normed.as<float>(), m, cfg.hidden, cfg.eps, stream());
+    if (norm_mark >= 0) Mark(norm_mark);
     Apply(w, normed.as<float>(), c, m, e);
   }
   // c = (SiLU(gate) * up) @ W: one kernel for a decode row, else SiLU*up in place first.
@@ -266,10 +292,14 @@ struct Model {
     const int64_t H = cfg.hidden, hd = head_dim, inter = cfg.intermediate;
     const int64_t pos = filled;
     int32_t* flag = words.as<int32_t>();
+    Mark(kMarkNode0);
+    Mark(kMarkNode1);
+    Mark(kMarkStart);
     if (check_ids) Check(hipMemsetAsync(flag, 0, sizeof(int32_t), s), "hipMemsetAsync");
     LaunchEmbedding(state != nullptr ? ids : ids + id_offset, embed_f.as<float>(), embed_q.as<int8_t>(),
                     embed_scale.as<float>(), hidden.as<float>(), seq, H, cfg.vocab, flag, s,
                     state != nullptr ? state + 1 : nullptr);
+    Mark(kMarkEmbedded);
     if (check_ids) {
       int32_t bad = 0;
       Check(hipMemcpyAsync(&bad, flag, sizeof(bad), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
@@ -292,7 +322,9 @@ struct Model {
       LayerWeights& l = layers[static_cast<size_t>(li)];
       float* kc = k_cache[static_cast<size_t>(li)].as<float>();
       float* vc = v_cache[static_cast<size_t>(li)].as<float>();
+      Mark(kMarkLayer, li);
       ApplyNormed(l.qkv, hidden.as<float>(), l.attn_norm, query.as<float>(), seq, qkv);
+      Mark(kMarkQkv, li);
       const int splits =
           seq == 1 && SplitAttention(l.o)
               ? LaunchDecodeSplitAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
@@ -301,12 +333,16 @@ struct Model {
                                            attn_work.buffer().bytes)
               : 0;
       if (splits > 0) {
+        Mark(kMarkAttention, li);
         GemvPrologue pro;
         pro.attn_partial = attn_work.as<float>();
         pro.attn_splits = splits;
         ApplyPrologue(l.o, attn_work.as<float>(), hidden.as<float>(), residual, pro);
+        Mark(kMarkO, li);
         ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
+        Mark(kMarkGateUp, li);
         ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
+        Mark(kMarkDown, li);
         continue;
       }
       if (seq != 1 || (fuse & 2) == 0 || !LaunchDecodeAttention(query.as<float>(), key.as<float>(), value.as<float>(), kc, vc,
@@ -320,12 +356,18 @@ struct Model {
                         state, cfg.context - 1, attn_work.as<float>(), attn_work.buffer().bytes,
                         !Ctx().exact_products);
       }
+      Mark(kMarkAttention, li);
       Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, residual);
+      Mark(kMarkO, li);
       ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
+      Mark(kMarkGateUp, li);
       ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
+      Mark(kMarkDown, li);
     }
+    Mark(kMarkLayers);
     ApplyNormed(lm_head, hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm, logits.as<float>(), 1,
-                Epilogue{});
+                Epilogue{}, kMarkHeadNorm);
+    Mark(kMarkHead);
   }
 
   // One decode step: forward of chosen[produced] at `position`, then both advance. The
@@ -333,7 +375,9 @@ struct Model {
   // captures it into a graph, and later calls replay the graph.
   void DecodeStep(int32_t* state) {
     const bool exact = Ctx().exact_products;
-    if (decode_graph != nullptr && (decode_graph_exact != exact || !GraphIsCurrent(decode_graph)))
+    decode_marks = MarksFromEnv();
+    if (decode_graph != nullptr &&
+        (decode_graph_exact != exact || graph_marks != decode_marks || !GraphIsCurrent(decode_graph)))
       DropDecodeGraph();
     // ACCEL_LLAMA_EAGER=1 launches every step directly (a profiler then sees each dispatch).
     static const bool eager = [] {
@@ -351,6 +395,7 @@ struct Model {
       try {
         Forward(chosen.as<int32_t>(), 1, 0, false, state);
         LaunchAdvance(state, stream());
+        Mark(kMarkAdvance);
       } catch (...) {
         void* broken = nullptr;
         accel_hip_capture_end(&broken);
@@ -359,6 +404,7 @@ struct Model {
       }
       if (accel_hip_capture_end(&decode_graph) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       decode_graph_exact = exact;
+      graph_marks = decode_marks;
     }
     if (accel_hip_graph_launch(decode_graph, 1) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
   }
@@ -386,8 +432,13 @@ struct Model {
     int32_t produced = 0;
     for (int32_t step = 0; step < max_new; ++step) {
       if (produced >= cfg.context) Fail(ACCEL_HIP_INVALID_ARGUMENT, "generation exceeded the token buffer");
+      const bool mark_sample = decode_marks >= 0 && decode_graph != nullptr;  // steps that replay the marked graph
+      if (mark_sample && accel_hip_event_record(kMarkSampleStart) != ACCEL_HIP_OK)
+        Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
                         state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
+      if (mark_sample && accel_hip_event_record(kMarkSampleEnd) != ACCEL_HIP_OK)
+        Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       produced += 1;
       if (eos_id >= 0 || on_token != nullptr) {
         // Only an eos id or a token callback needs the chosen id on the host before the next

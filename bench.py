@@ -322,40 +322,58 @@ def graph_node_floor_us(hip, nodes, reps=20):
     return ms * 1e3 / (nodes * reps)
 
 
+class SmolModel:
+    """The SmolLM2-135M-shape Llama of llama_q8_weights on the GPU (accel_llama_*) with a
+    512-id random prompt; generate(new) runs a greedy generation and returns its wall time."""
+
+    def __init__(self, hip, rng):
+        from accelep_amd.capi import F32P, I8P, LlamaConfig
+
+        self.L = L = hip.L
+        self.h = L.accel_llama_create(C.byref(LlamaConfig(**SMOL)))
+        if not self.h:
+            raise RuntimeError(L.accel_llama_last_error().decode())
+        try:
+            for kind, layer, w, sc in llama_q8_weights(SMOL, rng):
+                if sc is None:
+                    rc = L.accel_llama_weight(self.h, kind, layer, w.ctypes.data_as(F32P), w.shape[0], 1)
+                else:
+                    rc = L.accel_llama_weight_q8(self.h, kind, layer, w.ctypes.data_as(I8P), sc.ctypes.data_as(F32P),
+                                                 w.shape[0], w.shape[1])
+                if rc != 0:
+                    raise RuntimeError(L.accel_llama_last_error().decode())
+        except BaseException:
+            self.close()
+            raise
+        self.prompt = rng.integers(0, SMOL["vocab"], size=512).astype(np.int32)
+        self.out = np.zeros(129, np.int32)
+
+    def generate(self, new):
+        from accelep_amd.capi import I32P
+
+        count = C.c_int32()
+        t0 = time.perf_counter()
+        rc = self.L.accel_llama_generate(self.h, self.prompt.ctypes.data_as(I32P), self.prompt.size, new, -1, 0.0, 0,
+                                         0, self.out.ctypes.data_as(I32P), C.byref(count))
+        dt = time.perf_counter() - t0
+        if rc != 0:
+            raise RuntimeError(self.L.accel_llama_last_error().decode())
+        return dt
+
+    def close(self):
+        if self.h:
+            self.L.accel_llama_destroy(self.h)
+            self.h = None
+
+
 def bench_llama(hip, rng, reps=3):
     """SmolLM2-135M-shape Llama on the GPU (accel_llama_*): the int8 weights of
     llama_q8_weights, 512 random prompt ids, 128 greedy tokens. Prefill = generate with one
     new token; decode = the extra time of 128 more tokens. Best of `reps`."""
-    from accelep_amd.capi import F32P, I8P, I32P, LlamaConfig
-
-    L = hip.L
     cfg = SMOL
-    h = L.accel_llama_create(C.byref(LlamaConfig(**cfg)))
-    if not h:
-        raise RuntimeError(L.accel_llama_last_error().decode())
-    V = cfg["vocab"]
+    model = SmolModel(hip, rng)
+    generate = model.generate
     try:
-        for kind, layer, w, sc in llama_q8_weights(cfg, rng):
-            if sc is None:
-                rc = L.accel_llama_weight(h, kind, layer, w.ctypes.data_as(F32P), w.shape[0], 1)
-            else:
-                rc = L.accel_llama_weight_q8(h, kind, layer, w.ctypes.data_as(I8P), sc.ctypes.data_as(F32P),
-                                             w.shape[0], w.shape[1])
-            if rc != 0:
-                raise RuntimeError(L.accel_llama_last_error().decode())
-        prompt = rng.integers(0, V, size=512).astype(np.int32)
-        out = np.zeros(129, np.int32)
-        count = C.c_int32()
-
-        def generate(new):
-            t0 = time.perf_counter()
-            rc = L.accel_llama_generate(h, prompt.ctypes.data_as(I32P), prompt.size, new, -1, 0.0, 0, 0,
-                                        out.ctypes.data_as(I32P), C.byref(count))
-            dt = time.perf_counter() - t0
-            if rc != 0:
-                raise RuntimeError(L.accel_llama_last_error().decode())
-            return dt
-
         generate(129)  # warm-up: staging of the int8 weights, workspaces, the decode graph
         pre = min(generate(1) for _ in range(reps))
         full = min(generate(129) for _ in range(reps))
@@ -374,7 +392,70 @@ def bench_llama(hip, rng, reps=3):
                           "linear weights and tied embedding/LM head N(0,0.02) quantized to int8 per output row, "
                           "norms N(1,0.1), 512 random prompt ids, 128 greedy tokens, wall clock, best of 3"}
     finally:
-        L.accel_llama_destroy(h)
+        model.close()
+
+
+# Event slots the marked decode step records (the MarkSlot order of accelep_amd/csrc/llama.cc).
+MARKS = ("start", "embedded", "layer", "qkv", "attention", "o", "gate_up", "down", "layers", "head_norm", "head",
+         "advance", "sample_start", "sample_end", "node0", "node1")
+
+
+def decode_marks(hip, layers, rng, reps=3):
+    """Times the parts of one graph-replayed decode token from event nodes inside the captured
+    step (ACCEL_LLAMA_DECODE_MARKS=<layer>; the last step of a 512-id prompt and 128 tokens,
+    position 639): the sampler, the host's launch of the graph, the embedding, the given layers' five
+    kernels each, all 30 layers, the LM head's norm pass and product, and the position advance.
+    Every mark is an event node of the graph, which takes about as long as a dependent kernel:
+    each span holds the node that ends it, and two marks back to back at the start of the step
+    time one node on its own (event_node_us). The unmarked token (decode_us_per_token_unmarked)
+    is measured first. Best (smallest marked total) of `reps` generations per marked layer."""
+    slot = {name: i for i, name in enumerate(MARKS)}
+
+    def span(a, b):
+        ms = hip.L.accel_hip_event_elapsed_ms(slot[a], slot[b])
+        if ms < 0:
+            raise RuntimeError(hip.L.accel_hip_last_error().decode())
+        return ms * 1e3
+
+    model = SmolModel(hip, rng)
+    try:
+        os.environ.pop("ACCEL_LLAMA_DECODE_MARKS", None)
+        model.generate(129)
+        plain = min(model.generate(129) - model.generate(1) for _ in range(reps)) / 128 * 1e6
+        result = {"decode_us_per_token_unmarked": round(plain, 2), "layers": {}}
+        for layer in layers:
+            os.environ["ACCEL_LLAMA_DECODE_MARKS"] = str(layer)
+            model.generate(128)  # captures the marked step
+            best = None
+            for _ in range(reps):
+                model.generate(128)  # 128 tokens: the last one's sampler runs before the last graph replay
+                parts = {
+                    "sampler (GreedyKernel)": span("sample_start", "sample_end"),
+                    "graph launch (host) and start": span("sample_end", "start"),
+                    "embedding": span("start", "embedded"),
+                    "layers 0-29": span("embedded", "layers"),
+                    "LM head RMSNorm pass": span("layers", "head_norm"),
+                    "LM head GEMV 576 x 49152": span("head_norm", "head"),
+                    "advance": span("head", "advance"),
+                }
+                total = span("sample_start", "advance")
+                node = span("node0", "node1")
+                layer_parts = {
+                    "q/k/v GEMV (RMSNorm prologue)": span("layer", "qkv"),
+                    "split attention (RoPE, KV append)": span("qkv", "attention"),
+                    "o GEMV (attention combine, residual)": span("attention", "o"),
+                    "gate/up GEMV (RMSNorm prologue)": span("o", "gate_up"),
+                    "down GEMV (SiLU*up prologue, residual)": span("gate_up", "down"),
+                }
+                if best is None or total < best["token_us_marked"]:
+                    best = {"token_us_marked": round(total, 2), "event_node_us": round(node, 2),
+                            "parts_us": {k: round(v, 2) for k, v in parts.items()},
+                            "layer_us": {k: round(v, 2) for k, v in layer_parts.items()}}
+            result["layers"][str(layer)] = best
+        os.environ.pop("ACCEL_LLAMA_DECODE_MARKS", None)
+        return result
+    finally:
+        model.close()
 
 
 def calibrate_traffic(hip):
@@ -634,6 +715,9 @@ def main():
     ap.add_argument("--only-sweep", action="store_true",
                     help="run only the M = 4 and M = 16 int8 GEMVs of the decode sweep (for profiling)")
     ap.add_argument("--no-graph", action="store_true", help="launch each step directly instead of from HIP graphs")
+    ap.add_argument("--decode-marks", default=None, metavar="LAYERS",
+                    help="time the parts of a graph-replayed decode token (event nodes around the given layers' "
+                         "kernels, comma separated) and print them as one JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one residual add of known traffic (for profiler counter scaling)")
     args = ap.parse_args()
@@ -650,6 +734,10 @@ def main():
     hip = Hip()
     log(f"device {hip.arch}")
 
+    if args.decode_marks is not None:
+        layers = [int(v) for v in args.decode_marks.split(",") if v != ""]
+        print(json.dumps({"decode_marks": decode_marks(hip, layers, np.random.default_rng(11))}), flush=True)
+        return
     if args.only_llama:
         llama = bench_llama(hip, np.random.default_rng(11))
         print(json.dumps({"llama_decode": llama}), flush=True)

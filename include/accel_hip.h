@@ -225,9 +225,9 @@ ACCEL_HIP_API int accel_hip_sample_token(AccelHipBuffer logits, AccelHipBuffer c
  * back-to-back calls of fn(user); returns < 0 on failure. Used by bench.py. */
 typedef int (*AccelHipWorkFn)(void* user);
 ACCEL_HIP_API double accel_hip_time_ms(AccelHipWorkFn fn, void* user, int32_t iters);
-/* Records/reads an event pair on the library's stream (for timing regions driven from
- * Python). Recorded during a capture (accel_hip_capture_begin), the event becomes a node of
- * the graph, recorded each time the graph is replayed, and stays timeable. */
+/* Records/reads events on the library's stream (for timing regions driven from Python), in
+ * slots 0 .. 15. Recorded during a capture (accel_hip_capture_begin), the event becomes a node
+ * of the graph, recorded each time the graph is replayed, and stays timeable. */
 ACCEL_HIP_API int accel_hip_event_record(int32_t slot);
 ACCEL_HIP_API double accel_hip_event_elapsed_ms(int32_t start_slot, int32_t end_slot);
 
