@@ -756,6 +756,8 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if args.only_sweep:
+        if args.calibrate:
+            calibrate_traffic(hip)
         out = {}
         for m in (4, 16):
             per, gbs = bench_gemv(hip, m, args.steps, args.warmup, COPIES, rng)
