@@ -437,9 +437,8 @@ struct WsArgs {
 // measured 0.3 us faster per MLP step, A/B on one box; not taken.)
 //
 // The bf16 matrix cores run 16 times the fp32 MFMA rate, so six passes are 2.7 times the
-// throughput of one fp32 pass. The grid and K split are the wave-split kernel's: a 64 x 64 tile
-// per workgroup, each of its 4 waves over a quarter of the workgroup's K, 2 x 2 MFMA tiles of
-// 32 x 32 per wave, K split across workgroups through SplitReduceKernel when the tiles leave CUs
+// throughput of one fp32 pass. The grid: a 64 x 64 tile per workgroup, each of its 4 waves
+// over a quarter of the workgroup's K, 2 x 2 MFMA tiles of 32 x 32 per wave, K split across workgroups through SplitReduceKernel when the tiles leave CUs
 // idle. Operands load in groups of 32 k, two groups in flight; lane l (r = l % 32, h = l / 32)
 // loads per group:
 //  * A: row 32i + r of row tile i, k 16h .. 16h + 15, four float4 loads, so the two lanes of a
