@@ -143,7 +143,7 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
       rms.eps = epi.rms_eps;
       rms.out = epi.rms_out;
       rms_done = LaunchGemmF32(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream,
-                               epi.rms_weight != nullptr ? &rms : nullptr);
+                               epi.rms_weight != nullptr ? &rms : nullptr, stage_weights && b_f == b);
     }
   }
   if (epi.rms_weight != nullptr && !rms_done)

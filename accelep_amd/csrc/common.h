@@ -182,6 +182,20 @@ inline size_t StagedBf16Bytes(int64_t k, int64_t n) {
   return static_cast<size_t>((n + 31) / 32) * static_cast<size_t>(k / 16) * 1024;
 }
 const void* StagedBf16Image(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create = true);
+// fp32 B [k, n] (n % 64 == 0, k % 32 == 0) as bf16 parts in the B-operand order of the
+// small-grid fp32 GEMM (GemmF32SplitBf16Kernel), each value split as hi + mid + lo: for 64-column
+// tile T and 32-row group G, twelve 1 KB blocks at ((T * k/32 + G) * 12 + (2s + j) * 3 + p) * 1024
+// bytes, 16 bytes per lane l = part p (0 hi, 1 mid, 2 lo) of B[32G + 16(l / 32) + 8s + t]
+// [64T + 2(l % 32) + j], t = 0..7 (two values a word, the even t low).
+inline size_t StagedF32PartsBytes(int64_t k, int64_t n) {
+  return static_cast<size_t>(n / 64) * static_cast<size_t>(k / 32) * 12 * 1024;
+}
+// The staged parts of the fp32 matrix at b, or nullptr. With `create`, a copy is built on the
+// second use of the same [k, n] range of an allocation of this library with no write to that
+// allocation in between (a matrix that stays put across calls, i.e. a weight), never during a
+// graph capture (the product then splits B on the fly).
+const void* StagedF32Parts(const float* b, int64_t k, int64_t n, hipStream_t stream, bool create);
+void LaunchStageF32Parts(const float* b, int64_t k, int64_t n, void* dst, hipStream_t stream);
 void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream);
 // Whether the int8-weight GEMM runs this product from a staged bf16 copy (the caller stages it).
 bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v);
@@ -274,8 +288,9 @@ struct RmsRequest {
 // C[m, n] = A[m, k] @ B[k, n]; B is fp32 (b) or int8 (bq.q != nullptr). fp32 MFMA. With rms,
 // returns true when the kernel also produced the normalized rows (the caller runs the pass
 // otherwise).
+// stage_b: B may be staged as bf16 parts for the small-grid kernel (StagedF32Parts).
 bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
-                   const Epilogue& epi, hipStream_t stream, const RmsRequest* rms = nullptr);
+                   const Epilogue& epi, hipStream_t stream, const RmsRequest* rms = nullptr, bool stage_b = false);
 // The int8-weight GEMM on the bf16 matrix cores (exact products, activations split into
 // three bf16 parts): k % 32 == 0, n % 8 == 0, A 16-byte and q 8-byte aligned, per-column or
 // whole-tensor scale, no zero points (a grid of fewer 128 x 128 tiles than CUs splits K).

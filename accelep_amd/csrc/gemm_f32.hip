@@ -415,6 +415,7 @@ struct WsArgs {
   int64_t m, k, n;
   int64_t k_per_wg;    // K range of one workgroup (a multiple of kWsUnitK)
   float* partials;     // [splits][m][n] when K is split across workgroups, else nullptr
+  const u32x4* bparts;  // B as staged bf16 parts (the StagedF32Parts layout), or nullptr
   Epilogue epi;
 };
 
@@ -451,8 +452,9 @@ struct WsArgs {
 // the next step (VALU) is interleaved with the MFMAs of the current one.
 
 struct SbOperands {
-  float4 a[2][4];  // row tile i: k 16h .. 16h + 15 of the lane's row
-  float2 b[2][8];  // step s, row 16h + 8s + t: the lane's columns of column tiles 0 and 1
+  float4 a[2][4];      // row tile i: k 16h .. 16h + 15 of the lane's row
+  float2 b[2][8];      // step s, row 16h + 8s + t: the lane's columns of column tiles 0 and 1
+  u32x4 bp[2][2][3];   // staged B: step s, column tile j, part hi / mid / lo
 };
 
 struct SbParts {
@@ -460,6 +462,9 @@ struct SbParts {
   u32x4 b[2][3];  // column tile j, part hi / mid / lo
 };
 
+// kStaged: B's parts come from the staged copy, twelve 1 KB wave loads per group (one 16-byte
+// load per lane each) in place of the sixteen float2 loads and the split.
+template <bool kStaged>
 __device__ __forceinline__ void LoadSbGroup(const WsArgs& p, int64_t m0, int64_t n0, int64_t kb, int lane,
                                             SbOperands& r) {
   const int l32 = lane & 31, h = lane >> 5;
@@ -468,6 +473,16 @@ __device__ __forceinline__ void LoadSbGroup(const WsArgs& p, int64_t m0, int64_t
     const float* src = p.a + (m0 + 32 * i + l32) * p.k + kb + 16 * h;
 #pragma unroll
     for (int q = 0; q < 4; ++q) r.a[i][q] = *reinterpret_cast<const float4*>(src + 4 * q);
+  }
+  if (kStaged) {
+    const u32x4* src = p.bparts + ((n0 / kWsTile) * (p.k / 32) + kb / 32) * (12 * 64) + lane;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 3; ++q) r.bp[s][j][q] = src[((2 * s + j) * 3 + q) * 64];
+    return;
   }
 #pragma unroll
   for (int s = 0; s < 2; ++s)
@@ -486,12 +501,20 @@ __device__ __forceinline__ void SplitOperand(const float (&x)[8], u32x4 (&part)[
 }
 
 // The part operands of MFMA step s of a loaded group.
+template <bool kStaged>
 __device__ __forceinline__ void SplitSbStep(const SbOperands& r, int s, SbParts& q) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float4 u = r.a[i][2 * s], v = r.a[i][2 * s + 1];
     const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
     SplitOperand(x, q.a[i]);
+  }
+  if (kStaged) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int c = 0; c < 3; ++c) q.b[j][c] = r.bp[s][j][c];
+    return;
   }
   const float b0[8] = {r.b[s][0].x, r.b[s][1].x, r.b[s][2].x, r.b[s][3].x,
                        r.b[s][4].x, r.b[s][5].x, r.b[s][6].x, r.b[s][7].x};
@@ -546,8 +569,8 @@ __device__ __forceinline__ void StoreRows(const float (&v)[kWsRowsPerThread], co
 }
 
 // kGroups > 0: the K range of a wave is exactly kGroups groups of 32. kGroups == 0: any even
-// number of groups.
-template <int kGroups>
+// number of groups. kStaged: B's parts are read from p.bparts (the same bits the split gives).
+template <int kGroups, bool kStaged>
 __global__ __launch_bounds__(kThreads) void GemmF32SplitBf16Kernel(WsArgs p) {
   __shared__ float red[4][kWsTile][kWsPad];
   const int tid = threadIdx.x;
@@ -591,17 +614,17 @@ __global__ __launch_bounds__(kThreads) void GemmF32SplitBf16Kernel(WsArgs p) {
   // (requests past the end repeat the last group; never used).
   SbOperands ops[2];
   SbParts parts[2];
-  LoadSbGroup(p, m0, n0, kbeg, lane, ops[0]);
-  LoadSbGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(1, groups - 1)) * 32, lane, ops[1]);
-  SplitSbStep(ops[0], 0, parts[0]);
+  LoadSbGroup<kStaged>(p, m0, n0, kbeg, lane, ops[0]);
+  LoadSbGroup<kStaged>(p, m0, n0, kbeg + static_cast<int64_t>(min(1, groups - 1)) * 32, lane, ops[1]);
+  SplitSbStep<kStaged>(ops[0], 0, parts[0]);
 #pragma unroll (kGroups > 0 ? kGroups / 2 : 1)
   for (int g = 0; g < groups; g += 2) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      SplitSbStep(ops[st], 1, parts[1]);
+      SplitSbStep<kStaged>(ops[st], 1, parts[1]);
       SbStepMfmas(parts[0], hh, cross);
-      SplitSbStep(ops[st ^ 1], 0, parts[0]);
-      LoadSbGroup(p, m0, n0, kbeg + static_cast<int64_t>(min(g + st + 2, groups - 1)) * 32, lane, ops[st]);
+      SplitSbStep<kStaged>(ops[st ^ 1], 0, parts[0]);
+      LoadSbGroup<kStaged>(p, m0, n0, kbeg + static_cast<int64_t>(min(g + st + 2, groups - 1)) * 32, lane, ops[st]);
       SbStepMfmas(parts[1], hh, cross);
     }
   }
@@ -654,10 +677,42 @@ __global__ __launch_bounds__(kThreads) void GemmF32SplitBf16Kernel(WsArgs p) {
   }
 }
 
+// dst in the StagedF32Parts layout from B [k, n] (n % 64 == 0, k % 32 == 0): one thread per
+// 16-byte lane slot, split by the kernel's own SplitOperand, so the staged parts are the bits
+// the split on the fly gives.
+__global__ void StageF32PartsKernel(const float* b, int64_t k, int64_t n, u32x4* dst, int64_t slots) {
+  const int64_t groups = k / 32;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < slots;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int lane = static_cast<int>(idx & 63);
+    const int blk = static_cast<int>((idx >> 6) % 12);  // (2s + j) * 3 + part
+    const int64_t tg = (idx >> 6) / 12;                 // column tile * groups + group
+    const int part = blk % 3, s = blk / 6, j = (blk / 3) & 1;
+    const int64_t col = (tg / groups) * kWsTile + 2 * (lane & 31) + j;
+    const int64_t k0 = (tg % groups) * 32 + 16 * (lane >> 5) + 8 * s;
+    float x[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) x[t] = b[(k0 + t) * n + col];
+    u32x4 parts[3];
+    SplitOperand(x, parts);
+    dst[idx] = parts[part];
+  }
+}
+
 }  // namespace
 
+void LaunchStageF32Parts(const float* b, int64_t k, int64_t n, void* dst, hipStream_t stream) {
+  if (n % kWsTile != 0 || k % 32 != 0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "staged fp32 parts need n % 64 == 0, k % 32 == 0");
+  const int64_t slots = static_cast<int64_t>(StagedF32PartsBytes(k, n) / 16);
+  int64_t grid = (slots + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(StageF32PartsKernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, b, k, n,
+                     static_cast<u32x4*>(dst), slots);
+  Check(hipGetLastError(), "StageF32PartsKernel launch");
+}
+
 bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, int64_t m, int64_t k, int64_t n,
-                   const Epilogue& epi, hipStream_t stream, const RmsRequest* rms) {
+                   const Epilogue& epi, hipStream_t stream, const RmsRequest* rms, bool stage_b) {
   if (m < 1 || n < 1 || k < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMM shape out of range");
   Context& ctx0 = Ctx();
   const bool q8 = bq.q != nullptr;
@@ -688,9 +743,17 @@ bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
       ws.partials = wsplits > 1 ? static_cast<float*>(Workspace(static_cast<size_t>(wsplits * m * n) * sizeof(float)))
                                 : nullptr;
       ws.epi = epi;
+      // B's staged parts when it has them (a weight: built on its second use, StagedF32Parts).
+      ws.bparts = static_cast<const u32x4*>(StagedF32Parts(b, k, n, stream, stage_b));
       const dim3 grid(static_cast<uint32_t>(wtiles), static_cast<uint32_t>(wsplits));
-      if (ws.k_per_wg / 4 == 256) hipLaunchKernelGGL(GemmF32SplitBf16Kernel<8>, grid, dim3(kThreads), 0, stream, ws);
-      else hipLaunchKernelGGL(GemmF32SplitBf16Kernel<0>, grid, dim3(kThreads), 0, stream, ws);
+      const bool full = ws.k_per_wg / 4 == 256;
+      if (ws.bparts != nullptr) {
+        if (full) hipLaunchKernelGGL((GemmF32SplitBf16Kernel<8, true>), grid, dim3(kThreads), 0, stream, ws);
+        else hipLaunchKernelGGL((GemmF32SplitBf16Kernel<0, true>), grid, dim3(kThreads), 0, stream, ws);
+      } else {
+        if (full) hipLaunchKernelGGL((GemmF32SplitBf16Kernel<8, false>), grid, dim3(kThreads), 0, stream, ws);
+        else hipLaunchKernelGGL((GemmF32SplitBf16Kernel<0, false>), grid, dim3(kThreads), 0, stream, ws);
+      }
       Check(hipGetLastError(), "GemmF32SplitBf16Kernel launch");
       if (wsplits > 1)
         LaunchSplitReduce(ws.partials, static_cast<int32_t>(wsplits), m, n, c, kScalePerRow, nullptr, 0, epi, stream);

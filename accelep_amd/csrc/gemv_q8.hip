@@ -953,19 +953,34 @@ __global__ void TileGroupsKernel(const int8_t* q, int64_t k, int64_t n, int8_t* 
 
 // ---- split-K reduction ----------------------------------------------------------------------
 // One thread per output column of a row (blockIdx.y strides over rows): no index division.
+// Every load of an element (the first kReduceRegSplits partial sums, the column scale, the bias
+// and the residual) is issued before the first add, so an element costs one memory round trip
+// instead of one per split pair and one more for the epilogue; the sums are still added in
+// split order, so the bits are unchanged.
+constexpr int kReduceRegSplits = 8;
+
 __global__ void SplitReduceKernel(const float* partials, int32_t splits, int64_t m, int64_t n, float* c,
                                   int32_t mode, const float* scale, int64_t const_index, Epilogue epi) {
   const int64_t j = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (j >= n) return;
   const int64_t total = m * n;
-  float cs = 1.f;
-  if (scale != nullptr && mode == kScalePerCol) cs = scale[j];
-  if (scale != nullptr && mode == kScaleConst) cs = scale[const_index];
+  const float* sc = nullptr;
+  if (scale != nullptr && mode == kScalePerCol) sc = scale + j;
+  if (scale != nullptr && mode == kScaleConst) sc = scale + const_index;
   for (int64_t i = blockIdx.y; i < m; i += gridDim.y) {
     const int64_t idx = i * n + j;
-    float s = partials[idx];
-    for (int sp = 1; sp < splits; ++sp) s = s + partials[static_cast<int64_t>(sp) * total + idx];
-    StoreC(c, i, j, n, epi, ApplyEpilogue(__fmul_rn(s, cs), i, j, n, epi));
+    float v[kReduceRegSplits];
+#pragma unroll
+    for (int sp = 0; sp < kReduceRegSplits; ++sp) v[sp] = sp < splits ? partials[sp * total + idx] : 0.f;
+    const float cs = sc != nullptr ? *sc : 1.f;
+    const float bias_v = epi.bias != nullptr ? epi.bias[BiasIndex(epi, i, j)] : 0.f;
+    const float res_v = epi.residual != nullptr ? epi.residual[idx] : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int sp = 1; sp < kReduceRegSplits; ++sp)
+      if (sp < splits) s = s + v[sp];
+    for (int sp = kReduceRegSplits; sp < splits; ++sp) s = s + partials[static_cast<int64_t>(sp) * total + idx];
+    StoreC(c, i, j, n, epi, ApplyEpilogueLoaded(__fmul_rn(s, cs), epi, bias_v, res_v));
   }
 }
 

@@ -1,4 +1,4 @@
-// Staged copies of constant int8 weights in the layout the GEMV streams best.
+// Staged copies of constant weights in the layouts the GEMV and GEMM kernels stream best.
 //
 // accel::MatMulQuantized receives W as the row-major [k, n] int8 bytes the EP uploaded
 // (src/ep.cc:843-900, src/runtime.cc:326-327). Read in that layout, a workgroup that owns a
@@ -8,6 +8,11 @@
 // same tiles instead, and the int8-weight GEMM a bf16 copy in its MFMA operand order); later
 // calls read the copy. The original bytes stay as
 // they are, so every counted copy and every other kernel still sees the EP's layout.
+//
+// The small-grid fp32 GEMM reads an fp32 weight as bf16 parts (hi + mid + lo, its operand split)
+// staged the same way, but only on the matrix's second use with no write to its allocation in
+// between: a product whose B is rewritten before every call (an activation) never pays for a
+// copy it could not reuse.
 //
 // A copy is keyed by (allocation id, byte offset, k, n) and dropped when its allocation is
 // freed or written through this library (host-to-device copies, pokes, kernel outputs).
@@ -20,6 +25,7 @@
 #include <list>
 #include <map>
 #include <mutex>
+#include <set>
 #include <tuple>
 #include <unordered_set>
 #include <vector>
@@ -30,7 +36,7 @@
 namespace accel_hip {
 namespace {
 
-enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1, kLayoutBf16 = 2 };
+enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1, kLayoutBf16 = 2, kLayoutF32Parts = 3 };
 
 struct Key {
   uint64_t id;
@@ -53,7 +59,9 @@ std::mutex g_mu;
 std::map<Key, Entry> g_staged;
 size_t g_staged_bytes = 0;
 uint64_t g_tick = 0;
-std::atomic<bool> g_any{false};  // fast path for writes when nothing is staged
+std::atomic<bool> g_any{false};  // fast path for writes when nothing is staged or seen
+// fp32 matrices used once since their allocation was last written (staged on the next use).
+std::set<Key> g_seen;
 constexpr size_t kStagedLimit = size_t(64) << 30;
 uint64_t g_next_serial = 1;
 std::unordered_set<uint64_t> g_live_serials;
@@ -81,14 +89,15 @@ void EvictFor(size_t bytes) {
   }
 }
 
-const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStream_t stream, bool create) {
+const int8_t* Staged(const void* src, int64_t k, int64_t n, int layout, hipStream_t stream, bool create) {
   if (k <= 0 || n <= 0) return nullptr;
   uint64_t id = 0;
   const char* base = nullptr;
   size_t alloc_bytes = 0;
-  if (!FindAllocation(q, &id, &base, &alloc_bytes)) return nullptr;
-  const size_t offset = static_cast<size_t>(reinterpret_cast<const char*>(q) - base);
-  const size_t need = static_cast<size_t>(k) * static_cast<size_t>(n);
+  if (!FindAllocation(src, &id, &base, &alloc_bytes)) return nullptr;
+  const size_t offset = static_cast<size_t>(static_cast<const char*>(src) - base);
+  const size_t elem = layout == kLayoutF32Parts ? sizeof(float) : 1;
+  const size_t need = static_cast<size_t>(k) * static_cast<size_t>(n) * elem;
   if (offset + need > alloc_bytes) return nullptr;  // the matrix must lie inside one allocation
   std::lock_guard<std::mutex> lock(g_mu);
   const Key key{id, offset, k, n, layout};
@@ -99,16 +108,30 @@ const int8_t* Staged(const int8_t* q, int64_t k, int64_t n, int layout, hipStrea
     return it->second.data;
   }
   if (!create) return nullptr;
-  RefuseInCapture("staging an int8 weight copy for the GEMV (its first use)");
+  if (layout == kLayoutF32Parts) {
+    // Optional: B is split on the fly without it. Never built in a capture; built on the
+    // second use since the allocation was last written.
+    if (Capturing()) return nullptr;
+    if (g_seen.insert(key).second) {
+      g_any.store(true);
+      return nullptr;
+    }
+    g_seen.erase(key);
+  } else {
+    RefuseInCapture("staging an int8 weight copy for the GEMV (its first use)");
+  }
   ReleasePending();
-  const size_t bytes = layout == kLayoutGroups ? StagedGroupBytes(k, n)
-                       : layout == kLayoutBf16  ? StagedBf16Bytes(k, n)
-                                                : StagedTileBytes(k, n);
+  const size_t bytes = layout == kLayoutGroups     ? StagedGroupBytes(k, n)
+                       : layout == kLayoutBf16     ? StagedBf16Bytes(k, n)
+                       : layout == kLayoutF32Parts ? StagedF32PartsBytes(k, n)
+                                                   : StagedTileBytes(k, n);
   EvictFor(bytes);
   int8_t* dst = nullptr;
   if (hipMalloc(reinterpret_cast<void**>(&dst), bytes) != hipSuccess) return nullptr;  // fall back to raw
+  const int8_t* q = static_cast<const int8_t*>(src);
   if (layout == kLayoutGroups) LaunchTileGroups(q, k, n, dst, stream);
   else if (layout == kLayoutBf16) LaunchTileBf16(q, k, n, dst, stream);
+  else if (layout == kLayoutF32Parts) LaunchStageF32Parts(static_cast<const float*>(src), k, n, dst, stream);
   else LaunchTileColumns(q, k, n, dst, stream);
   const uint64_t serial = g_next_serial++;
   g_staged.emplace(key, Entry{dst, bytes, ++g_tick, serial});
@@ -132,6 +155,11 @@ const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_
 const void* StagedBf16Image(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
   if (k % 32 != 0) return nullptr;
   return Staged(q, k, n, kLayoutBf16, stream, create);
+}
+
+const void* StagedF32Parts(const float* b, int64_t k, int64_t n, hipStream_t stream, bool create) {
+  if (b == nullptr || k % 32 != 0 || n % 64 != 0) return nullptr;
+  return Staged(b, k, n, kLayoutF32Parts, stream, create);
 }
 
 void BeginStagedUses() {
@@ -174,7 +202,9 @@ void DropStagedForAllocation(uint64_t id) {
     FreeEntry(it->second);
     it = g_staged.erase(it);
   }
-  g_any.store(!g_staged.empty());
+  for (auto it = g_seen.lower_bound(Key{id, 0, INT64_MIN, INT64_MIN, 0}); it != g_seen.end() && it->id == id;)
+    it = g_seen.erase(it);
+  g_any.store(!g_staged.empty() || !g_seen.empty());
 }
 
 }  // namespace accel_hip

@@ -152,8 +152,8 @@ def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
 
     Step i reads weight copy i % rotation. The warm-up calls every copy at least once, so
     each is staged (the GEMV's first use of a weight builds its tiled copy, which the library
-    refuses inside a capture) and the workspaces have their final size before anything is
-    captured. A lead-in of whole rotations (at least 4 steps) runs untimed right before the
+    refuses inside a capture; the fp32 GEMM stages a weight's bf16 parts on its second use)
+    and the workspaces have their final size before anything is captured. A lead-in of whole rotations (at least 4 steps) runs untimed right before the
     start event and ends on the last copy, so the timed steps walk the copies in order and a
     copy is never read again before the other copies (> 256 MB) have streamed through the
     cache.

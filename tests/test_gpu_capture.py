@@ -9,6 +9,8 @@ what a capture must refuse, and stale graphs.
 * A graph whose capture read a staged weight copy is refused at launch once that copy has
   been dropped (W rewritten or freed): the launch returns ACCEL_HIP_RUNTIME_ERROR and the
   graph is never replayed. A graph that did not read the dropped copy still replays.
+* The fp32 GEMM's staged bf16 parts of a weight (built on its second use) give the same bits
+  as the split on the fly, and a graph that read them is refused once they are dropped.
 
 * An event recorded during a capture becomes a node of the graph that every replay records,
   and stays timeable (the bench times its steps between two such events).
@@ -301,3 +303,72 @@ def test_event_records_inside_a_capture_are_timeable():
                                    rtol=1e-4, atol=1e-4)
     finally:
         check(L.accel_hip_graph_destroy(handle))
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 1024, 512), (64, 2048, 192)])
+def test_fp32_weight_parts_staged_on_second_use(m, k, n):
+    """The small-grid fp32 GEMM stages B as bf16 parts on B's second use with no write to it in
+    between, and reads the parts from then on. The staged parts are the bits of the split on the
+    fly, so every call stores the same bits. A graph captured after the staging reads the parts:
+    rewriting B drops them and the graph is refused (which shows the parts were read). A B
+    rewritten before each call (an activation) is never staged: its graph replays after the
+    rewrite and follows the new values. (128 x 1024 x 512: one K range per workgroup; 64 x 2048 x
+    192: K split over two workgroups.)"""
+    L = lib()
+    r = np.random.default_rng(m + n)
+    a_h = r.standard_normal((m, k)).astype(np.float32)
+    b1 = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
+    b2 = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
+    a, b, c = dev(a_h), dev(b1), dev(np.zeros((m, n), np.float32))
+
+    def run():
+        check(L.accel_hip_matmul_fused(a.ptr, b.ptr, c.ptr, m, k, n, None))
+        return c.numpy()
+
+    print(f"fp32 staged parts m={m} k={k} n={n}", flush=True)
+    first = run()  # split on the fly; B seen once
+    assert_gamma_bound(first, a_h, b1)
+    same_bits(run(), first)  # stages the parts, then reads them
+    same_bits(run(), first)
+    check(L.accel_hip_capture_begin())
+    try:
+        check(L.accel_hip_matmul_fused(a.ptr, b.ptr, c.ptr, m, k, n, None))
+    finally:
+        graph = _end_capture()
+    try:
+        c.upload(np.zeros((m, n), np.float32))
+        check(L.accel_hip_graph_launch(graph, 1))
+        same_bits(c.numpy(), first)
+        b.upload(b2)  # drops the staged parts the graph reads
+        c.upload(np.full((m, n), 7.0, np.float32))
+        rc = L.accel_hip_graph_launch(graph, 1)
+        msg = L.accel_hip_last_error().decode()
+        assert rc == RUNTIME_ERROR and "stale" in msg, (rc, msg)
+        assert (c.numpy() == 7.0).all()  # nothing ran
+    finally:
+        check(L.accel_hip_graph_destroy(graph))
+    again = run()  # seen again after the rewrite
+    assert_gamma_bound(again, a_h, b2)
+    same_bits(run(), again)  # staged anew
+
+    # An activation: rewritten before every call, so never staged.
+    act = dev(b1)
+    outs = []
+    for bh in (b1, b2, b1):
+        act.upload(bh)
+        check(L.accel_hip_matmul_fused(a.ptr, act.ptr, c.ptr, m, k, n, None))
+        outs.append(c.numpy())
+    same_bits(outs[0], first)
+    same_bits(outs[1], again)
+    same_bits(outs[2], first)
+    check(L.accel_hip_capture_begin())
+    try:
+        check(L.accel_hip_matmul_fused(a.ptr, act.ptr, c.ptr, m, k, n, None))
+    finally:
+        graph = _end_capture()
+    try:
+        act.upload(b2)
+        check(L.accel_hip_graph_launch(graph, 1))  # reads B itself: not stale
+        same_bits(c.numpy(), again)
+    finally:
+        check(L.accel_hip_graph_destroy(graph))
