@@ -36,6 +36,10 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
     # Packed fp32 (v_pk_*_f32) stays off: the compiler may only emit scalar fp32 VALU ops.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Kernel arguments preloaded into SGPRs at wave launch (gfx950 kernarg preload): a wave
+    # issues its first global loads without a scalar-load round trip to the kernarg segment.
+    # Kernels also keep a prologue that loads them, for firmware without preload.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-result", "-fvisibility=hidden",
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]

@@ -267,6 +267,13 @@ struct GemvPrologue {
   // (the GEMV's `a` is not read).
   const float* attn_partial = nullptr;
   int32_t attn_splits = 0;
+  // Side outputs of the m = 1 entry kernel without an input transform (the launcher refuses
+  // them elsewhere), for a decode step's LM head. greedy_keys [tiles of 8 columns]: each
+  // tile's largest greedy key (GreedyKey of the stored value and its column), reduced by
+  // LaunchGreedyKeys. advance: workgroup 0 adds 1 to advance[0] and advance[1]
+  // (LaunchAdvance's step), which the product does not read.
+  uint64_t* greedy_keys = nullptr;
+  int32_t* advance = nullptr;
 };
 constexpr int64_t kGemvPrologueMaxK = 4096;
 constexpr int64_t kGemvAttnMaxPairs = 2048;  // heads x splits of GemvPrologue::attn_partial
@@ -378,5 +385,12 @@ void LaunchSampleToken(const float* logits, int32_t* chosen, int64_t vocab, floa
                        int32_t top_k, hipStream_t stream, const int32_t* index_dev = nullptr,
                        void* greedy_work = nullptr, size_t greedy_bytes = 0);
 size_t GreedyWorkBytes(int64_t vocab);
+// The greedy pick from the per-tile keys a GEMV stored (GemvPrologue::greedy_keys, `count`
+// keys over the logits row `logits`): chosen[*index_dev] = the id of the largest key, 0 when
+// every value is a NaN or logits[0] is a NaN (the same id as LaunchSampleToken's greedy pick).
+// One workgroup; count <= kGreedyKeysMax.
+constexpr int64_t kGreedyKeysMax = 65536;
+void LaunchGreedyKeys(const uint64_t* keys, int64_t count, const float* logits, int32_t* chosen,
+                      const int32_t* index_dev, hipStream_t stream);
 
 }  // namespace accel_hip

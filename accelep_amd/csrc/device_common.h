@@ -146,6 +146,20 @@ __device__ __forceinline__ float ByteToFloat(uint32_t word, int b) {
   return static_cast<float>(static_cast<int32_t>(word << (24 - 8 * b)) >> 24);
 }
 
+// An unsigned key whose order is the float order (-0 below +0, NaNs by their bits).
+__device__ __forceinline__ uint32_t OrderKey(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// Greedy pick key of value v at id i: OrderKey(v == 0 ? +0 : v) << 32 | (2^32 - 1 - i), and 0
+// for a NaN. The largest key is the largest value and, among equal values (-0 equals +0), the
+// earliest id; a NaN never wins.
+__device__ __forceinline__ uint64_t GreedyKey(float v, uint32_t i) {
+  if (isnan(v)) return 0;
+  const float c = v == 0.f ? 0.f : v;
+  return (static_cast<uint64_t>(OrderKey(c)) << 32) | static_cast<uint64_t>(0xffffffffu - i);
+}
+
 __device__ __forceinline__ unsigned FloatBits(float x) { return __builtin_bit_cast(unsigned, x); }
 __device__ __forceinline__ float BitsFloat(unsigned x) { return __builtin_bit_cast(float, x); }
 // x from lane l ^ 8 (row_ror:8 inside each 16-lane row), l + 7 - 2 (l % 8) (row_half_mirror),

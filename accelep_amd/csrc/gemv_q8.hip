@@ -464,14 +464,17 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
 // issued (the general kernel reads its fields from one argument struct, and the compiler
 // spreads those reads over three or four dependent rounds ahead of the first weight load).
 // The epilogue's arguments, bias and residual values are read while the weight loads are in
-// flight instead of after the sums, so the last workgroup's store waits for no memory. With
+// flight instead of after the sums, so the last workgroup's store waits for no memory. The
+// leading 14 argument dwords (pointers and sizes, `second` the input transform's second
+// operand) are preloaded into SGPRs at wave launch, so every load a step needs issues without
+// waiting for the kernarg segment; c, the epilogue and the prologue are read behind them. With
 // an input prologue (kAOp) the weight loads are issued first, the transformed row is staged
 // in LDS (StageInputRow) while they are in flight, and A is read from there.
 template <int kSteps, bool kClamp, bool kPlain, int kAOp, bool kCached>
 __global__ __launch_bounds__(NarrowShape<1>::kThreads)
 __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) void GemvM1Kernel(
-    const int8_t* tiled, const float* a, const float* scale, float* c, int32_t k, int32_t n, int32_t tiles,
-    int32_t tiles_per_xcd, int32_t scale_index_mul, int32_t const_index, Epilogue epi, GemvPrologue pro) {
+    const int8_t* tiled, const float* a, const float* second, const float* scale, int32_t k, int32_t n,
+    int32_t attn_splits, int32_t scale_index_mul, int32_t const_index, float* c, Epilogue epi, GemvPrologue pro) {
   using S = NarrowShape<1>;
   static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
   __shared__ float red[S::kWaves][kNarrowTile];
@@ -479,6 +482,8 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int tiles = (n + kNarrowTile - 1) / kNarrowTile;  // the launcher's tile count and grid
+  const int tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
   const int tile_raw = (blockIdx.x % kXcds) * tiles_per_xcd + blockIdx.x / kXcds;
   const bool tile_live = tile_raw < tiles;
   const int tile = tile_live ? tile_raw : tiles - 1;
@@ -498,7 +503,6 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     // norm weight, or up for SiLU*up), with no LDS stage and no barrier.
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp, kCached>(u, 2 * tid, k, tbase, b);
-    const float* second = kAOp == kAOpRmsAfter ? pro.rms_weight : pro.silu_up;
     float2 xv[kSteps], wv[kSteps];
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) {
@@ -528,13 +532,13 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp, kCached>(u, 2 * tid, k, tbase, b);
     constexpr int kStride = 2 + kAttnDim;
-    const int splits = pro.attn_splits;
+    const int splits = attn_splits;
     float2 ml[kSteps][kAttnRegSplits], ac[kSteps][kAttnRegSplits];
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) {
       const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
       const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole, in one head
-      const float* head = pro.attn_partial + (rp / kAttnDim) * splits * kStride;
+      const float* head = second + (rp / kAttnDim) * splits * kStride;
 #pragma unroll
       for (int sp = 0; sp < kAttnRegSplits; ++sp) {
         ml[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride);
@@ -545,7 +549,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     for (int u = 0; u < kSteps; ++u) {
       const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
       const int rp = !kClamp || r < k - 2 ? r : k - 2;
-      AttnCombinePair(pro.attn_partial, splits, rp / kAttnDim, rp % kAttnDim, ml[u], ac[u], b.a[u][0][0],
+      AttnCombinePair(second, splits, rp / kAttnDim, rp % kAttnDim, ml[u], ac[u], b.a[u][0][0],
                       b.a[u][0][1]);
     }
   } else {
@@ -586,6 +590,8 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     if (lane == 0) ss_part[wave] = w_ss;
   }
   __syncthreads();
+  [[maybe_unused]] float out = 0.f;
+  [[maybe_unused]] uint64_t key = 0;
   if (tile_live && tid < kNarrowTile && col < n) {
     float sum = red[0][tid];
 #pragma unroll
@@ -601,7 +607,24 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     if (kPlain) {
       c[col] = x;
     } else {
-      StoreC(c, 0, col, n, epi, ApplyEpilogueLoaded(x, epi, bias_v, res_v));
+      out = ApplyEpilogueLoaded(x, epi, bias_v, res_v);
+      StoreC(c, 0, col, n, epi, out);
+      if constexpr (kAOp == kAOpNone) key = GreedyKey(out, static_cast<uint32_t>(col));
+    }
+  }
+  if constexpr (!kPlain && kAOp == kAOpNone) {
+    // Side outputs (GemvPrologue): the tile's largest greedy key, from lanes 0..7 of wave 0
+    // (the other lanes hold key 0 and only lanes 0..7 meet in the xor 4, 2, 1 exchanges), and
+    // the decode loop's advance.
+    if (pro.greedy_keys != nullptr && wave == 0) {
+      key = max(key, XorLane<4>(key));
+      key = max(key, XorLane<2>(key));
+      key = max(key, XorLane<1>(key));
+      if (lane == 0 && tile_live) pro.greedy_keys[tile] = key;
+    }
+    if (pro.advance != nullptr && blockIdx.x == 0 && tid == 0) {
+      pro.advance[0] = pro.advance[0] + 1;
+      pro.advance[1] = pro.advance[1] + 1;
     }
   }
 }
@@ -1075,6 +1098,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                    : prologue->silu_up != nullptr                          ? kAOpSiluUp
                                                                            : kAOpNone;
   static_assert(kGemvPrologueMaxK <= NarrowShape<1>::kBatchRows, "prologue rows fit one batch");
+  const bool side = prologue != nullptr && (prologue->greedy_keys != nullptr || prologue->advance != nullptr);
   if (a_op != kAOpNone && (m != 1 || b.tiled == nullptr || b.zero != nullptr || b.mode == kScalePerRow ||
                            k > kGemvPrologueMaxK))
     Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV input prologue needs m = 1, staged tiles, no zero points, k <= 4096");
@@ -1093,6 +1117,8 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                           k % kSplitBlockRows == 0 && k < (int64_t(1) << 28) && m * n <= 0x7fffffff &&
                           reinterpret_cast<uintptr_t>(a) % 16 == 0 && (b.mode == kScalePerCol || b.mode == kScaleConst);
   const bool narrow = !split_bf16 && m <= 4 && b.tiled != nullptr && k < (int64_t(1) << 28);
+  if (side && !narrow)
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV greedy keys and advance need the m = 1 kernel (m = 1, staged tiles)");
   const int64_t tile_cols = narrow || split_bf16 ? kNarrowTile : kWideTile;
   const int64_t tiles = (n + tile_cols - 1) / tile_cols;
   int64_t splits = 1;
@@ -1176,21 +1202,30 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     const bool m1 = m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
                     n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
                     epi.rms_weight == nullptr;
+    if (side && (!m1 || a_op != kAOpNone))
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV greedy keys and advance need the m = 1 kernel (m = 1, k <= 4096, "
+                                       "staged tiles, per-column or tensor scale, aligned pairs) and no input "
+                                       "prologue");
     if (!m1 && a_op == kAOpRmsAfter) a_op = kAOpRms;  // the general kernel normalizes first
     if (!m1 && a_op == kAOpAttn)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV attention prologue needs the m = 1 kernel (per-column or tensor scale)");
     if (m1) {
       const int steps = static_cast<int>((k + NarrowShape<1>::kStepRows - 1) / NarrowShape<1>::kStepRows);
       const bool clamp = k != steps * NarrowShape<1>::kStepRows;
-      const bool plain = epi.Identity() && epi.split[0] == 0 && a_op == kAOpNone;
+      const bool plain = epi.Identity() && epi.split[0] == 0 && a_op == kAOpNone && !side;
       const GemvPrologue pro = prologue != nullptr ? *prologue : GemvPrologue{};
+      // The input transform's second operand (its pointer is among the preloaded arguments).
+      const float* second = a_op == kAOpRmsAfter ? pro.rms_weight
+                            : a_op == kAOpSiluUp ? pro.silu_up
+                            : a_op == kAOpAttn   ? pro.attn_partial
+                                                 : nullptr;
+      const int32_t attn_splits = a_op == kAOpAttn ? pro.attn_splits : 0;
       const int32_t mul = b.mode == kScalePerCol ? 1 : 0;
       const int32_t cidx = b.mode == kScalePerCol ? 0 : static_cast<int32_t>(b.const_index);
       const dim3 block(NarrowShape<1>::kThreads);
 #define ACCEL_GEMV_M1_KC(ST, CL, PL, OP, CA)                                                                   \
-  hipLaunchKernelGGL((GemvM1Kernel<ST, CL, PL, OP, CA>), grid, block, 0, stream, b.tiled, a, b.scale, c,        \
-                     static_cast<int32_t>(k), static_cast<int32_t>(n), static_cast<int32_t>(tiles),            \
-                     static_cast<int32_t>(tiles_per_xcd), mul, cidx, epi, pro)
+  hipLaunchKernelGGL((GemvM1Kernel<ST, CL, PL, OP, CA>), grid, block, 0, stream, b.tiled, a, second, b.scale,  \
+                     static_cast<int32_t>(k), static_cast<int32_t>(n), attn_splits, mul, cidx, c, epi, pro)
 #define ACCEL_GEMV_M1_K(ST, CL, PL, OP)          \
   do {                                           \
     if (b.cached)                                \

@@ -144,6 +144,9 @@ struct Model {
   DevBuf attn_work;
   DevBuf attn_arrivals;  // uint32 per head, zero between decode attention launches
   DevBuf greedy_work;    // the greedy pick's count (zero between launches) and keys
+  DevBuf greedy_keys;    // uint64 per 8-column tile of the LM head: the largest greedy key
+  // The last forward's LM head stored greedy_keys for its logits (fused head, ApplyHead).
+  bool head_keys = false;
   ByteBpe bpe;           // accel_llama_tokenizer
   DevBuf text_out;       // a completion's UTF-8 text on its way back (grows to the longest)
 
@@ -280,12 +283,36 @@ struct Model {
     LaunchSiluMul(g, u, m * cfg.intermediate, stream());
     Apply(w, g, c, m, e);
   }
+  // logits = RMSNorm(x; final_norm) @ lm_head for one row: the norm pass, then the product.
+  // Where the m = 1 GEMV runs the product (fast mode, int8 head) the same kernel also stores
+  // the greedy keys of the logits and, given the decode loop's state, advances it (no sampler
+  // scan over the logits and no advance kernel). The logits keep the bits of the plain product.
+  // (Normalizing inside the product, as the layer GEMVs do, made each of the head's 6144
+  // workgroups reduce the row's sum of squares again: 13.3 us against 2.1 + 7.9.) Returns
+  // whether it advanced `state`.
+  bool ApplyHead(const float* x, int32_t* state) {
+    LaunchRmsNormRows(x, final_norm.as<float>(), normed.as<float>(), 1, cfg.hidden, cfg.eps, stream());
+    Mark(kMarkHeadNorm);
+    const bool side = !lm_head.q.empty() && !Ctx().exact_products && lm_head.in <= kGemvPrologueMaxK &&
+                      lm_head.in % 2 == 0 && (lm_head.out + 7) / 8 <= kGreedyKeysMax;
+    head_keys = side;
+    if (!side) {
+      Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, Epilogue{});
+      return false;
+    }
+    GemvPrologue pro;
+    pro.greedy_keys = greedy_keys.as<uint64_t>();
+    pro.advance = state;
+    ApplyPrologue(lm_head, normed.as<float>(), logits.as<float>(), Epilogue{}, pro);
+    return state != nullptr;
+  }
 
   // Forward over `seq` ids at ids[id_offset ..] (device int32) from position `filled`
   // (src/llama_model.cc:209-247). Leaves the last row's logits in `logits`.
   // With `state` (device int32 [position, produced], seq == 1) the position and the id index
-  // are read on the device, so the launches do not depend on the step.
-  void Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids, const int32_t* state = nullptr) {
+  // are read on the device, so the launches do not depend on the step. Returns whether the LM
+  // head advanced `state` (else the caller launches the advance).
+  bool Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids, int32_t* state = nullptr) {
     if (ids == nullptr || seq <= 0 || filled < 0 || seq > cfg.context || filled > cfg.context - seq)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
     const hipStream_t s = stream();
@@ -365,9 +392,9 @@ struct Model {
       Mark(kMarkDown, li);
     }
     Mark(kMarkLayers);
-    ApplyNormed(lm_head, hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, final_norm, logits.as<float>(), 1,
-                Epilogue{}, kMarkHeadNorm);
+    const bool advanced = ApplyHead(hidden.as<float>() + static_cast<int64_t>(seq - 1) * H, state);
     Mark(kMarkHead);
+    return advanced;
   }
 
   // One decode step: forward of chosen[produced] at `position`, then both advance. The
@@ -385,17 +412,17 @@ struct Model {
       return v != nullptr && v[0] == '1';
     }();
     if (eager || (decode_graph == nullptr && !decode_warm)) {
-      Forward(chosen.as<int32_t>(), 1, 0, false, state);
-      LaunchAdvance(state, stream());
+      if (!Forward(chosen.as<int32_t>(), 1, 0, false, state)) LaunchAdvance(state, stream());
       decode_warm = true;
       return;
     }
     if (decode_graph == nullptr) {
       if (accel_hip_capture_begin() != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       try {
-        Forward(chosen.as<int32_t>(), 1, 0, false, state);
-        LaunchAdvance(state, stream());
-        Mark(kMarkAdvance);
+        if (!Forward(chosen.as<int32_t>(), 1, 0, false, state)) {
+          LaunchAdvance(state, stream());
+          Mark(kMarkAdvance);
+        }
       } catch (...) {
         void* broken = nullptr;
         accel_hip_capture_end(&broken);
@@ -435,8 +462,12 @@ struct Model {
       const bool mark_sample = decode_marks >= 0 && decode_graph != nullptr;  // steps that replay the marked graph
       if (mark_sample && accel_hip_event_record(kMarkSampleStart) != ACCEL_HIP_OK)
         Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
-      LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
-                        state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
+      if (!(temperature > 0.f) && head_keys)
+        LaunchGreedyKeys(greedy_keys.as<uint64_t>(), (cfg.vocab + 7) / 8, logits.as<float>(), chosen.as<int32_t>(),
+                         state + 1, stream());
+      else
+        LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
+                          state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
       if (mark_sample && accel_hip_event_record(kMarkSampleEnd) != ACCEL_HIP_OK)
         Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       produced += 1;
@@ -712,6 +743,7 @@ ACCEL_LLAMA_API AccelLlama* accel_llama_create(const AccelLlamaConfig* config) {
                                    static_cast<size_t>(config->heads) * kDecodeSplitMaxBytesPerHead));
     m->attn_arrivals = DevBuf(static_cast<size_t>(config->heads) * sizeof(uint32_t));
     m->greedy_work = DevBuf(GreedyWorkBytes(config->vocab));
+    m->greedy_keys = DevBuf(static_cast<size_t>((config->vocab + 7) / 8) * sizeof(uint64_t));
     for (int32_t l = 0; l < config->layers; ++l) {
       m->k_cache.emplace_back(k_n * f);
       m->v_cache.emplace_back(k_n * f);

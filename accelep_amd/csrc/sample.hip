@@ -19,11 +19,6 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 
-__device__ __forceinline__ uint32_t OrderKey(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 __device__ __forceinline__ uint32_t XorShift32(uint32_t x) {
   x ^= x << 13;
   x ^= x >> 17;
@@ -307,12 +302,6 @@ constexpr int kGreedyThreads = 256;
 constexpr int kGreedyIds = 2048;  // ids per workgroup
 constexpr int kGreedyMaxBlocks = 1024;
 
-__device__ __forceinline__ uint64_t GreedyKey(float v, uint32_t i) {
-  if (isnan(v)) return 0;
-  const float c = v == 0.f ? 0.f : v;
-  return (static_cast<uint64_t>(OrderKey(c)) << 32) | static_cast<uint64_t>(0xffffffffu - i);
-}
-
 __device__ uint64_t BlockMaxKey(uint64_t k, uint64_t* sk) {
   k = max(k, XorLane<32>(k));
   k = max(k, XorLane<16>(k));
@@ -368,7 +357,60 @@ __global__ __launch_bounds__(kGreedyThreads) void GreedyKernel(const float* logi
   }
 }
 
+// ---- greedy from per-tile keys ----------------------------------------------------------------
+// The keys a GEMV stored per 8-column tile (GemvPrologue::greedy_keys) hold the same maximum as
+// GreedyKernel's per-workgroup keys, so one workgroup reduces them (8 loads a thread in flight
+// at once) and answers as GreedyKernel's last workgroup does. No other workgroup is involved.
+constexpr int kKeysThreads = 1024;
+constexpr int kKeysBatch = 8;
+
+__global__ __launch_bounds__(kKeysThreads) void GreedyKeysKernel(const uint64_t* keys, int32_t count,
+                                                                 const float* logits, int32_t* chosen,
+                                                                 const int32_t* index_dev) {
+  __shared__ uint64_t sk[kKeysThreads / 64];
+  const int tid = threadIdx.x;
+  int32_t index = 0;
+  float first = 0.f;
+  if (tid == 0) {
+    index = index_dev != nullptr ? *index_dev : 0;
+    first = logits[0];
+  }
+  uint64_t best = 0;
+  for (int i0 = 0; i0 < count; i0 += kKeysBatch * kKeysThreads) {
+    uint64_t v[kKeysBatch];
+#pragma unroll
+    for (int u = 0; u < kKeysBatch; ++u) {
+      const int i = i0 + u * kKeysThreads + tid;
+      v[u] = i < count ? keys[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kKeysBatch; ++u) best = max(best, v[u]);
+  }
+  best = max(best, XorLane<32>(best));
+  best = max(best, XorLane<16>(best));
+  best = max(best, XorLane<8>(best));
+  best = max(best, XorLane<4>(best));
+  best = max(best, XorLane<2>(best));
+  best = max(best, XorLane<1>(best));
+  if ((tid & 63) == 0) sk[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t k = sk[0];
+    for (int w = 1; w < kKeysThreads / 64; ++w) k = max(k, sk[w]);
+    chosen[index] = (k == 0 || isnan(first)) ? 0 : static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k));
+  }
+}
+
 }  // namespace
+
+void LaunchGreedyKeys(const uint64_t* keys, int64_t count, const float* logits, int32_t* chosen,
+                      const int32_t* index_dev, hipStream_t stream) {
+  if (keys == nullptr || logits == nullptr || chosen == nullptr || count < 1 || count > kGreedyKeysMax)
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "greedy keys: need 1 .. 65536 keys, the logits and the chosen ids");
+  hipLaunchKernelGGL(GreedyKeysKernel, dim3(1), dim3(kKeysThreads), 0, stream, keys, static_cast<int32_t>(count),
+                     logits, chosen, index_dev);
+  Check(hipGetLastError(), "GreedyKeysKernel launch");
+}
 
 size_t GreedyWorkBytes(int64_t vocab) {
   return 64 + static_cast<size_t>((vocab + kGreedyIds - 1) / kGreedyIds) * sizeof(uint64_t);

@@ -404,7 +404,8 @@ def decode_marks(hip, layers, rng, reps=3):
     """Times the parts of one graph-replayed decode token from event nodes inside the captured
     step (ACCEL_LLAMA_DECODE_MARKS=<layer>; the last step of a 512-id prompt and 128 tokens,
     position 639): the sampler, the host's launch of the graph, the embedding, the given layers' five
-    kernels each, all 30 layers, the LM head's norm pass and product, and the position advance.
+    kernels each, all 30 layers, the LM head's norm pass and its product (which also stores the
+    greedy keys and advances the position).
     Every mark is an event node of the graph, which takes about as long as a dependent kernel:
     each span holds the node that ends it, and two marks back to back at the start of the step
     time one node on its own (event_node_us). The unmarked token (decode_us_per_token_unmarked)
@@ -430,15 +431,14 @@ def decode_marks(hip, layers, rng, reps=3):
             for _ in range(reps):
                 model.generate(128)  # 128 tokens: the last one's sampler runs before the last graph replay
                 parts = {
-                    "sampler (GreedyKernel)": span("sample_start", "sample_end"),
+                    "sampler (GreedyKeysKernel)": span("sample_start", "sample_end"),
                     "graph launch (host) and start": span("sample_end", "start"),
                     "embedding": span("start", "embedded"),
                     "layers 0-29": span("embedded", "layers"),
                     "LM head RMSNorm pass": span("layers", "head_norm"),
-                    "LM head GEMV 576 x 49152": span("head_norm", "head"),
-                    "advance": span("head", "advance"),
+                    "LM head GEMV 576 x 49152 (greedy keys, advance)": span("head_norm", "head"),
                 }
-                total = span("sample_start", "advance")
+                total = span("sample_start", "head")
                 node = span("node0", "node1")
                 layer_parts = {
                     "q/k/v GEMV (RMSNorm prologue)": span("layer", "qkv"),

@@ -249,3 +249,69 @@ def test_llama_errors():
         assert b"exceeds context" in L.accel_llama_last_error()
     finally:
         L.accel_llama_destroy(h)
+
+
+def _head_scale_cases(t):
+    """Per-row scales of an LM head whose rows repeat 8 int8 patterns, so logit o is
+    fl(T[o % 8] * s[o]) with T the 8 sums the hidden row gives (read with s = 1): crafted
+    maxima, ties, signed zeros, NaNs and infinities over a ragged vocabulary."""
+    v = 4099
+    sign = np.where(t[np.arange(v) % 8] < 0, -1.0, 1.0).astype(np.float32)
+    r = np.random.default_rng(31)
+    base = (r.uniform(1e-3, 1e-2, v) * r.choice([-1.0, 1.0], v)).astype(np.float32)
+    yield "random", base
+    s = np.ones(v, np.float32)
+    yield "ties_across_tiles", s  # every slot's value repeats in every tile: the earliest id wins
+    s = (-np.abs(base) * sign).astype(np.float32)  # every logit negative
+    s[[3000, 1200]] = 0.0
+    s[1200] = -0.0 * sign[1200]  # -0 at 1200, +0 at 3000: equal values, 1200 wins
+    yield "signed_zero", s
+    s = base.copy(); s[0] = np.nan
+    yield "nan_at_0", s
+    s = base.copy(); s[[1, 7, 2048, 4000]] = np.nan; s[999] = 10.0 * sign[999]
+    yield "nan_elsewhere", s
+    s = np.full(v, np.nan, np.float32); s[0] = -3.0
+    yield "all_nan_but_0", s
+    yield "all_neg_inf", (-np.inf * sign).astype(np.float32)
+    s = base.copy(); s[v - 1] = np.inf * sign[v - 1]
+    yield "inf_in_ragged_tail", s
+
+
+def test_head_greedy_keys_pick_matches_oracle():
+    """The LM head's GEMV stores a greedy key per 8-column tile and one workgroup reduces them:
+    a generate's first id equals the oracle's strict > scan over the logits that the same
+    forward leaves on the device, for crafted rows (ties across tiles, -0 beside +0, NaN at id 0
+    and elsewhere, all NaN, all -inf, +inf in a partial last tile of a 4099-id vocabulary). In
+    exact-products mode (no keys) the many-workgroup greedy kernel gives the oracle's id for
+    its own logits too."""
+    from oracle_ctypes import oracle
+
+    cfg = dict(llama_config("tiny"), vocab=4099)
+    w, q = llama_weights(cfg, 17)
+    w = [(k, l, a) for (k, l, a) in w if k != 3]  # the head is uploaded per case below
+    prompt = np.random.default_rng(3).integers(0, cfg["vocab"], size=9).astype(np.int32)
+    pattern = np.random.default_rng(4).integers(-127, 128, size=(8, cfg["hidden"])).astype(np.int8)
+    head_q = np.ascontiguousarray(pattern[np.arange(cfg["vocab"]) % 8])
+    eng = Engine(cfg, w, q)
+    try:
+        def set_head(scale):
+            s = np.ascontiguousarray(scale, np.float32)
+            assert eng.L.accel_llama_weight_q8(eng.h, 3, -1, head_q.ctypes.data_as(I8P), s.ctypes.data_as(F32P),
+                                               head_q.shape[0], head_q.shape[1]) == 0, eng.L.accel_llama_last_error()
+
+        case = dict(prompt=prompt, max_new=1, eos=-1, temperature=0.0, seed=0, top_k=0)
+        for exact in (0, 1):
+            check(eng.L.accel_hip_set_exact_products(exact))
+            set_head(np.ones(cfg["vocab"], np.float32))
+            t = eng.prefill_logits(prompt)[:8].copy()
+            assert np.all(t != 0) and np.isfinite(t).all()
+            for name, scale in _head_scale_cases(t):
+                set_head(scale)
+                got = int(eng.generate(case)[0])
+                row = eng.prefill_logits(prompt)
+                want, _ = oracle().sample_token(row, 0.0, 1, 0)
+                print(f"exact {exact} {name}: gpu {got} oracle {want}", flush=True)
+                assert got == want
+    finally:
+        check(eng.L.accel_hip_set_exact_products(0))
+        eng.close()
