@@ -732,10 +732,13 @@ constexpr int kDecodeSplitMin = 8;  // the GEMV prologue reads the first 8 split
 constexpr int kDecodeSplitMax = 64;
 static_assert(kDecodeSplitMaxBytesPerHead == kDecodeSplitMax * (2 + kStepDim) * sizeof(float), "partial room");
 
+// The position's pointer, the sizes and the key/value cache and q/k pointers lead the arguments:
+// the first 14 dwords are preloaded into SGPRs at wave launch, so the position load issues at
+// once and every load that depends on it right after; the others are read in its shadow.
 __global__ __launch_bounds__(kDecodeSplitThreads) void DecodeSplitAttentionKernel(
-    const float* q_raw, const float* k_raw, const float* v_raw, float* k_cache, float* v_cache, const float* cos_t,
-    const float* sin_t, int32_t position_arg, const int32_t* position_dev, int32_t group, int32_t kv_heads,
-    int32_t splits, float* partial) {
+    const int32_t* position_dev, int32_t position_arg, int32_t group, int32_t kv_heads, int32_t splits,
+    float* k_cache, float* v_cache, const float* q_raw, const float* k_raw, const float* v_raw, const float* cos_t,
+    const float* sin_t, float* partial) {
   constexpr int kWaves = kDecodeSplitThreads / 64;
   constexpr int kCols = 4;
   constexpr int kQuads = kStepDim / kCols;                 // 16 column quads
@@ -747,8 +750,6 @@ __global__ __launch_bounds__(kDecodeSplitThreads) void DecodeSplitAttentionKerne
   __shared__ float es[kDecodeSplitRows];
   __shared__ float acc_part[kGroups * kStepDim];
   __shared__ float wred[2][kWaves];
-  asm volatile("" ::"s"(k_cache), "s"(v_cache), "s"(q_raw), "s"(k_raw), "s"(v_raw), "s"(cos_t), "s"(sin_t),
-               "s"(position_arg), "s"(group), "s"(kv_heads), "s"(splits), "s"(partial));
   const int position = position_dev != nullptr ? *position_dev : position_arg;
   const int h = blockIdx.x;
   const int sp = blockIdx.y;
@@ -1008,9 +1009,9 @@ int LaunchDecodeSplitAttention(const float* q, const float* k, const float* v, f
   if (partial_bytes < static_cast<size_t>(heads * splits * (2 + kStepDim)) * sizeof(float))
     Fail(ACCEL_HIP_INVALID_ARGUMENT, "attention scratch is too small");
   hipLaunchKernelGGL(DecodeSplitAttentionKernel, dim3(static_cast<uint32_t>(heads), static_cast<uint32_t>(splits)),
-                     dim3(kDecodeSplitThreads), 0, stream, q, k, v, k_cache, v_cache, cos_table, sin_table,
-                     static_cast<int32_t>(position), position_dev, static_cast<int32_t>(heads / kv_heads),
-                     static_cast<int32_t>(kv_heads), static_cast<int32_t>(splits), partial);
+                     dim3(kDecodeSplitThreads), 0, stream, position_dev, static_cast<int32_t>(position),
+                     static_cast<int32_t>(heads / kv_heads), static_cast<int32_t>(kv_heads),
+                     static_cast<int32_t>(splits), k_cache, v_cache, q, k, v, cos_table, sin_table, partial);
   Check(hipGetLastError(), "DecodeSplitAttentionKernel launch");
   return splits;
 }

@@ -92,8 +92,11 @@ __global__ void SiluMulKernel(float* gate, const float* up, int64_t count) {
 
 // SimEmbed (src/sim_embed.cc:9-20). Float table, or int8 table with a per-row scale
 // (value = float(q) * scale[id], the fl(q*s) a float table quantized per row holds).
-__global__ void EmbeddingKernel(const int32_t* ids, const float* table, const int8_t* qtable, const float* row_scale,
-                                float* out, int64_t hidden, int64_t vocab, int32_t* bad, const int32_t* index_dev) {
+// The arguments a row's loads depend on come first: the leading 14 dwords are preloaded into
+// SGPRs at wave launch, so the id chain (index, id, row) starts without a kernarg round trip.
+__global__ void EmbeddingKernel(const int32_t* index_dev, const int32_t* ids, const int8_t* qtable,
+                                const float* row_scale, int64_t hidden, int64_t vocab, const float* table, float* out,
+                                int32_t* bad) {
   const int64_t s = blockIdx.x;
   const int32_t id = ids[(index_dev != nullptr ? *index_dev : 0) + s];
   if (id < 0 || id >= vocab) {
@@ -257,8 +260,8 @@ void LaunchEmbedding(const int32_t* ids, const float* table, const int8_t* qtabl
                      const int32_t* index_dev) {
   if (seq <= 0 || hidden <= 0) return;
   if (seq > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Embedding is too large");
-  hipLaunchKernelGGL(EmbeddingKernel, dim3(static_cast<uint32_t>(seq)), dim3(kBlock), 0, stream, ids, table, qtable,
-                     row_scale, out, hidden, vocab, bad, index_dev);
+  hipLaunchKernelGGL(EmbeddingKernel, dim3(static_cast<uint32_t>(seq)), dim3(kBlock), 0, stream, index_dev, ids, qtable,
+                     row_scale, hidden, vocab, table, out, bad);
   Check(hipGetLastError(), "EmbeddingKernel launch");
 }
 
