@@ -297,10 +297,11 @@ def llama_q8_weights(cfg, rng):
 
 
 # Kernels of one graph-replayed decode token: per layer the q/k/v GEMV, the split attention,
-# the o, gate/up and down GEMVs; then the embedding, the final RMSNorm, the LM head and the
-# position advance in the graph, and the greedy pick launched between replays.
+# the o, gate/up and down GEMVs; then the embedding, the final RMSNorm and the LM head (which
+# also stores the greedy keys and advances the position) in the graph, and the greedy pick
+# from the keys launched between replays.
 def decode_kernels_per_token(cfg):
-    return 5 * cfg["layers"] + 5
+    return 5 * cfg["layers"] + 4
 
 
 def graph_node_floor_us(hip, nodes, reps=20):
