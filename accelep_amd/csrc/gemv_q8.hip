@@ -306,6 +306,42 @@ __device__ __forceinline__ void AttnCombinePair(const float* part, int splits, i
   a1 = __fdiv_rn(o1, l);
 }
 
+// Lane l's value x of lane (l & ~7) | j: a broadcast inside each group of 8 lanes (ds_swizzle in
+// bit mode, and-mask 0x18 and or-mask j over the 32-lane halves; no LDS memory is touched).
+template <int J>
+__device__ __forceinline__ float Bcast8(float x) {
+  static_assert(J >= 0 && J < 8, "lane of an 8-lane group");
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x18 | (J << 5)));
+}
+
+// AttnCombinePair for exactly 8 splits with the work spread over an 8-lane group: the 8 lanes
+// of a group hold row pairs of one head (pairs 32h .. 32h + 31 form head h), so lane l loads
+// only split l % 8's (m, l) beside its own 8 acc pairs, forms that split's weight (one expf),
+// and the group exchanges the weights and the weighted l values. The max, every weight and
+// both sums in split order are AttnCombinePair's, so the pair carries the same bits.
+__device__ __forceinline__ void AttnCombinePairLanes(float2 mls, const float2 (&ac)[kAttnRegSplits], float& a0,
+                                                     float& a1) {
+  float big = mls.x;
+  big = fmaxf(big, XorLane<1>(big));
+  big = fmaxf(big, XorLane<2>(big));
+  big = fmaxf(big, XorLane<4>(big));
+  const float w = mls.x == -INFINITY ? 0.f : expf(__fsub_rn(mls.x, big));
+  const float wl = __fmul_rn(w, mls.y);
+  const float ws[kAttnRegSplits] = {Bcast8<0>(w), Bcast8<1>(w), Bcast8<2>(w), Bcast8<3>(w),
+                                    Bcast8<4>(w), Bcast8<5>(w), Bcast8<6>(w), Bcast8<7>(w)};
+  const float wls[kAttnRegSplits] = {Bcast8<0>(wl), Bcast8<1>(wl), Bcast8<2>(wl), Bcast8<3>(wl),
+                                     Bcast8<4>(wl), Bcast8<5>(wl), Bcast8<6>(wl), Bcast8<7>(wl)};
+  float l = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < kAttnRegSplits; ++sp) {
+    l = __fadd_rn(l, wls[sp]);
+    o0 = __fadd_rn(o0, __fmul_rn(ws[sp], ac[sp].x));
+    o1 = __fadd_rn(o1, __fmul_rn(ws[sp], ac[sp].y));
+  }
+  a0 = __fdiv_rn(o0, l);
+  a1 = __fdiv_rn(o1, l);
+}
+
 // Writes the transformed input row (kAOp) into a_stage; every thread of the workgroup takes
 // part and the row is complete when this returns.
 template <int kAOp, int kThreads>
@@ -533,24 +569,46 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     for (int u = 0; u < kSteps; ++u) LoadNarrowWAt<1, kSteps, kClamp, kCached>(u, 2 * tid, k, tbase, b);
     constexpr int kStride = 2 + kAttnDim;
     const int splits = attn_splits;
-    float2 ml[kSteps][kAttnRegSplits], ac[kSteps][kAttnRegSplits];
+    if (splits == kAttnRegSplits) {
+      // Eight splits: the weights are formed once per 8-lane group (AttnCombinePairLanes). The
+      // groups never mix heads or live and clamped rows: k is 64 x heads, so a head's 32 pairs
+      // and the live pairs both end on a multiple of 8 lanes.
+      float2 mls[kSteps], ac[kSteps][kAttnRegSplits];
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) {
-      const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
-      const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole, in one head
-      const float* head = second + (rp / kAttnDim) * splits * kStride;
+      for (int u = 0; u < kSteps; ++u) {
+        const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+        const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole, in one head
+        const float* head = second + (rp / kAttnDim) * kAttnRegSplits * kStride;
+        mls[u] = *reinterpret_cast<const float2*>(head + (lane & 7) * kStride);
 #pragma unroll
-      for (int sp = 0; sp < kAttnRegSplits; ++sp) {
-        ml[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride);
-        ac[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride + 2 + rp % kAttnDim);
+        for (int sp = 0; sp < kAttnRegSplits; ++sp)
+          ac[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride + 2 + rp % kAttnDim);
       }
-    }
+      // c is read here, while the partials are in flight, not after the combine's arithmetic.
+      asm volatile("" ::"s"(c));
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) {
-      const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
-      const int rp = !kClamp || r < k - 2 ? r : k - 2;
-      AttnCombinePair(second, splits, rp / kAttnDim, rp % kAttnDim, ml[u], ac[u], b.a[u][0][0],
-                      b.a[u][0][1]);
+      for (int u = 0; u < kSteps; ++u) AttnCombinePairLanes(mls[u], ac[u], b.a[u][0][0], b.a[u][0][1]);
+    } else {
+      float2 ml[kSteps][kAttnRegSplits], ac[kSteps][kAttnRegSplits];
+#pragma unroll
+      for (int u = 0; u < kSteps; ++u) {
+        const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+        const int rp = !kClamp || r < k - 2 ? r : k - 2;  // k is even: the pair is whole, in one head
+        const float* head = second + (rp / kAttnDim) * splits * kStride;
+#pragma unroll
+        for (int sp = 0; sp < kAttnRegSplits; ++sp) {
+          ml[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride);
+          ac[u][sp] = *reinterpret_cast<const float2*>(head + sp * kStride + 2 + rp % kAttnDim);
+        }
+      }
+      asm volatile("" ::"s"(c));
+#pragma unroll
+      for (int u = 0; u < kSteps; ++u) {
+        const int r = 2 * tid + u * static_cast<int>(S::kStepRows);
+        const int rp = !kClamp || r < k - 2 ? r : k - 2;
+        AttnCombinePair(second, splits, rp / kAttnDim, rp % kAttnDim, ml[u], ac[u], b.a[u][0][0],
+                        b.a[u][0][1]);
+      }
     }
   } else {
 #pragma unroll
@@ -566,6 +624,10 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
     for (int u = 0; u < kSteps; ++u) LoadNarrowAAt<1, kSteps, false, false, true, kClamp>(u, unused, srow, 2 * tid, k, b);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // c and the norm's eps (not among the preloaded arguments) are read now, behind the loads,
+  // not where the store and the norm factor need them.
+  asm volatile("" ::"s"(c));
+  if constexpr (kAOp == kAOpRmsAfter) asm volatile("" ::"s"(pro.rms_eps));
   float bias_v = 0.f;
   float res_v = 0.f;
   if (!kPlain) {
