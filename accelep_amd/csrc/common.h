@@ -253,7 +253,9 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
 //  * rms_weight: a = fl(float(double(x) * inv) * w), inv = 1/sqrt(sum(double(x)^2)/k + eps),
 //    the sum taken exactly as RmsNormKernel takes it (same bits as the separate pass); or,
 //    with rms_after, a = fl(x * w) and the sums times float(inv) at the store;
-//  * silu_up: a = fl(fl(x / fl(1 + expf(-x))) * up), SiluMulKernel's formula.
+//  * silu_up: a = fl(fl(x / fl(1 + expf(-x))) * up), SiluMulKernel's formula;
+//  * mul_up: a = fl(x * up), for an x that already holds fl(g / fl(1 + expf(-g))) (a GEMV that
+//    stored it with silu_split0): the two kernels together form SiluMulKernel's bits.
 struct GemvPrologue {
   const float* rms_weight = nullptr;
   float rms_eps = 0.f;
@@ -262,6 +264,11 @@ struct GemvPrologue {
   // Used where the m = 1 entry kernel runs (even k <= 4096, x and w 8-byte aligned).
   bool rms_after = false;
   const float* silu_up = nullptr;
+  const float* mul_up = nullptr;
+  // m = 1 kernel with rms_after only: the stored values of columns [0, epi.split[0]) become
+  // fl(v / fl(1 + expf(-v))), SiluMulKernel's first half (the gate of a gate/up product whose
+  // down projection then takes mul_up).
+  bool silu_split0 = false;
   // Decode attention partials [k / 64 heads][attn_splits][2 + 64] (m, l, acc[64]) of
   // LaunchDecodeSplitAttention: the input row is their combine, head h at rows 64h .. 64h + 63
   // (the GEMV's `a` is not read).

@@ -268,6 +268,8 @@ constexpr int kAOpSiluUp = 2;
 constexpr int kAOpRmsAfter = 3;
 // The decode attention's split partials combined into the row (GemvPrologue::attn_partial).
 constexpr int kAOpAttn = 4;
+// A = fl(x * second) (GemvPrologue::mul_up).
+constexpr int kAOpMul = 5;
 constexpr int kAttnDim = 64;
 constexpr int kAttnMaxPairs = static_cast<int>(kGemvAttnMaxPairs);
 constexpr int kAttnRegSplits = 8;  // splits loaded with the weights; more are read after them
@@ -534,7 +536,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   if (kAOp == kAOpNone) {
     const float* const arow[1] = {a};
     LoadNarrowBatch<1, kSteps, false, false, true, kClamp, kCached>(unused, arow, 2 * tid, k, k, tbase, b);
-  } else if (kAOp == kAOpRmsAfter || kAOp == kAOpSiluUp) {
+  } else if (kAOp == kAOpRmsAfter || kAOp == kAOpSiluUp || kAOp == kAOpMul) {
     // Elementwise inputs: each lane forms its own A pairs from x and the second operand (the
     // norm weight, or up for SiLU*up), with no LDS stage and no barrier.
 #pragma unroll
@@ -557,6 +559,9 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
           ss += static_cast<double>(xv[u].x) * static_cast<double>(xv[u].x);
           ss += static_cast<double>(xv[u].y) * static_cast<double>(xv[u].y);
         }
+      } else if (kAOp == kAOpMul) {
+        b.a[u][0][0] = __fmul_rn(xv[u].x, wv[u].x);
+        b.a[u][0][1] = __fmul_rn(xv[u].y, wv[u].y);
       } else {  // SiluMulKernel's formula
         b.a[u][0][0] = __fmul_rn(__fdiv_rn(xv[u].x, __fadd_rn(1.f, expf(-xv[u].x))), wv[u].x);
         b.a[u][0][1] = __fmul_rn(__fdiv_rn(xv[u].y, __fadd_rn(1.f, expf(-xv[u].y))), wv[u].y);
@@ -670,6 +675,9 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
       c[col] = x;
     } else {
       out = ApplyEpilogueLoaded(x, epi, bias_v, res_v);
+      if constexpr (kAOp == kAOpRmsAfter) {
+        if (pro.silu_split0 && col < epi.split[0]) out = __fdiv_rn(out, __fadd_rn(1.f, expf(-out)));
+      }
       StoreC(c, 0, col, n, epi, out);
       if constexpr (kAOp == kAOpNone) key = GreedyKey(out, static_cast<uint32_t>(col));
     }
@@ -1158,6 +1166,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                    : prologue->rms_weight != nullptr && prologue->rms_after ? kAOpRmsAfter
                    : prologue->rms_weight != nullptr                       ? kAOpRms
                    : prologue->silu_up != nullptr                          ? kAOpSiluUp
+                   : prologue->mul_up != nullptr                           ? kAOpMul
                                                                            : kAOpNone;
   static_assert(kGemvPrologueMaxK <= NarrowShape<1>::kBatchRows, "prologue rows fit one batch");
   const bool side = prologue != nullptr && (prologue->greedy_keys != nullptr || prologue->advance != nullptr);
@@ -1258,6 +1267,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
                           : a_op == kAOpRmsAfter
                               ? pair_a && reinterpret_cast<uintptr_t>(prologue->rms_weight) % 8 == 0
                           : a_op == kAOpSiluUp ? pair_a && reinterpret_cast<uintptr_t>(prologue->silu_up) % 8 == 0
+                          : a_op == kAOpMul    ? pair_a && reinterpret_cast<uintptr_t>(prologue->mul_up) % 8 == 0
                           : a_op == kAOpAttn
                               ? k % 2 == 0 && reinterpret_cast<uintptr_t>(prologue->attn_partial) % 8 == 0
                               : k % 2 == 0;  // kAOpRms: the row is staged in LDS
@@ -1268,9 +1278,13 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV greedy keys and advance need the m = 1 kernel (m = 1, k <= 4096, "
                                        "staged tiles, per-column or tensor scale, aligned pairs) and no input "
                                        "prologue");
+    if (prologue != nullptr && prologue->silu_split0 && (!m1 || a_op != kAOpRmsAfter || epi.split[0] <= 0))
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV SiLU store needs the m = 1 kernel with the norm after the product "
+                                       "and a column split");
     if (!m1 && a_op == kAOpRmsAfter) a_op = kAOpRms;  // the general kernel normalizes first
-    if (!m1 && a_op == kAOpAttn)
-      Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV attention prologue needs the m = 1 kernel (per-column or tensor scale)");
+    if (!m1 && (a_op == kAOpAttn || a_op == kAOpMul))
+      Fail(ACCEL_HIP_INVALID_ARGUMENT,
+           "GEMV attention and mul prologues need the m = 1 kernel (per-column or tensor scale, aligned pairs)");
     if (m1) {
       const int steps = static_cast<int>((k + NarrowShape<1>::kStepRows - 1) / NarrowShape<1>::kStepRows);
       const bool clamp = k != steps * NarrowShape<1>::kStepRows;
@@ -1279,6 +1293,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
       // The input transform's second operand (its pointer is among the preloaded arguments).
       const float* second = a_op == kAOpRmsAfter ? pro.rms_weight
                             : a_op == kAOpSiluUp ? pro.silu_up
+                            : a_op == kAOpMul    ? pro.mul_up
                             : a_op == kAOpAttn   ? pro.attn_partial
                                                  : nullptr;
       const int32_t attn_splits = a_op == kAOpAttn ? pro.attn_splits : 0;
@@ -1301,6 +1316,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     else if (a_op == kAOpAttn) ACCEL_GEMV_M1_K(ST, CL, false, kAOpAttn);                    \
     else if (a_op == kAOpRmsAfter) ACCEL_GEMV_M1_K(ST, CL, false, kAOpRmsAfter);            \
     else if (a_op == kAOpSiluUp) ACCEL_GEMV_M1_K(ST, CL, false, kAOpSiluUp);                \
+    else if (a_op == kAOpMul) ACCEL_GEMV_M1_K(ST, CL, false, kAOpMul);                      \
     else if (plain) ACCEL_GEMV_M1_K(ST, CL, true, kAOpNone);                                \
     else ACCEL_GEMV_M1_K(ST, CL, false, kAOpNone);                                          \
   } while (0)

@@ -258,13 +258,16 @@ struct Model {
   // c = RMSNorm(x; norm) @ W: one kernel for a decode row, else the norm pass into `normed`.
   // A wide product (the LM head: 6144 workgroups) takes the separate pass too, rather than
   // every workgroup reading and normalizing the row again.
+  // silu_split0 (only where SiluFold holds): the product's first column split is stored as
+  // SiLU(v) (GemvPrologue::silu_split0).
   void ApplyNormed(const Linear& w, const float* x, const DevBuf& norm, float* c, int64_t m, const Epilogue& e,
-                   int32_t norm_mark = -1) {
+                   int32_t norm_mark = -1, bool silu_split0 = false) {
     if (Fusable(w, m) && w.out <= kFusedNormMaxOut) {
       GemvPrologue pro;
       pro.rms_weight = norm.as<float>();
       pro.rms_eps = cfg.eps;
       pro.rms_after = true;
+      pro.silu_split0 = silu_split0;
       ApplyPrologue(w, x, c, e, pro);
       return;
     }
@@ -272,16 +275,26 @@ struct Model {
     if (norm_mark >= 0) Mark(norm_mark);
     Apply(w, normed.as<float>(), c, m, e);
   }
-  // c = (SiLU(gate) * up) @ W: one kernel for a decode row, else SiLU*up in place first.
-  void ApplySiluUp(const Linear& w, float* g, const float* u, float* c, int64_t m, const Epilogue& e) {
+  // c = (SiLU(gate) * up) @ W: one kernel for a decode row, else SiLU*up in place first. With
+  // silu_done the gate already holds SiLU(gate) (SiluFold) and the GEMV multiplies by up.
+  void ApplySiluUp(const Linear& w, float* g, const float* u, float* c, int64_t m, const Epilogue& e,
+                   bool silu_done = false) {
     if (Fusable(w, m)) {
       GemvPrologue pro;
-      pro.silu_up = u;
+      if (silu_done) pro.mul_up = u;
+      else pro.silu_up = u;
       ApplyPrologue(w, g, c, e, pro);
       return;
     }
     LaunchSiluMul(g, u, m * cfg.intermediate, stream());
     Apply(w, g, c, m, e);
+  }
+  // A decode row's SiLU(gate) * up in two halves: the gate/up GEMV stores SiLU(gate) for its
+  // gate columns (one expf per gate value) and the down GEMV multiplies by up, the same
+  // operations as SiluMulKernel's, instead of every down workgroup forming SiLU per lane.
+  bool SiluFold(const LayerWeights& l, int64_t m) const {
+    return Fusable(l.gu, m) && l.gu.out <= kFusedNormMaxOut && l.gu.in % 2 == 0 && Fusable(l.down, m) &&
+           l.down.in % 2 == 0;
   }
   // logits = RMSNorm(x; final_norm) @ lm_head for one row: the norm pass, then the product.
   // Where the m = 1 GEMV runs the product (fast mode, int8 head) the same kernel also stores
@@ -366,9 +379,10 @@ struct Model {
         pro.attn_splits = splits;
         ApplyPrologue(l.o, attn_work.as<float>(), hidden.as<float>(), residual, pro);
         Mark(kMarkO, li);
-        ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
+        const bool silu_fold = SiluFold(l, seq);
+        ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu, -1, silu_fold);
         Mark(kMarkGateUp, li);
-        ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
+        ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual, silu_fold);
         Mark(kMarkDown, li);
         continue;
       }
@@ -386,9 +400,10 @@ struct Model {
       Mark(kMarkAttention, li);
       Apply(l.o, mixed.as<float>(), hidden.as<float>(), seq, residual);
       Mark(kMarkO, li);
-      ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu);
+      const bool silu_fold = SiluFold(l, seq);
+      ApplyNormed(l.gu, hidden.as<float>(), l.post_norm, gate.as<float>(), seq, gu, -1, silu_fold);
       Mark(kMarkGateUp, li);
-      ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual);
+      ApplySiluUp(l.down, gate.as<float>(), up.as<float>(), hidden.as<float>(), seq, residual, silu_fold);
       Mark(kMarkDown, li);
     }
     Mark(kMarkLayers);
