@@ -508,14 +508,18 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
 // waiting for the kernarg segment; c, the epilogue and the prologue are read behind them. With
 // an input prologue (kAOp) the weight loads are issued first, the transformed row is staged
 // in LDS (StageInputRow) while they are in flight, and A is read from there.
-template <int kSteps, bool kClamp, bool kPlain, int kAOp, bool kCached>
-__global__ __launch_bounds__(NarrowShape<1>::kThreads)
+// kWaves: 4, or 8 for a single step (k <= 1024): every lane then forms at most one row pair
+// of the input transform, where 4 waves would form a second, mostly clamped, one.
+template <int kSteps, bool kClamp, bool kPlain, int kAOp, bool kCached, int kWaves = NarrowShape<1>::kWaves>
+__global__ __launch_bounds__(64 * kWaves)
 __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) void GemvM1Kernel(
     const int8_t* tiled, const float* a, const float* second, const float* scale, int32_t k, int32_t n,
     int32_t attn_splits, int32_t scale_index_mul, int32_t const_index, float* c, Epilogue epi, GemvPrologue pro) {
   using S = NarrowShape<1>;
   static_assert(kSteps >= 1 && kSteps <= S::kUnroll, "one batch");
-  __shared__ float red[S::kWaves][kNarrowTile];
+  // The load helpers step by S::kStepRows (4 waves); a wider workgroup takes one step only.
+  static_assert(kWaves == S::kWaves || (kSteps == 1 && kWaves == 8 && kAOp != kAOpRms), "8 waves: one step");
+  __shared__ float red[kWaves][kNarrowTile];
   __shared__ __align__(16) float a_stage[kAOp == kAOpRms ? kGemvPrologueMaxK : 1];  // the staged row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -651,7 +655,7 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   ComputeNarrowBatch<1, kSteps, false, false, kClamp>(b, 2 * tid, k, zc, acc);
   const float v = WaveColumnSum8(acc[0], lane);
   if ((lane & 7) == 0) red[wave][lane >> 3] = v;
-  __shared__ double ss_part[S::kWaves];
+  __shared__ double ss_part[kWaves];
   if (kAOp == kAOpRmsAfter) {
     const double w_ss = WaveButterfly(ss, [](double x, double y) { return x + y; });
     if (lane == 0) ss_part[wave] = w_ss;
@@ -662,11 +666,11 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   if (tile_live && tid < kNarrowTile && col < n) {
     float sum = red[0][tid];
 #pragma unroll
-    for (int wv = 1; wv < S::kWaves; ++wv) sum = sum + red[wv][tid];
+    for (int wv = 1; wv < kWaves; ++wv) sum = sum + red[wv][tid];
     if (kAOp == kAOpRmsAfter) {
       double total = ss_part[0];
 #pragma unroll
-      for (int wv = 1; wv < S::kWaves; ++wv) total += ss_part[wv];
+      for (int wv = 1; wv < kWaves; ++wv) total += ss_part[wv];
       const double inv = 1.0 / sqrt(total / static_cast<double>(k) + static_cast<double>(pro.rms_eps));
       sum = __fmul_rn(sum, static_cast<float>(inv));
     }
@@ -1320,6 +1324,19 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     else if (plain) ACCEL_GEMV_M1_K(ST, CL, true, kAOpNone);                                \
     else ACCEL_GEMV_M1_K(ST, CL, false, kAOpNone);                                          \
   } while (0)
+      if (a_op == kAOpAttn && k <= 2 * 512) {
+        // One step of 512 lanes: each lane combines at most one row pair of the attention.
+        const dim3 block8(512);
+        const bool clamp8 = k != 1024;
+#define ACCEL_GEMV_M1_ATTN8(CL, CA)                                                                          \
+  hipLaunchKernelGGL((GemvM1Kernel<1, CL, false, kAOpAttn, CA, 8>), grid, block8, 0, stream, b.tiled, a, second, \
+                     b.scale, static_cast<int32_t>(k), static_cast<int32_t>(n), attn_splits, mul, cidx, c, epi, pro)
+        if (clamp8 && b.cached) ACCEL_GEMV_M1_ATTN8(true, true);
+        else if (clamp8) ACCEL_GEMV_M1_ATTN8(true, false);
+        else if (b.cached) ACCEL_GEMV_M1_ATTN8(false, true);
+        else ACCEL_GEMV_M1_ATTN8(false, false);
+#undef ACCEL_GEMV_M1_ATTN8
+      } else {
       switch (steps * 2 + (clamp ? 1 : 0)) {
         case 2: ACCEL_GEMV_M1(1, false); break;
         case 3: ACCEL_GEMV_M1(1, true); break;
@@ -1337,6 +1354,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
         case 15: ACCEL_GEMV_M1(7, true); break;
         case 16: ACCEL_GEMV_M1(8, false); break;
         default: ACCEL_GEMV_M1(8, true); break;
+      }
       }
 #undef ACCEL_GEMV_M1
 #undef ACCEL_GEMV_M1_K
