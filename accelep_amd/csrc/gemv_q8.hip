@@ -703,6 +703,83 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
   }
 }
 
+// ---- one wave per tile: m = 1, a wide product with a short k (the LM head) -------------------
+// Each wave owns one staged 8-column tile over all of k (k <= 1024: at most 8 row pairs a
+// lane, all loads issued first), four tiles a workgroup, and its 8 column sums meet inside the
+// wave (WaveColumnSum8): no LDS stage and no barrier. For 576 x 49152 the 6144 tiles take
+// 1536 workgroups, all resident at once, where one workgroup per tile took three rounds of
+// resident workgroups of 4.6 KB each. Identity epilogue; with kSide the side outputs of
+// GemvPrologue (the tile's greedy key from lanes 0, 8, .., 56, which hold its 8 stored
+// values, and workgroup 0's advance). A lane adds its row pairs in order, then the wave sums:
+// another association than GemvM1Kernel's (rounding only).
+constexpr int kWaveTileWaves = 4;
+
+template <int kLoads, bool kCached, bool kSide>
+__global__ __launch_bounds__(64 * kWaveTileWaves) void GemvWaveTileKernel(const int8_t* tiled, const float* a,
+                                                                          const float* scale, int32_t k, int32_t n,
+                                                                          int32_t scale_index_mul, int32_t const_index,
+                                                                          float* c, GemvPrologue pro) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tiles = (n + kNarrowTile - 1) / kNarrowTile;
+  const int groups = (tiles + kWaveTileWaves - 1) / kWaveTileWaves;
+  const int groups_per_xcd = (groups + kXcds - 1) / kXcds;
+  const int group = (blockIdx.x % kXcds) * groups_per_xcd + blockIdx.x / kXcds;
+  const int tile_raw = group * kWaveTileWaves + wave;
+  const bool tile_live = tile_raw < tiles;
+  const int tile = tile_live ? tile_raw : tiles - 1;
+  const int8_t* tbase = tiled + static_cast<int64_t>(tile) * k * kNarrowTile;  // k is even
+  u32x4 w[kLoads];
+  float2 x[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const int r = 2 * (lane + 64 * j);
+    const int rw = r < k - 2 ? r : k - 2;
+    const u32x4* at = reinterpret_cast<const u32x4*>(tbase + static_cast<uint32_t>(rw) * 8u);
+    if constexpr (kCached)
+      w[j] = *at;
+    else
+      w[j] = __builtin_nontemporal_load(at);
+    x[j] = *reinterpret_cast<const float2*>(a + rw);
+  }
+  const int col = tile * kNarrowTile + (lane >> 3);
+  const int colc = col < n ? col : n - 1;
+  const float col_scale = scale[scale_index_mul * colc + const_index];
+  asm volatile("" ::"s"(c));
+  __builtin_amdgcn_sched_barrier(0);
+  float acc[kNarrowTile];
+#pragma unroll
+  for (int cc = 0; cc < kNarrowTile; ++cc) acc[cc] = 0.f;
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const bool live = 2 * (lane + 64 * j) < k;
+    const float x0 = live ? x[j].x : 0.f;
+    const float x1 = live ? x[j].y : 0.f;
+#pragma unroll
+    for (int cc = 0; cc < kNarrowTile; ++cc) {
+      acc[cc] = __builtin_fmaf(x0, ByteToFloat(w[j][cc >> 2], cc & 3), acc[cc]);
+      acc[cc] = __builtin_fmaf(x1, ByteToFloat(w[j][2 + (cc >> 2)], cc & 3), acc[cc]);
+    }
+  }
+  const float v = WaveColumnSum8(acc, lane);
+  const bool store = tile_live && (lane & 7) == 0 && col < n;
+  const float out = __fmul_rn(v, col_scale);
+  if (store) c[col] = out;
+  if constexpr (kSide) {
+    if (pro.greedy_keys != nullptr) {
+      uint64_t key = store ? GreedyKey(out, static_cast<uint32_t>(col)) : 0;
+      key = max(key, XorLane<8>(key));
+      key = max(key, XorLane<16>(key));
+      key = max(key, XorLane<32>(key));
+      if (lane == 0 && tile_live) pro.greedy_keys[tile] = key;
+    }
+    if (pro.advance != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+      pro.advance[0] = pro.advance[0] + 1;
+      pro.advance[1] = pro.advance[1] + 1;
+    }
+  }
+}
+
 // ---- wide kernel: 4 < m <= 16 ----------------------------------------------------------------
 constexpr int kWideThreads = 256;
 constexpr int kWideWaves = kWideThreads / 64;
@@ -1324,7 +1401,35 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     else if (plain) ACCEL_GEMV_M1_K(ST, CL, true, kAOpNone);                                \
     else ACCEL_GEMV_M1_K(ST, CL, false, kAOpNone);                                          \
   } while (0)
-      if (a_op == kAOpAttn && k <= 2 * 512) {
+      const int64_t wave_tile_loads = (k / 2 + 63) / 64;  // row pairs a lane covers (k is even here)
+      if (a_op == kAOpNone && epi.Identity() && epi.split[0] == 0 && wave_tile_loads <= 8 && k % 2 == 0 &&
+          tiles >= 8 * cus) {
+        const int64_t groups = (tiles + kWaveTileWaves - 1) / kWaveTileWaves;
+        const dim3 wgrid(static_cast<uint32_t>((groups + kXcds - 1) / kXcds * kXcds));
+        const dim3 wblock(64 * kWaveTileWaves);
+#define ACCEL_GEMV_WT(L, CA, SD)                                                                             \
+  hipLaunchKernelGGL((GemvWaveTileKernel<L, CA, SD>), wgrid, wblock, 0, stream, b.tiled, a, b.scale,          \
+                     static_cast<int32_t>(k), static_cast<int32_t>(n), mul, cidx, c, pro)
+#define ACCEL_GEMV_WT_L(L)                             \
+  do {                                                 \
+    if (b.cached && side) ACCEL_GEMV_WT(L, true, true);    \
+    else if (b.cached) ACCEL_GEMV_WT(L, true, false);      \
+    else if (side) ACCEL_GEMV_WT(L, false, true);          \
+    else ACCEL_GEMV_WT(L, false, false);                   \
+  } while (0)
+        switch (wave_tile_loads) {
+          case 1: ACCEL_GEMV_WT_L(1); break;
+          case 2: ACCEL_GEMV_WT_L(2); break;
+          case 3: ACCEL_GEMV_WT_L(3); break;
+          case 4: ACCEL_GEMV_WT_L(4); break;
+          case 5: ACCEL_GEMV_WT_L(5); break;
+          case 6: ACCEL_GEMV_WT_L(6); break;
+          case 7: ACCEL_GEMV_WT_L(7); break;
+          default: ACCEL_GEMV_WT_L(8); break;
+        }
+#undef ACCEL_GEMV_WT_L
+#undef ACCEL_GEMV_WT
+      } else if (a_op == kAOpAttn && k <= 2 * 512) {
         // One step of 512 lanes: each lane combines at most one row pair of the attention.
         const dim3 block8(512);
         const bool clamp8 = k != 1024;

@@ -349,6 +349,31 @@ def test_gemv_m1_entry_kernel_matches_general_kernel(k, n, axis):
         assert_plugin_tolerance(entry, case["a"], dequant_host(case["bq"], k, n))
 
 
+@pytest.mark.parametrize("k,n,axis", [(2, 16389, 1), (130, 16384, 1), (576, 49152, 1), (1022, 20000, -1),
+                                      (1024, 16392, 1)])
+def test_gemv_wave_tile_kernel(k, n, axis):
+    """m = 1 with k <= 1024 over at least 2048 tiles (the LM head's shape, 576 x 49152): one wave
+    per 8-column tile, four tiles a workgroup. k = 2 is one row pair, 130 and 1022 end inside a
+    lane's last load, 1024 fills 8 loads; n = 16389 leaves a partial last tile and dead waves;
+    axis -1 is one scale for the tensor. Within 2 gamma_K and the plugin tolerance of float64,
+    and with integer activations (every partial sum an exact integer) fl(S * scale) bit for bit."""
+    case = c3_case(1, k, n, 11 * k + n, axis=max(axis, 0) if axis >= 0 else 1)
+    if axis < 0:
+        case["bq"]["scale"] = np.array([0.0042], np.float32)
+        case["bq"]["axis"] = -1
+    w = dequant_host(case["bq"], k, n)
+    got = matmul_quantized(case)
+    assert_gamma_bound(got, case["a"], w)
+    assert_plugin_tolerance(got, case["a"], w)
+    r = np.random.default_rng(k)
+    case["a"] = r.integers(-16, 17, size=(1, k)).astype(np.float32)
+    got = matmul_quantized(case)
+    s = case["a"].astype(np.int64) @ case["bq"]["q"].reshape(k, n).astype(np.int64)
+    assert np.abs(s).max() < 2 ** 24
+    scale = case["bq"]["scale"] if axis >= 0 else np.full(n, case["bq"]["scale"][0], np.float32)
+    same_bits(got, (s.astype(np.float32) * scale[None, :]).astype(np.float32))
+
+
 def test_gemv_m1_entry_kernel_epilogues():
     """alpha, beta * bias, Relu / exact Gelu and the residual on the m = 1 entry kernel, whose
     epilogue inputs are loaded before the sums: the general kernel's bits and the composed
