@@ -292,6 +292,10 @@ constexpr int64_t kGemvAttnMaxPairs = 2048;  // heads x splits of GemvPrologue::
 // kGemvPrologueMaxK.
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
                   hipStream_t stream, const GemvPrologue* prologue = nullptr);
+// Whether an m = 1 GEMV of this shape (on staged tiles, aligned pairs, per-column or tensor scale,
+// identity epilogue) runs one wave per tile: an even k <= 1024 over at least 8 tiles per CU. There
+// the norm-after prologue may come with the greedy keys and the advance.
+bool GemvWaveTileApplies(int64_t m, int64_t k, int64_t n);
 // An RMSNormalization of the product's rows (after the epilogue) that a GEMM may take over:
 // out[i, :] = RmsNorm(C[i, :]) with the weight and eps given (SimRmsNorm's arithmetic).
 struct RmsRequest {

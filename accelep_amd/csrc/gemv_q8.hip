@@ -711,12 +711,15 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<1, false, false, kAOp>()))) vo
 // resident workgroups of 4.6 KB each. Identity epilogue; with kSide the side outputs of
 // GemvPrologue (the tile's greedy key from lanes 0, 8, .., 56, which hold its 8 stored
 // values, and workgroup 0's advance). A lane adds its row pairs in order, then the wave sums:
-// another association than GemvM1Kernel's (rounding only).
+// another association than GemvM1Kernel's (rounding only). kRms: the RMSNorm after the
+// product (GemvPrologue::rms_after, weight `second`): every wave holds the whole row, so it
+// reduces the double sum of squares itself (no barrier) and scales its sums by float(1/rms).
 constexpr int kWaveTileWaves = 4;
 
-template <int kLoads, bool kCached, bool kSide>
+template <int kLoads, bool kCached, bool kSide, bool kRms>
 __global__ __launch_bounds__(64 * kWaveTileWaves) void GemvWaveTileKernel(const int8_t* tiled, const float* a,
-                                                                          const float* scale, int32_t k, int32_t n,
+                                                                          const float* second, const float* scale,
+                                                                          int32_t k, int32_t n,
                                                                           int32_t scale_index_mul, int32_t const_index,
                                                                           float* c, GemvPrologue pro) {
   const int lane = threadIdx.x & 63;
@@ -731,6 +734,7 @@ __global__ __launch_bounds__(64 * kWaveTileWaves) void GemvWaveTileKernel(const 
   const int8_t* tbase = tiled + static_cast<int64_t>(tile) * k * kNarrowTile;  // k is even
   u32x4 w[kLoads];
   float2 x[kLoads];
+  [[maybe_unused]] float2 g[kLoads];
 #pragma unroll
   for (int j = 0; j < kLoads; ++j) {
     const int r = 2 * (lane + 64 * j);
@@ -741,27 +745,41 @@ __global__ __launch_bounds__(64 * kWaveTileWaves) void GemvWaveTileKernel(const 
     else
       w[j] = __builtin_nontemporal_load(at);
     x[j] = *reinterpret_cast<const float2*>(a + rw);
+    if constexpr (kRms) g[j] = *reinterpret_cast<const float2*>(second + rw);
   }
   const int col = tile * kNarrowTile + (lane >> 3);
   const int colc = col < n ? col : n - 1;
   const float col_scale = scale[scale_index_mul * colc + const_index];
   asm volatile("" ::"s"(c));
+  if constexpr (kRms) asm volatile("" ::"s"(pro.rms_eps));
   __builtin_amdgcn_sched_barrier(0);
   float acc[kNarrowTile];
 #pragma unroll
   for (int cc = 0; cc < kNarrowTile; ++cc) acc[cc] = 0.f;
+  [[maybe_unused]] double ss = 0.0;  // kRms: this lane's share of sum(double(x)^2)
 #pragma unroll
   for (int j = 0; j < kLoads; ++j) {
     const bool live = 2 * (lane + 64 * j) < k;
-    const float x0 = live ? x[j].x : 0.f;
-    const float x1 = live ? x[j].y : 0.f;
+    float x0 = live ? x[j].x : 0.f;
+    float x1 = live ? x[j].y : 0.f;
+    if constexpr (kRms) {
+      ss += static_cast<double>(x0) * static_cast<double>(x0);
+      ss += static_cast<double>(x1) * static_cast<double>(x1);
+      x0 = __fmul_rn(x0, g[j].x);
+      x1 = __fmul_rn(x1, g[j].y);
+    }
 #pragma unroll
     for (int cc = 0; cc < kNarrowTile; ++cc) {
       acc[cc] = __builtin_fmaf(x0, ByteToFloat(w[j][cc >> 2], cc & 3), acc[cc]);
       acc[cc] = __builtin_fmaf(x1, ByteToFloat(w[j][2 + (cc >> 2)], cc & 3), acc[cc]);
     }
   }
-  const float v = WaveColumnSum8(acc, lane);
+  float v = WaveColumnSum8(acc, lane);
+  if constexpr (kRms) {
+    const double total = WaveButterfly(ss, [](double p, double q) { return p + q; });
+    const double inv = 1.0 / sqrt(total / static_cast<double>(k) + static_cast<double>(pro.rms_eps));
+    v = __fmul_rn(v, static_cast<float>(inv));
+  }
   const bool store = tile_live && (lane & 7) == 0 && col < n;
   const float out = __fmul_rn(v, col_scale);
   if (store) c[col] = out;
@@ -1239,6 +1257,12 @@ void LaunchNarrow(const GemvArgs& args, dim3 grid, bool zero, bool row_scale, bo
 
 }  // namespace
 
+bool GemvWaveTileApplies(int64_t m, int64_t k, int64_t n) {
+  const Context& ctx = Ctx();
+  const int64_t cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
+  return m == 1 && k >= 2 && k <= 1024 && k % 2 == 0 && n < (int64_t(1) << 30) && (n + kNarrowTile - 1) / kNarrowTile >= 8 * cus;
+}
+
 void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
                   hipStream_t stream, const GemvPrologue* prologue) {
   if (m < 1 || m > 16 || k < 1 || n < 1) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV shape out of range");
@@ -1355,10 +1379,14 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     const bool m1 = m == 1 && !zero && !row_scale && splits == 1 && m1_pairs && k <= NarrowShape<1>::kBatchRows &&
                     n < (int64_t(1) << 30) && (b.mode == kScalePerCol || b.mode == kScaleConst) &&
                     epi.rms_weight == nullptr;
-    if (side && (!m1 || a_op != kAOpNone))
+    // The side outputs: the m = 1 kernel without an input transform, or the one-wave-per-tile
+    // kernel (k <= 1024 over at least 8 x CUs tiles) with the norm after the product.
+    const bool wave_tile_rms = a_op == kAOpRmsAfter && GemvWaveTileApplies(m, k, n) && epi.Identity() &&
+                               epi.split[0] == 0;
+    if (side && (!m1 || (a_op != kAOpNone && !wave_tile_rms)))
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV greedy keys and advance need the m = 1 kernel (m = 1, k <= 4096, "
                                        "staged tiles, per-column or tensor scale, aligned pairs) and no input "
-                                       "prologue");
+                                       "prologue but the norm over a wide product");
     if (prologue != nullptr && prologue->silu_split0 && (!m1 || a_op != kAOpRmsAfter || epi.split[0] <= 0))
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV SiLU store needs the m = 1 kernel with the norm after the product "
                                        "and a column split");
@@ -1402,20 +1430,26 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     else ACCEL_GEMV_M1_K(ST, CL, false, kAOpNone);                                          \
   } while (0)
       const int64_t wave_tile_loads = (k / 2 + 63) / 64;  // row pairs a lane covers (k is even here)
-      if (a_op == kAOpNone && epi.Identity() && epi.split[0] == 0 && wave_tile_loads <= 8 && k % 2 == 0 &&
-          tiles >= 8 * cus) {
+      if ((a_op == kAOpNone || a_op == kAOpRmsAfter) && epi.Identity() && epi.split[0] == 0 &&
+          !pro.silu_split0 && GemvWaveTileApplies(m, k, n)) {
+        const bool rms = a_op == kAOpRmsAfter;
         const int64_t groups = (tiles + kWaveTileWaves - 1) / kWaveTileWaves;
         const dim3 wgrid(static_cast<uint32_t>((groups + kXcds - 1) / kXcds * kXcds));
         const dim3 wblock(64 * kWaveTileWaves);
-#define ACCEL_GEMV_WT(L, CA, SD)                                                                             \
-  hipLaunchKernelGGL((GemvWaveTileKernel<L, CA, SD>), wgrid, wblock, 0, stream, b.tiled, a, b.scale,          \
+#define ACCEL_GEMV_WT(L, CA, SD, RM)                                                                         \
+  hipLaunchKernelGGL((GemvWaveTileKernel<L, CA, SD, RM>), wgrid, wblock, 0, stream, b.tiled, a, second, b.scale, \
                      static_cast<int32_t>(k), static_cast<int32_t>(n), mul, cidx, c, pro)
-#define ACCEL_GEMV_WT_L(L)                             \
-  do {                                                 \
-    if (b.cached && side) ACCEL_GEMV_WT(L, true, true);    \
-    else if (b.cached) ACCEL_GEMV_WT(L, true, false);      \
-    else if (side) ACCEL_GEMV_WT(L, false, true);          \
-    else ACCEL_GEMV_WT(L, false, false);                   \
+#define ACCEL_GEMV_WT_R(L, RM)                             \
+  do {                                                     \
+    if (b.cached && side) ACCEL_GEMV_WT(L, true, true, RM);    \
+    else if (b.cached) ACCEL_GEMV_WT(L, true, false, RM);      \
+    else if (side) ACCEL_GEMV_WT(L, false, true, RM);          \
+    else ACCEL_GEMV_WT(L, false, false, RM);                   \
+  } while (0)
+#define ACCEL_GEMV_WT_L(L)              \
+  do {                                  \
+    if (rms) ACCEL_GEMV_WT_R(L, true);  \
+    else ACCEL_GEMV_WT_R(L, false);     \
   } while (0)
         switch (wave_tile_loads) {
           case 1: ACCEL_GEMV_WT_L(1); break;
@@ -1428,6 +1462,7 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
           default: ACCEL_GEMV_WT_L(8); break;
         }
 #undef ACCEL_GEMV_WT_L
+#undef ACCEL_GEMV_WT_R
 #undef ACCEL_GEMV_WT
       } else if (a_op == kAOpAttn && k <= 2 * 512) {
         // One step of 512 lanes: each lane combines at most one row pair of the attention.

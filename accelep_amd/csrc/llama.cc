@@ -296,19 +296,31 @@ struct Model {
     return Fusable(l.gu, m) && l.gu.out <= kFusedNormMaxOut && l.gu.in % 2 == 0 && Fusable(l.down, m) &&
            l.down.in % 2 == 0;
   }
-  // logits = RMSNorm(x; final_norm) @ lm_head for one row: the norm pass, then the product.
-  // Where the m = 1 GEMV runs the product (fast mode, int8 head) the same kernel also stores
-  // the greedy keys of the logits and, given the decode loop's state, advances it (no sampler
-  // scan over the logits and no advance kernel). The logits keep the bits of the plain product.
-  // (Normalizing inside the product, as the layer GEMVs do, made each of the head's 6144
-  // workgroups reduce the row's sum of squares again: 13.3 us against 2.1 + 7.9.) Returns
-  // whether it advanced `state`.
+  // logits = RMSNorm(x; final_norm) @ lm_head for one row. Where the m = 1 GEMV runs the
+  // product (fast mode, int8 head) the same kernel also stores the greedy keys of the logits
+  // and, given the decode loop's state, advances it (no sampler scan over the logits and no
+  // advance kernel). A wide head with a short row (one wave per tile, GemvWaveTileApplies)
+  // with the fused inputs on takes the norm after the product in that kernel too; otherwise the
+  // norm is a pass of its own (in the one-workgroup-per-tile kernel every workgroup would
+  // reduce the row's sum of squares across its waves again: 13.3 us against 2.1 + 7.9).
+  // Returns whether it advanced `state`.
   bool ApplyHead(const float* x, int32_t* state) {
-    LaunchRmsNormRows(x, final_norm.as<float>(), normed.as<float>(), 1, cfg.hidden, cfg.eps, stream());
-    Mark(kMarkHeadNorm);
     const bool side = !lm_head.q.empty() && !Ctx().exact_products && lm_head.in <= kGemvPrologueMaxK &&
                       lm_head.in % 2 == 0 && (lm_head.out + 7) / 8 <= kGreedyKeysMax;
     head_keys = side;
+    if (side && Fusable(lm_head, 1) && GemvWaveTileApplies(1, lm_head.in, lm_head.out)) {
+      // One wave per tile holds the whole row: the norm goes after the product, in the same kernel.
+      GemvPrologue pro;
+      pro.rms_weight = final_norm.as<float>();
+      pro.rms_eps = cfg.eps;
+      pro.rms_after = true;
+      pro.greedy_keys = greedy_keys.as<uint64_t>();
+      pro.advance = state;
+      ApplyPrologue(lm_head, x, logits.as<float>(), Epilogue{}, pro);
+      return state != nullptr;
+    }
+    LaunchRmsNormRows(x, final_norm.as<float>(), normed.as<float>(), 1, cfg.hidden, cfg.eps, stream());
+    Mark(kMarkHeadNorm);
     if (!side) {
       Apply(lm_head, normed.as<float>(), logits.as<float>(), 1, Epilogue{});
       return false;

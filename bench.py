@@ -405,8 +405,8 @@ def decode_marks(hip, layers, rng, reps=3):
     """Times the parts of one graph-replayed decode token from event nodes inside the captured
     step (ACCEL_LLAMA_DECODE_MARKS=<layer>; the last step of a 512-id prompt and 128 tokens,
     position 639): the sampler, the host's launch of the graph, the embedding, the given layers' five
-    kernels each, all 30 layers, the LM head's norm pass and its product (which also stores the
-    greedy keys and advances the position).
+    kernels each, all 30 layers, and the LM head (one kernel: its norm, product, greedy keys and
+    the position advance).
     Every mark is an event node of the graph, which takes about as long as a dependent kernel:
     each span holds the node that ends it, and two marks back to back at the start of the step
     time one node on its own (event_node_us). The unmarked token (decode_us_per_token_unmarked)
@@ -436,8 +436,7 @@ def decode_marks(hip, layers, rng, reps=3):
                     "graph launch (host) and start": span("sample_end", "start"),
                     "embedding": span("start", "embedded"),
                     "layers 0-29": span("embedded", "layers"),
-                    "LM head RMSNorm pass": span("layers", "head_norm"),
-                    "LM head GEMV 576 x 49152 (greedy keys, advance)": span("head_norm", "head"),
+                    "LM head (RMSNorm, GEMV 576 x 49152, greedy keys, advance)": span("layers", "head"),
                 }
                 total = span("sample_start", "head")
                 node = span("node0", "node1")

@@ -251,11 +251,10 @@ def test_llama_errors():
         L.accel_llama_destroy(h)
 
 
-def _head_scale_cases(t):
+def _head_scale_cases(t, v):
     """Per-row scales of an LM head whose rows repeat 8 int8 patterns, so logit o is
     fl(T[o % 8] * s[o]) with T the 8 sums the hidden row gives (read with s = 1): crafted
-    maxima, ties, signed zeros, NaNs and infinities over a ragged vocabulary."""
-    v = 4099
+    maxima, ties, signed zeros, NaNs and infinities over a ragged vocabulary of v ids."""
     sign = np.where(t[np.arange(v) % 8] < 0, -1.0, 1.0).astype(np.float32)
     r = np.random.default_rng(31)
     base = (r.uniform(1e-3, 1e-2, v) * r.choice([-1.0, 1.0], v)).astype(np.float32)
@@ -268,7 +267,7 @@ def _head_scale_cases(t):
     yield "signed_zero", s
     s = base.copy(); s[0] = np.nan
     yield "nan_at_0", s
-    s = base.copy(); s[[1, 7, 2048, 4000]] = np.nan; s[999] = 10.0 * sign[999]
+    s = base.copy(); s[[1, 7, 2048, 4000, v - 2]] = np.nan; s[999] = 10.0 * sign[999]
     yield "nan_elsewhere", s
     s = np.full(v, np.nan, np.float32); s[0] = -3.0
     yield "all_nan_but_0", s
@@ -277,16 +276,18 @@ def _head_scale_cases(t):
     yield "inf_in_ragged_tail", s
 
 
-def test_head_greedy_keys_pick_matches_oracle():
+@pytest.mark.parametrize("vocab", [4099, 16387])
+def test_head_greedy_keys_pick_matches_oracle(vocab):
     """The LM head's GEMV stores a greedy key per 8-column tile and one workgroup reduces them:
     a generate's first id equals the oracle's strict > scan over the logits that the same
     forward leaves on the device, for crafted rows (ties across tiles, -0 beside +0, NaN at id 0
-    and elsewhere, all NaN, all -inf, +inf in a partial last tile of a 4099-id vocabulary). In
-    exact-products mode (no keys) the many-workgroup greedy kernel gives the oracle's id for
-    its own logits too."""
+    and elsewhere, all NaN, all -inf, +inf in a partial last tile of a ragged vocabulary). With
+    4099 ids the head is the one-workgroup-per-tile GEMV after a norm pass; with 16387 (2049
+    tiles) it is the one-wave-per-tile GEMV with the norm inside. In exact-products mode (no
+    keys) the many-workgroup greedy kernel gives the oracle's id for its own logits too."""
     from oracle_ctypes import oracle
 
-    cfg = dict(llama_config("tiny"), vocab=4099)
+    cfg = dict(llama_config("tiny"), vocab=vocab)
     w, q = llama_weights(cfg, 17)
     w = [(k, l, a) for (k, l, a) in w if k != 3]  # the head is uploaded per case below
     prompt = np.random.default_rng(3).integers(0, cfg["vocab"], size=9).astype(np.int32)
@@ -305,7 +306,7 @@ def test_head_greedy_keys_pick_matches_oracle():
             set_head(np.ones(cfg["vocab"], np.float32))
             t = eng.prefill_logits(prompt)[:8].copy()
             assert np.all(t != 0) and np.isfinite(t).all()
-            for name, scale in _head_scale_cases(t):
+            for name, scale in _head_scale_cases(t, cfg["vocab"]):
                 set_head(scale)
                 got = int(eng.generate(case)[0])
                 row = eng.prefill_logits(prompt)
