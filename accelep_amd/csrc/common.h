@@ -403,5 +403,11 @@ size_t GreedyWorkBytes(int64_t vocab);
 constexpr int64_t kGreedyKeysMax = 65536;
 void LaunchGreedyKeys(const uint64_t* keys, int64_t count, const float* logits, int32_t* chosen,
                       const int32_t* index_dev, hipStream_t stream);
+// LaunchGreedyKeys' pick, then the picked id's embedding row into `out` (hidden floats): the fp32
+// `table` [vocab, hidden], or with table null the int8 `qtable` times row_scale[id]
+// (LaunchEmbedding's row). One workgroup.
+void LaunchGreedyEmbed(const uint64_t* keys, int64_t count, const int32_t* index_dev, const int8_t* qtable,
+                       const float* row_scale, const float* table, const float* logits, int32_t* chosen, float* out,
+                       int64_t hidden, hipStream_t stream);
 
 }  // namespace accel_hip

@@ -126,6 +126,7 @@ struct Model {
   // replayed for every step after it. Dropped when a weight changes or the product mode does.
   void* decode_graph = nullptr;
   bool decode_graph_exact = false;
+  bool decode_graph_pick = false;  // decode_graph starts with the greedy pick (GreedyEmbedKernel)
   bool decode_warm = false;
   // Timing marks of the decode step (ACCEL_LLAMA_DECODE_MARKS=<layer>, read at each capture):
   // the captured step records the event slots of accel_hip_event_record around the embedding,
@@ -335,9 +336,13 @@ struct Model {
   // Forward over `seq` ids at ids[id_offset ..] (device int32) from position `filled`
   // (src/llama_model.cc:209-247). Leaves the last row's logits in `logits`.
   // With `state` (device int32 [position, produced], seq == 1) the position and the id index
-  // are read on the device, so the launches do not depend on the step. Returns whether the LM
-  // head advanced `state` (else the caller launches the advance).
-  bool Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids, int32_t* state = nullptr) {
+  // are read on the device, so the launches do not depend on the step. With `pick` as well,
+  // the step starts by picking the greedy id from the previous head's keys into
+  // ids[state[1]] and embedding it (one kernel, GreedyEmbedKernel) instead of embedding an id
+  // a sampler wrote there. Returns whether the LM head advanced `state` (else the caller
+  // launches the advance).
+  bool Forward(const int32_t* ids, int32_t seq, int64_t id_offset, bool check_ids, int32_t* state = nullptr,
+               bool pick = false) {
     if (ids == nullptr || seq <= 0 || filled < 0 || seq > cfg.context || filled > cfg.context - seq)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "forward exceeds context");
     const hipStream_t s = stream();
@@ -348,9 +353,14 @@ struct Model {
     Mark(kMarkNode1);
     Mark(kMarkStart);
     if (check_ids) Check(hipMemsetAsync(flag, 0, sizeof(int32_t), s), "hipMemsetAsync");
-    LaunchEmbedding(state != nullptr ? ids : ids + id_offset, embed_f.as<float>(), embed_q.as<int8_t>(),
-                    embed_scale.as<float>(), hidden.as<float>(), seq, H, cfg.vocab, flag, s,
-                    state != nullptr ? state + 1 : nullptr);
+    if (pick && state != nullptr && seq == 1)
+      LaunchGreedyEmbed(greedy_keys.as<uint64_t>(), (cfg.vocab + 7) / 8, state + 1, embed_q.as<int8_t>(),
+                        embed_scale.as<float>(), embed_f.as<float>(), logits.as<float>(), const_cast<int32_t*>(ids),
+                        hidden.as<float>(), H, s);
+    else
+      LaunchEmbedding(state != nullptr ? ids : ids + id_offset, embed_f.as<float>(), embed_q.as<int8_t>(),
+                      embed_scale.as<float>(), hidden.as<float>(), seq, H, cfg.vocab, flag, s,
+                      state != nullptr ? state + 1 : nullptr);
     Mark(kMarkEmbedded);
     if (check_ids) {
       int32_t bad = 0;
@@ -424,14 +434,15 @@ struct Model {
     return advanced;
   }
 
-  // One decode step: forward of chosen[produced] at `position`, then both advance. The
-  // first call runs it directly (staging the weights and sizing the workspaces), the second
-  // captures it into a graph, and later calls replay the graph.
-  void DecodeStep(int32_t* state) {
+  // One decode step: forward of chosen[produced] at `position` (with `pick`, chosen[produced]
+  // is first picked from the previous head's greedy keys), then both advance. The first call
+  // runs it directly (staging the weights and sizing the workspaces), the second captures it
+  // into a graph, and later calls replay the graph.
+  void DecodeStep(int32_t* state, bool pick = false) {
     const bool exact = Ctx().exact_products;
     decode_marks = MarksFromEnv();
-    if (decode_graph != nullptr &&
-        (decode_graph_exact != exact || graph_marks != decode_marks || !GraphIsCurrent(decode_graph)))
+    if (decode_graph != nullptr && (decode_graph_exact != exact || graph_marks != decode_marks ||
+                                    decode_graph_pick != pick || !GraphIsCurrent(decode_graph)))
       DropDecodeGraph();
     // ACCEL_LLAMA_EAGER=1 launches every step directly (a profiler then sees each dispatch).
     static const bool eager = [] {
@@ -439,14 +450,14 @@ struct Model {
       return v != nullptr && v[0] == '1';
     }();
     if (eager || (decode_graph == nullptr && !decode_warm)) {
-      if (!Forward(chosen.as<int32_t>(), 1, 0, false, state)) LaunchAdvance(state, stream());
+      if (!Forward(chosen.as<int32_t>(), 1, 0, false, state, pick)) LaunchAdvance(state, stream());
       decode_warm = true;
       return;
     }
     if (decode_graph == nullptr) {
       if (accel_hip_capture_begin() != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       try {
-        if (!Forward(chosen.as<int32_t>(), 1, 0, false, state)) {
+        if (!Forward(chosen.as<int32_t>(), 1, 0, false, state, pick)) {
           LaunchAdvance(state, stream());
           Mark(kMarkAdvance);
         }
@@ -458,6 +469,7 @@ struct Model {
       }
       if (accel_hip_capture_end(&decode_graph) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
       decode_graph_exact = exact;
+      decode_graph_pick = pick;
       graph_marks = decode_marks;
     }
     if (accel_hip_graph_launch(decode_graph, 1) != ACCEL_HIP_OK) Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
@@ -484,19 +496,29 @@ struct Model {
     Check(hipMemcpyAsync(state, state0, sizeof(state0), hipMemcpyHostToDevice, stream()), "hipMemcpyAsync");
     Check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
     int32_t produced = 0;
+    // Greedy with the head's keys and no id needed on the host between steps: each decode step
+    // starts by picking its id from the previous head's keys (GreedyEmbedKernel), so no sampler
+    // kernel runs between the steps. The picks and forwards run in the same order as with one.
+    const bool pick = !(temperature > 0.f) && head_keys && eos_id < 0 && on_token == nullptr;
     for (int32_t step = 0; step < max_new; ++step) {
       if (produced >= cfg.context) Fail(ACCEL_HIP_INVALID_ARGUMENT, "generation exceeded the token buffer");
       const bool mark_sample = decode_marks >= 0 && decode_graph != nullptr;  // steps that replay the marked graph
-      if (mark_sample && accel_hip_event_record(kMarkSampleStart) != ACCEL_HIP_OK)
-        Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
-      if (!(temperature > 0.f) && head_keys)
+      if (!pick) {
+        if (mark_sample && accel_hip_event_record(kMarkSampleStart) != ACCEL_HIP_OK)
+          Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+        if (!(temperature > 0.f) && head_keys)
+          LaunchGreedyKeys(greedy_keys.as<uint64_t>(), (cfg.vocab + 7) / 8, logits.as<float>(), chosen.as<int32_t>(),
+                           state + 1, stream());
+        else
+          LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
+                            state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
+        if (mark_sample && accel_hip_event_record(kMarkSampleEnd) != ACCEL_HIP_OK)
+          Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+      } else if (filled >= cfg.context) {
+        // The last id, with no forward after it.
         LaunchGreedyKeys(greedy_keys.as<uint64_t>(), (cfg.vocab + 7) / 8, logits.as<float>(), chosen.as<int32_t>(),
                          state + 1, stream());
-      else
-        LaunchSampleToken(logits.as<float>(), chosen.as<int32_t>(), cfg.vocab, temperature, rng, top_k, stream(),
-                          state + 1, greedy_work.as<uint32_t>(), greedy_work.buffer().bytes);
-      if (mark_sample && accel_hip_event_record(kMarkSampleEnd) != ACCEL_HIP_OK)
-        Fail(ACCEL_HIP_RUNTIME_ERROR, accel_hip_last_error());
+      }
       produced += 1;
       if (eos_id >= 0 || on_token != nullptr) {
         // Only an eos id or a token callback needs the chosen id on the host before the next
@@ -509,7 +531,7 @@ struct Model {
         if (id == eos_id) break;
       }
       if (filled >= cfg.context) break;
-      DecodeStep(state);
+      DecodeStep(state, pick);
       NoteForward();
       filled += 1;
     }

@@ -401,7 +401,75 @@ __global__ __launch_bounds__(kKeysThreads) void GreedyKeysKernel(const uint64_t*
   }
 }
 
+// GreedyKeysKernel's pick followed by the embedding of the picked id (EmbeddingKernel's row:
+// the fp32 table row, or fl(float(q) * row_scale[id]) of the int8 table), in one workgroup:
+// the first kernel of a decode step whose previous step left its greedy keys. The id goes to
+// chosen[*index_dev] as the sampler would write it, and the row to `out`.
+__global__ __launch_bounds__(kKeysThreads) void GreedyEmbedKernel(const uint64_t* keys, int32_t count,
+                                                                  const int32_t* index_dev, const int8_t* qtable,
+                                                                  const float* row_scale, const float* table,
+                                                                  const float* logits, int32_t* chosen, float* out,
+                                                                  int32_t hidden) {
+  __shared__ uint64_t sk[kKeysThreads / 64];
+  __shared__ int32_t picked;
+  const int tid = threadIdx.x;
+  int32_t index = 0;
+  float first = 0.f;
+  if (tid == 0) {
+    index = *index_dev;
+    first = logits[0];
+  }
+  uint64_t best = 0;
+  for (int i0 = 0; i0 < count; i0 += kKeysBatch * kKeysThreads) {
+    uint64_t v[kKeysBatch];
+#pragma unroll
+    for (int u = 0; u < kKeysBatch; ++u) {
+      const int i = i0 + u * kKeysThreads + tid;
+      v[u] = i < count ? keys[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kKeysBatch; ++u) best = max(best, v[u]);
+  }
+  best = max(best, XorLane<32>(best));
+  best = max(best, XorLane<16>(best));
+  best = max(best, XorLane<8>(best));
+  best = max(best, XorLane<4>(best));
+  best = max(best, XorLane<2>(best));
+  best = max(best, XorLane<1>(best));
+  if ((tid & 63) == 0) sk[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t k = sk[0];
+    for (int w = 1; w < kKeysThreads / 64; ++w) k = max(k, sk[w]);
+    const int32_t id = (k == 0 || isnan(first)) ? 0 : static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k));
+    chosen[index] = id;
+    picked = id;
+  }
+  __syncthreads();
+  const int64_t id = picked;
+  if (table != nullptr) {
+    const float* src = table + id * hidden;
+    for (int i = tid; i < hidden; i += kKeysThreads) out[i] = src[i];
+  } else {
+    const int8_t* src = qtable + id * hidden;
+    const float sc = row_scale[id];
+    for (int i = tid; i < hidden; i += kKeysThreads) out[i] = __fmul_rn(static_cast<float>(src[i]), sc);
+  }
+}
+
 }  // namespace
+
+void LaunchGreedyEmbed(const uint64_t* keys, int64_t count, const int32_t* index_dev, const int8_t* qtable,
+                       const float* row_scale, const float* table, const float* logits, int32_t* chosen, float* out,
+                       int64_t hidden, hipStream_t stream) {
+  if (keys == nullptr || logits == nullptr || chosen == nullptr || index_dev == nullptr || out == nullptr ||
+      count < 1 || count > kGreedyKeysMax || hidden < 1 || hidden > 0x7fffffff ||
+      (table == nullptr && (qtable == nullptr || row_scale == nullptr)))
+    Fail(ACCEL_HIP_INVALID_ARGUMENT, "greedy embed: need 1 .. 65536 keys, the index, a table and the output row");
+  hipLaunchKernelGGL(GreedyEmbedKernel, dim3(1), dim3(kKeysThreads), 0, stream, keys, static_cast<int32_t>(count),
+                     index_dev, qtable, row_scale, table, logits, chosen, out, static_cast<int32_t>(hidden));
+  Check(hipGetLastError(), "GreedyEmbedKernel launch");
+}
 
 void LaunchGreedyKeys(const uint64_t* keys, int64_t count, const float* logits, int32_t* chosen,
                       const int32_t* index_dev, hipStream_t stream) {

@@ -296,12 +296,12 @@ def llama_q8_weights(cfg, rng):
             yield kind, layer, q, sc
 
 
-# Kernels of one graph-replayed decode token: per layer the q/k/v GEMV, the split attention,
-# the o, gate/up and down GEMVs; then the embedding, the final RMSNorm and the LM head (which
-# also stores the greedy keys and advances the position) in the graph, and the greedy pick
-# from the keys launched between replays.
+# Kernels of one graph-replayed decode token: the greedy pick from the previous head's keys with
+# the embedding of the picked id; per layer the q/k/v GEMV, the split attention, the o, gate/up
+# and down GEMVs; then the LM head (its RMSNorm inside, storing the greedy keys and advancing
+# the position). Nothing runs between replays.
 def decode_kernels_per_token(cfg):
-    return 5 * cfg["layers"] + 4
+    return 5 * cfg["layers"] + 2
 
 
 def graph_node_floor_us(hip, nodes, reps=20):
@@ -404,9 +404,10 @@ MARKS = ("start", "embedded", "layer", "qkv", "attention", "o", "gate_up", "down
 def decode_marks(hip, layers, rng, reps=3):
     """Times the parts of one graph-replayed decode token from event nodes inside the captured
     step (ACCEL_LLAMA_DECODE_MARKS=<layer>; the last step of a 512-id prompt and 128 tokens,
-    position 639): the sampler, the host's launch of the graph, the embedding, the given layers' five
-    kernels each, all 30 layers, and the LM head (one kernel: its norm, product, greedy keys and
-    the position advance).
+    position 639): the greedy pick from the previous head's keys with the embedding (one kernel),
+    the given layers' five kernels each, all 30 layers, and the LM head (one kernel: its norm,
+    product, greedy keys and the position advance). The marks cover the graph from its first node;
+    the host's launch of the graph between tokens is in the unmarked token only.
     Every mark is an event node of the graph, which takes about as long as a dependent kernel:
     each span holds the node that ends it, and two marks back to back at the start of the step
     time one node on its own (event_node_us). The unmarked token (decode_us_per_token_unmarked)
@@ -432,13 +433,12 @@ def decode_marks(hip, layers, rng, reps=3):
             for _ in range(reps):
                 model.generate(128)  # 128 tokens: the last one's sampler runs before the last graph replay
                 parts = {
-                    "sampler (GreedyKeysKernel)": span("sample_start", "sample_end"),
-                    "graph launch (host) and start": span("sample_end", "start"),
-                    "embedding": span("start", "embedded"),
+                    "graph start (3 event nodes)": span("node0", "start"),
+                    "greedy pick and embedding (GreedyEmbedKernel)": span("start", "embedded"),
                     "layers 0-29": span("embedded", "layers"),
                     "LM head (RMSNorm, GEMV 576 x 49152, greedy keys, advance)": span("layers", "head"),
                 }
-                total = span("sample_start", "head")
+                total = span("node0", "head")
                 node = span("node0", "node1")
                 layer_parts = {
                     "q/k/v GEMV (RMSNorm prologue)": span("layer", "qkv"),

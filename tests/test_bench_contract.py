@@ -29,10 +29,9 @@ def test_bad_step_counts_are_refused():
 
 
 def test_decode_kernel_count_matches_the_step_graph():
-    # Per layer: q/k/v GEMV, split attention, o, gate/up and down GEMVs; then embedding, final
-    # RMSNorm, the LM head (greedy keys and the advance in the same kernel), and the greedy pick
-    # from the keys between replays.
-    assert bench.decode_kernels_per_token(bench.SMOL) == 5 * 30 + 4 == 154
+    # The greedy pick with the embedding; per layer q/k/v GEMV, split attention, o, gate/up and
+    # down GEMVs; then the LM head (its norm, the greedy keys and the advance in the same kernel).
+    assert bench.decode_kernels_per_token(bench.SMOL) == 5 * 30 + 2 == 152
 
 
 def test_decode_roofline_bytes_follow_the_model_shape():

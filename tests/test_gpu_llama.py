@@ -316,3 +316,24 @@ def test_head_greedy_keys_pick_matches_oracle(vocab):
     finally:
         check(eng.L.accel_hip_set_exact_products(0))
         eng.close()
+
+
+def test_greedy_pick_in_step_matches_sampler_path():
+    """A greedy generate with no eos id and no callback picks each id inside the next decode
+    step (GreedyEmbedKernel); with an eos id that never occurs the sampler runs between the
+    steps and the host reads each id. Both must give the same ids and count, here through the
+    end of the context (48 positions: 40 prompt ids, 8 decode steps, a ninth id with no forward
+    after it), and the reference's ids on the golden greedy case."""
+    cfg = llama_config("tiny")
+    w, q = llama_weights(cfg, 101)
+    prompt = np.random.default_rng(9).integers(0, cfg["vocab"], size=40).astype(np.int32)
+    eng = Engine(cfg, w, q)
+    try:
+        base = dict(prompt=prompt, max_new=12, temperature=0.0, seed=0, top_k=0)
+        in_step = eng.generate(dict(base, eos=-1))
+        sampler = eng.generate(dict(base, eos=cfg["vocab"] + 5))
+        print(f"in-step {in_step.tolist()} sampler {sampler.tolist()}", flush=True)
+        assert in_step.size == 9
+        np.testing.assert_array_equal(in_step, sampler)
+    finally:
+        eng.close()
