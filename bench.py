@@ -95,11 +95,19 @@ class Hip:
             self.check(self.L.accel_hip_capture_end(C.byref(g)))
         return g
 
+    def elapsed(self):
+        ms = self.L.accel_hip_event_elapsed_ms(0, 1)
+        if ms < 0:
+            raise RuntimeError(self.L.accel_hip_last_error().decode())
+        return ms
+
     def time_in_graph(self, step, lead_len, steps):
         """Times `steps` calls of step(i) between two event records captured in one graph after
         `lead_len` untimed calls (whole weight rotations): the graph's launch and the lead-in
-        fall before the start event. Replayed once untimed (the first replay uploads it), then
-        once timed. Returns elapsed ms."""
+        fall before the start event. The first replay uploads the graph and sizes the clock
+        warm-up; then the graph is replayed back to back for at least CLOCK_WARM_MS of GPU time
+        and the last replay's event pair, which holds exactly `steps` steps, is the result.
+        Returns elapsed ms."""
         self.check(self.L.accel_hip_capture_begin())
         try:
             for i in range(lead_len):
@@ -113,23 +121,23 @@ class Hip:
             self.check(self.L.accel_hip_capture_end(C.byref(g)))
         try:
             self.check(self.L.accel_hip_graph_launch(g, 1))
-            self.sync()
-            self.check(self.L.accel_hip_graph_launch(g, 1))
-            ms = self.L.accel_hip_event_elapsed_ms(0, 1)
-            if ms < 0:
-                raise RuntimeError(self.L.accel_hip_last_error().decode())
-            return ms
+            replay_ms = self.elapsed() * (lead_len + steps) / steps
+            self.check(self.L.accel_hip_graph_launch(g, warm_replays(replay_ms) + 1))
+            return self.elapsed()
         finally:
             self.L.accel_hip_graph_destroy(g)
 
-    def time_graph(self, graphs_and_reps, lead=None):
+    def time_graph(self, graphs_and_reps, lead=None, warm=None):
         """Event-timed replay: list of (graph, reps); returns elapsed ms.
 
         `lead`, a graph replayed once (untimed) just before the start event, keeps the GPU busy
         while the host submits the start event, the timed graphs and the end event: the timed
         interval then holds the steps and not the host's submission latency (about 12 us,
-        which over 20 steps of a 10.5 us GEMV would read as 0.6 us a step)."""
+        which over 20 steps of a 10.5 us GEMV would read as 0.6 us a step). `warm`, a (graph,
+        reps) pair replayed untimed before the lead, brings the clocks to their steady state."""
         self.sync()
+        if warm is not None:
+            self.check(self.L.accel_hip_graph_launch(warm[0], warm[1]))
         if lead is not None:
             self.check(self.L.accel_hip_graph_launch(lead, 1))
         self.check(self.L.accel_hip_event_record(0))
@@ -145,6 +153,16 @@ class Hip:
 
 GRAPHS = True  # --no-graph: launch every step directly (profiler counter runs see each dispatch)
 LEAD_STEPS = 4  # untimed steps replayed right before the start event (rounded up to whole rotations)
+# Untimed GPU work replayed back to back right before a timed replay. From idle, the first
+# milliseconds of a memory-bound stream run slow: the m = 1 GEMV's first replay of 400 steps read
+# 10.4-10.6 us a step where later ones read 10.2 (one box, same graph), and a lone replay of 20
+# steps after the short warm-up ran slower still. 50 ms of the same steps takes that out.
+CLOCK_WARM_MS = 50.0
+
+
+def warm_replays(replay_ms):
+    """Replays of a graph of `replay_ms` that cover CLOCK_WARM_MS (at most 20000)."""
+    return int(min(20000, max(1, -(-CLOCK_WARM_MS // max(replay_ms, 1e-3)))))
 
 
 def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
@@ -159,11 +177,13 @@ def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
     cache.
     - Up to 400 steps: one graph holds the lead-in, the start event record, exactly `steps`
       steps and the end event record (records inside a capture become timeable event nodes),
-      replayed once untimed (its first replay uploads it) and once timed. Neither the host's
-      submission nor the graph's launch on the GPU (about 5 us) falls inside the interval.
+      replayed once untimed (its first replay uploads it), then back to back for the clock
+      warm-up (CLOCK_WARM_MS), the last replay timed. Neither the host's submission nor the
+      graph's launch on the GPU (about 5 us) falls inside the interval.
     - More steps: graphs of `period` nodes (a whole number of rotations) plus one for the
-      rest, each replayed once untimed; then the lead-in graph and the timed replays back to
-      back between two events on the stream (one graph launch per `period` steps stays in)."""
+      rest, each replayed once untimed; then the first of them for the clock warm-up, the
+      lead-in graph and the timed replays back to back between two events on the stream (one
+      graph launch per `period` steps stays in)."""
     for i in range(max(warmup, rotation, 1)):
         step(i)
     hip.sync()
@@ -189,7 +209,8 @@ def timed_steps(hip, step, steps, warmup, period=200, rotation=1):
     try:
         for g in graphs:  # the first replay of a graph uploads it
             hip.check(hip.L.accel_hip_graph_launch(g, 1))
-        return hip.time_graph(plan, lead=lead)
+        period_ms = hip.time_graph([(plan[0][0], 1)])
+        return hip.time_graph(plan, lead=lead, warm=(plan[0][0], warm_replays(period_ms)))
     finally:
         for g in graphs:
             hip.L.accel_hip_graph_destroy(g)
