@@ -133,7 +133,7 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
     if (ctx.exact_products) {
       LaunchExactMatmul(a_f, q8 ? nullptr : b_f, q8 ? view : Q8View{}, c, m, k, n, main, ctx.stream);
     } else if (q8 && m <= 16) {
-      if (GemvWantsGroups(m, k, view)) view.grouped = StagedGroupTiles(view.q, k, n, ctx.stream, stage_weights);
+      if (GemvWantsGroups(m, k, n, view)) view.grouped = StagedGroupTiles(view.q, k, n, ctx.stream, stage_weights);
       else if (m <= 4) view.tiled = StagedColumnTiles(view.q, k, n, ctx.stream, stage_weights);
       LaunchGemvQ8(a_f, view, c, m, k, n, main, ctx.stream);
     } else {

@@ -202,13 +202,13 @@ bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v);
 // Whether a weight of this form can have the staged bf16 copy at all (GemmWantsBf16Image
 // without the grid condition on m).
 bool GemmBf16Stageable(int64_t k, int64_t n, const Q8View& v);
-// Whether LaunchGemvQ8 takes an m-row product with this k and weight view from the
-// group-interleaved copy (the caller stages that copy instead of the 8-column tiles).
+// Whether LaunchGemvQ8 takes an m-row product with this k, n and weight view from the
+// group-interleaved copy (the caller stages that copy instead of the 8-column tiles): 3 <= m
+// <= 16, whole 32-row blocks, no zero points or per-row scale, and for m <= 4 a product large
+// enough to give every CU a workgroup of the split-bf16 kernel (a smaller one runs on the
+// narrow kernel's tiles, one workgroup per tile and no K-split exchange).
 constexpr int64_t kGemvGroupMinM = 3;
-inline bool GemvWantsGroups(int64_t m, int64_t k, const Q8View& v) {
-  return m >= kGemvGroupMinM && m <= 16 && k % kGemvGroupRows == 0 && v.zero == nullptr &&
-         (v.mode == kScalePerCol || v.mode == kScaleConst);
-}
+bool GemvWantsGroups(int64_t m, int64_t k, int64_t n, const Q8View& v);
 
 struct Epilogue {
   float alpha = 1.f;

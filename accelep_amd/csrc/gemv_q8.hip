@@ -1258,7 +1258,34 @@ void LaunchNarrow(const GemvArgs& args, dim3 grid, bool zero, bool row_scale, bo
   }
 }
 
+// The split-bf16 kernel's grid for a k x n product (k a multiple of the 32-row block): column
+// groups of 128 and K splits, about 1.75 workgroups per CU (4 splits for 4096 x 14336, measured
+// best there; twice the splits costs more in partial sums and arrivals than it gains in
+// parallelism), each split at least one batch of every wave.
+void SplitBf16Grid(int64_t k, int64_t n, int64_t cus, int64_t* groups, int64_t* splits) {
+  const int64_t target = 7 * cus / 4;
+  const int64_t tiles = (n + kNarrowTile - 1) / kNarrowTile;
+  *groups = (tiles + kSplitTiles - 1) / kSplitTiles;
+  const int64_t blocks = k / kSplitBlockRows;
+  *splits = std::max<int64_t>(1, std::min<int64_t>((target + *groups - 1) / *groups, blocks / (kSplitWaves * kSplitBatch)));
+}
+
+int64_t CuCount() {
+  const Context& ctx = Ctx();
+  return ctx.cu_count > 0 ? ctx.cu_count : 256;
+}
+
 }  // namespace
+
+bool GemvWantsGroups(int64_t m, int64_t k, int64_t n, const Q8View& v) {
+  if (m < kGemvGroupMinM || m > 16 || k % kGemvGroupRows != 0 || v.zero != nullptr ||
+      (v.mode != kScalePerCol && v.mode != kScaleConst))
+    return false;
+  if (m > 4) return true;  // the narrow kernel takes m <= 4 only
+  int64_t groups = 0, splits = 0;
+  SplitBf16Grid(k, n, CuCount(), &groups, &splits);
+  return groups * splits >= CuCount();
+}
 
 bool GemvWaveTileApplies(int64_t m, int64_t k, int64_t n) {
   const Context& ctx = Ctx();
@@ -1303,12 +1330,9 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   int64_t splits = 1;
   int64_t rows = k;
   if (split_bf16) {
-    // About 1.75 workgroups per CU: K split into 4 for 4096 x 14336 (measured best there;
-    // twice the splits costs more in partial sums and arrivals than it gains in parallelism).
-    const int64_t target = 7 * cus / 4;
-    const int64_t groups = (tiles + kSplitTiles - 1) / kSplitTiles;
+    int64_t groups = 0;
+    SplitBf16Grid(k, n, cus, &groups, &splits);
     const int64_t blocks = k / kSplitBlockRows;
-    splits = std::max<int64_t>(1, std::min<int64_t>((target + groups - 1) / groups, blocks / (kSplitWaves * kSplitBatch)));
     rows = (blocks + splits - 1) / splits * kSplitBlockRows;
   } else if (narrow) {
     // One workgroup per tile over all of K, unless the tiles leave the CUs short of work on a

@@ -222,7 +222,7 @@ struct Model {
       if (ctx.exact_products) {
         LaunchExactMatmul(a, nullptr, v, c, m, w.in, w.out, e, ctx.stream);
       } else if (m <= 16) {
-        if (GemvWantsGroups(m, w.in, v)) v.grouped = StagedGroupTiles(v.q, w.in, w.out, ctx.stream);
+        if (GemvWantsGroups(m, w.in, w.out, v)) v.grouped = StagedGroupTiles(v.q, w.in, w.out, ctx.stream);
         else if (m <= 4) v.tiled = StagedColumnTiles(v.q, w.in, w.out, ctx.stream);
         LaunchGemvQ8(a, v, c, m, w.in, w.out, e, ctx.stream);
       } else {
