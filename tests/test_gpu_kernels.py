@@ -252,9 +252,12 @@ def test_gemv_unaligned_a(m):
     assert_plugin_tolerance(c.numpy(), case["a"], dequant_host(case["bq"], k, n))
 
 
-# ---- split-bf16 MFMA GEMV: 1 < m <= 16, no zero points, k a multiple of 32 --------------------
+# ---- split-bf16 MFMA GEMV: 2 < m <= 16, no zero points, k a multiple of 32 --------------------
 # Each activation enters three bf16 MFMAs as hi + mid + lo (exact), each weight byte as an
-# exact bf16; only the fp32 accumulation rounds.
+# exact bf16; only the fp32 accumulation rounds. A product with m <= 4 too small to give every
+# CU a workgroup of that kernel (GemvWantsGroups) runs on the narrow kernel's 8-column tiles
+# instead, so the m <= 4 cases of small shapes below check that route, and each has a twin
+# with m = 5 or 6 on the split-bf16 kernel.
 
 def _split_case(m, k, n, seed, whole_scale=False, a=None, q=None):
     r = np.random.default_rng(seed)
@@ -268,8 +271,9 @@ def _split_case(m, k, n, seed, whole_scale=False, a=None, q=None):
 
 
 @pytest.mark.parametrize("m,k,n,whole", [
-    (2, 32, 8, False), (3, 64, 1001, False), (5, 576, 1536, False), (8, 1024, 77, True), (4, 96, 14336, False),
-    (13, 4096, 264, False), (16, 8192, 130, False), (16, 12288, 2048, True)])
+    (2, 32, 8, False), (3, 64, 1001, False), (6, 64, 1001, False), (5, 576, 1536, False), (8, 1024, 77, True),
+    (4, 96, 14336, False), (5, 96, 14336, False), (13, 4096, 264, False), (16, 8192, 130, False),
+    (16, 12288, 2048, True)])
 def test_gemv_split_bf16_bound(m, k, n, whole):
     """Ragged n (tiles past the end of the last 16-tile group), one block, split K, a
     whole-tensor scale: within 2 gamma_K of the float64 product, and for k <= 1024 also the
@@ -282,7 +286,7 @@ def test_gemv_split_bf16_bound(m, k, n, whole):
         assert_plugin_tolerance(got, case["a"], w)
 
 
-@pytest.mark.parametrize("m,k,n", [(4, 576, 1536), (16, 1024, 264), (7, 4096, 136)])
+@pytest.mark.parametrize("m,k,n", [(4, 576, 1536), (5, 576, 1536), (16, 1024, 264), (7, 4096, 136)])
 def test_gemv_split_bf16_integer_sums_exact(m, k, n):
     """Integer A with |a| <= 16: every partial sum is an integer below 2^24, so any order of
     summation gives the exact sum S and C = fl(S * scale) bit for bit. A row, column or k
@@ -296,7 +300,7 @@ def test_gemv_split_bf16_integer_sums_exact(m, k, n):
     same_bits(got, (s.astype(np.float32) * case["bq"]["scale"][None, :]).astype(np.float32))
 
 
-@pytest.mark.parametrize("m,k,n", [(16, 4096, 1001), (3, 96, 64), (9, 1024, 520)])
+@pytest.mark.parametrize("m,k,n", [(16, 4096, 1001), (3, 96, 64), (6, 96, 64), (9, 1024, 520)])
 def test_gemv_split_bf16_full_precision_a(m, k, n):
     """One nonzero weight per column, a power of two: C = fl(a * w * scale) exactly, which
     needs all 24 significand bits of every activation (N(0, 1) values) to reach the sum;
