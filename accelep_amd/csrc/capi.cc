@@ -138,6 +138,7 @@ void RunMatmul(const float* a, const AccelHipQuantPlane* aq, const float* b, con
       LaunchGemvQ8(a_f, view, c, m, k, n, main, ctx.stream);
     } else {
       if (q8 && GemmWantsBf16Image(m, k, n, view)) view.bf16 = StagedBf16Image(view.q, k, n, ctx.stream, stage_weights);
+      else if (q8 && GemmWantsSmall(m, k, n, view)) view.bf16x16 = StagedBf16x16(view.q, k, n, ctx.stream, stage_weights);
       RmsRequest rms;
       rms.weight = epi.rms_weight;
       rms.eps = epi.rms_eps;
@@ -245,15 +246,20 @@ ACCEL_HIP_API int accel_hip_prepare_quantized(const AccelHipQuantPlane* b_quant,
     const bool groups_ok = k % kGemvGroupRows == 0 && view.zero == nullptr &&
                            (view.mode == kScalePerCol || view.mode == kScaleConst);
     const bool bf16_ok = GemmBf16Stageable(k, n, view);
+    const bool small_ok = GemmSmallStageable(k, n, view);
     const uint32_t want = layouts != 0 ? layouts
                                        : ACCEL_HIP_STAGE_GEMV_TILES | (groups_ok ? ACCEL_HIP_STAGE_GEMV_GROUPS : 0u) |
-                                             (bf16_ok ? ACCEL_HIP_STAGE_GEMM_BF16 : 0u);
+                                             (bf16_ok ? ACCEL_HIP_STAGE_GEMM_BF16 : 0u) |
+                                             (small_ok ? ACCEL_HIP_STAGE_GEMM_SMALL : 0u);
     if ((want & ACCEL_HIP_STAGE_GEMV_GROUPS) != 0 && !groups_ok)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the group-interleaved copy needs k % 32 == 0, no zero points and a "
                                        "per-column or whole-tensor scale");
     if ((want & ACCEL_HIP_STAGE_GEMM_BF16) != 0 && !bf16_ok)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the bf16 copy needs k % 32 == 0, k >= 64, n % 8 == 0, no zero points "
                                        "and a per-column or whole-tensor scale");
+    if ((want & ACCEL_HIP_STAGE_GEMM_SMALL) != 0 && !small_ok)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the small GEMM's bf16 copy needs k % 32 == 0, k <= 768, n % 8 == 0, "
+                                       "no zero points and a per-column or whole-tensor scale");
     const hipStream_t s = Ctx().stream;
     const auto built = [](const void* p) {
       if (p == nullptr) Fail(ACCEL_HIP_INVALID_ARGUMENT, "prepare: the weight is not inside a live allocation of this library");
@@ -270,6 +276,10 @@ ACCEL_HIP_API int accel_hip_prepare_quantized(const AccelHipQuantPlane* b_quant,
     if ((want & ACCEL_HIP_STAGE_GEMM_BF16) != 0) {
       built(StagedBf16Image(view.q, k, n, s));
       done |= ACCEL_HIP_STAGE_GEMM_BF16;
+    }
+    if ((want & ACCEL_HIP_STAGE_GEMM_SMALL) != 0) {
+      built(StagedBf16x16(view.q, k, n, s));
+      done |= ACCEL_HIP_STAGE_GEMM_SMALL;
     }
     if (staged != nullptr) *staged = done;
   });

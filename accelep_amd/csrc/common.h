@@ -122,6 +122,7 @@ struct Q8View {
   const int8_t* tiled = nullptr;  // staged column-tiled copy of q (kGemvTileCols wide), or nullptr
   const int8_t* grouped = nullptr;  // staged group-interleaved copy of q, or nullptr
   const void* bf16 = nullptr;       // staged bf16 copy in the GEMM's MFMA operand order, or nullptr
+  const void* bf16x16 = nullptr;    // staged bf16 copy in the small GEMM's operand order, or nullptr
   // Load policy of the one-row GEMV: false streams the weight (nontemporal loads, the right
   // choice for weights read once per pass over more than the 256 MB last-level cache); true
   // uses plain loads, for a caller whose whole working set stays cached between passes.
@@ -197,8 +198,23 @@ inline size_t StagedF32PartsBytes(int64_t k, int64_t n) {
 const void* StagedF32Parts(const float* b, int64_t k, int64_t n, hipStream_t stream, bool create);
 void LaunchStageF32Parts(const float* b, int64_t k, int64_t n, void* dst, hipStream_t stream);
 void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream);
+// bf16 copy of a [k, n] int8 matrix (k % 32 == 0) in the operand order of
+// v_mfma_f32_16x16x32_bf16's B operand, for the small int8-weight GEMM: 16-column block cb
+// (columns past n zero) and 32-row block kb form 1 KB at (cb * k/32 + kb) * 1024 bytes, 16 bytes
+// per lane l = the 8 values W[32kb + 8(l / 16) + j][16cb + l % 16], j = 0..7, each float(q)
+// exactly (j even in the low half of a word).
+inline size_t StagedBf16x16Bytes(int64_t k, int64_t n) {
+  return static_cast<size_t>((n + 15) / 16) * static_cast<size_t>(k / 32) * 1024;
+}
+const void* StagedBf16x16(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create = true);
+void LaunchTileBf16x16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream);
 // Whether the int8-weight GEMM runs this product from a staged bf16 copy (the caller stages it).
 bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v);
+// Whether a weight of this form can have the small GEMM's bf16 copy at all (k <= 768).
+bool GemmSmallStageable(int64_t k, int64_t n, const Q8View& v);
+// Whether the int8-weight GEMM runs this m-row product (m > 16) on the small kernel from its
+// bf16 copy (the caller stages it): a short k and a grid too small for the 128-tile image path.
+bool GemmWantsSmall(int64_t m, int64_t k, int64_t n, const Q8View& v);
 // Whether a weight of this form can have the staged bf16 copy at all (GemmWantsBf16Image
 // without the grid condition on m).
 bool GemmBf16Stageable(int64_t k, int64_t n, const Q8View& v);

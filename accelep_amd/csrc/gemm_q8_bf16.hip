@@ -38,6 +38,7 @@ namespace accel_hip {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -783,6 +784,144 @@ __global__ void RmsScaleKernel(const float* c, const double* __restrict__ row_ss
   }
 }
 
+// ---- small products: 16-row blocks over all of a short k, no LDS round trip per chunk ------
+// An m > 16 product whose 128-tile grid leaves CUs idle and whose k is short (k <= 768: the
+// Llama prompt's q/k/v, o and gate/up at 512 rows) spends its time in GemmQ8Bf16Kernel's
+// per-chunk chain of LDS stores, barrier and LDS reads, and in a split-K reduce launch. Here a
+// workgroup of kSmallWaves waves owns one 16-row block and kSmallWaves 16-column blocks over
+// all of k (no K split):
+//  * the block's 16 activation rows are split once into hi/mid/lo bf16 planes in LDS, in the
+//    A-operand order of v_mfma_f32_16x16x32_bf16 (piece (kb, part, lane) at (kb * 3 + part) *
+//    64 + lane: row 16 rb + lane % 16, k = 32 kb + 8 (lane / 16) .. + 7), one barrier;
+//  * each wave reads its column block's B operands straight from the staged copy
+//    (StagedBf16x16), one 16-byte load per lane and 32 x 16 block, kSmallStages blocks in flight;
+//  * three MFMAs per block, hi into one accumulator and mid + lo into another, added at the end,
+//    as in the kernels above: exact products, only the fp32 accumulation rounds. The column
+//    scale and the epilogue apply at the store.
+constexpr int kSmallWaves = 8;
+constexpr int kSmallThreads = kSmallWaves * 64;
+constexpr int kSmallStages = 6;
+constexpr int64_t kSmallMaxK = 768;
+constexpr int kSmallMaxBlocks = static_cast<int>(kSmallMaxK / kBK);
+
+struct SmallArgs {
+  const float* a;
+  const u32x4* w16;  // StagedBf16x16 layout
+  const float* scale;
+  int32_t mode;
+  int64_t const_index;
+  float* c;
+  int32_t m, k, n;     // k % 32 == 0, 32 <= k <= kSmallMaxK
+  int32_t col_groups;  // workgroups along n: ceil(ceil(n / 16) / kSmallWaves)
+  Epilogue epi;
+};
+
+// One thread per 16-byte lane piece of the staged copy (layout: StagedBf16x16Bytes).
+__global__ void TileBf16x16Kernel(const int8_t* __restrict__ q, int64_t k, int64_t n, u32x4* __restrict__ out,
+                                  int64_t kbs, int64_t items) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= items) return;
+  const int lane = static_cast<int>(t & 63);
+  const int64_t blk = t >> 6;
+  const int64_t cb = blk / kbs;
+  const int64_t kb = blk - cb * kbs;
+  const int64_t col = cb * 16 + (lane & 15);
+  const int64_t k0 = kb * 32 + 8 * (lane >> 4);
+  uint32_t w[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const float q0 = col < n ? static_cast<float>(q[(k0 + 2 * h) * n + col]) : 0.f;
+    const float q1 = col < n ? static_cast<float>(q[(k0 + 2 * h + 1) * n + col]) : 0.f;
+    w[h] = PackBf16(q0, q1);
+  }
+  out[t] = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// kKbs: k / 32 fixed at compile time (every loop unrolled, constant LDS offsets), or 0 for any k.
+template <int kKbs>
+__global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(SmallArgs p) {
+  static_assert(kKbs >= 0 && kKbs <= kSmallMaxBlocks, "k blocks");
+  __shared__ u32x4 parts[(kKbs > 0 ? kKbs : kSmallMaxBlocks) * 3 * 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int kbs = kKbs > 0 ? kKbs : p.k / kBK;
+  const int cbs = (p.n + 15) / 16;
+  const int rb = static_cast<int>(blockIdx.x) / p.col_groups;
+  const int cb = (static_cast<int>(blockIdx.x) % p.col_groups) * kSmallWaves + wave;
+  const int cbc = cb < cbs ? cb : cbs - 1;  // a wave past the last block loads a valid one, stores nothing
+  const u32x4* wp = p.w16 + static_cast<int64_t>(cbc) * kbs * 64 + lane;
+  // The first kSmallStages blocks of W are requested before the split, which they do not need.
+  u32x4 rw[kSmallStages];
+#pragma unroll
+  for (int i = 0; i < kSmallStages; ++i) {
+    rw[i] = wp[static_cast<int64_t>(i < kbs ? i : kbs - 1) * 64];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int pc = tid; pc < kbs * 64; pc += kSmallThreads) {
+    const int kb = pc >> 6;
+    const int l = pc & 63;
+    const int row = rb * 16 + (l & 15);
+    float x[8];
+    if (row < p.m) {
+      const float4* src = reinterpret_cast<const float4*>(p.a + static_cast<int64_t>(row) * p.k + kb * kBK + 8 * (l >> 4));
+      const float4 x0 = src[0], x1 = src[1];
+      x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+      x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = 0.f;
+    }
+    u32x4 hi, mid, lo;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      uint32_t ph, pm, pl;
+      SplitBf16Pair(x[2 * h], x[2 * h + 1], ph, pm, pl);
+      hi[h] = ph;
+      mid[h] = pm;
+      lo[h] = pl;
+    }
+    parts[(kb * 3 + 0) * 64 + l] = hi;
+    parts[(kb * 3 + 1) * 64 + l] = mid;
+    parts[(kb * 3 + 2) * 64 + l] = lo;
+  }
+  // An LDS-only barrier: the W blocks in flight stay in flight.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  v4f acc_hi = v4f{0.f, 0.f, 0.f, 0.f};
+  v4f acc_ml = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int kb0 = 0; kb0 < kbs; kb0 += kSmallStages) {
+#pragma unroll
+    for (int st = 0; st < kSmallStages; ++st) {
+      const int kb = kb0 + st;
+      if (kb >= kbs) break;  // uniform
+      const u32x4 a0 = parts[(kb * 3 + 0) * 64 + lane];
+      const u32x4 a1 = parts[(kb * 3 + 1) * 64 + lane];
+      const u32x4 a2 = parts[(kb * 3 + 2) * 64 + lane];
+      acc_hi = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, rw[st]),
+                                                       acc_hi, 0, 0, 0);
+      acc_ml = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, rw[st]),
+                                                       acc_ml, 0, 0, 0);
+      acc_ml = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a2), __builtin_bit_cast(bf16x8, rw[st]),
+                                                       acc_ml, 0, 0, 0);
+      if (kb + kSmallStages < kbs) rw[st] = wp[static_cast<int64_t>(kb + kSmallStages) * 64];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (cb >= cbs) return;
+  // Element r of the 16 x 16 tile: row 16 rb + 4 (lane / 16) + r, column 16 cb + lane % 16.
+  const int col = cb * 16 + (lane & 15);
+  if (col >= p.n) return;
+  const float cs = p.scale[p.mode == kScalePerCol ? col : p.const_index];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = rb * 16 + 4 * (lane >> 4) + r;
+    if (row < p.m)
+      StoreC(p.c, row, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(acc_hi[r] + acc_ml[r], cs), row, col, p.n, p.epi));
+  }
+}
+
 }  // namespace
 
 void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream) {
@@ -794,6 +933,28 @@ void LaunchTileBf16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_
   hipLaunchKernelGGL(TileBf16Kernel, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, q, k, n,
                      static_cast<u32x4*>(dst), k_steps, items);
   Check(hipGetLastError(), "TileBf16Kernel launch");
+}
+
+void LaunchTileBf16x16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStream_t stream) {
+  const int64_t kbs = k / 32;
+  const int64_t items = (n + 15) / 16 * kbs * 64;
+  if (items <= 0) return;
+  const int64_t grid = (items + kThreads - 1) / kThreads;
+  if (grid > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "weight too large to stage");
+  hipLaunchKernelGGL(TileBf16x16Kernel, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, q, k, n,
+                     static_cast<u32x4*>(dst), kbs, items);
+  Check(hipGetLastError(), "TileBf16x16Kernel launch");
+}
+
+bool GemmSmallStageable(int64_t k, int64_t n, const Q8View& v) {
+  if (v.q == nullptr || v.zero != nullptr || (v.mode != kScalePerCol && v.mode != kScaleConst)) return false;
+  return k >= kBK && k <= kSmallMaxK && k % kBK == 0 && n >= 8 && n % 8 == 0 && n < (int64_t(1) << 30);
+}
+
+bool GemmWantsSmall(int64_t m, int64_t k, int64_t n, const Q8View& v) {
+  if (m <= 16 || m >= (int64_t(1) << 30) || !GemmSmallStageable(k, n, v) || GemmWantsBf16Image(m, k, n, v)) return false;
+  const int64_t groups = ((n + 15) / 16 + kSmallWaves - 1) / kSmallWaves;
+  return (m + 15) / 16 * groups <= 0x7fffffff;
 }
 
 bool GemmBf16Stageable(int64_t k, int64_t n, const Q8View& v) {
@@ -868,6 +1029,27 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
       }
       return true;
     }
+  }
+  if (b.bf16x16 != nullptr && GemmWantsSmall(m, k, n, b)) {
+    SmallArgs sa;
+    sa.a = a;
+    sa.w16 = static_cast<const u32x4*>(b.bf16x16);
+    sa.scale = b.scale;
+    sa.mode = b.mode;
+    sa.const_index = b.const_index;
+    sa.c = c;
+    sa.m = static_cast<int32_t>(m);
+    sa.k = static_cast<int32_t>(k);
+    sa.n = static_cast<int32_t>(n);
+    sa.col_groups = static_cast<int32_t>(((n + 15) / 16 + kSmallWaves - 1) / kSmallWaves);
+    sa.epi = epi;
+    const int64_t blocks = (m + 15) / 16 * sa.col_groups;
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    if (k == 576) hipLaunchKernelGGL(GemmQ8SmallKernel<18>, grid, dim3(kSmallThreads), 0, stream, sa);
+    else if (k == 768) hipLaunchKernelGGL(GemmQ8SmallKernel<24>, grid, dim3(kSmallThreads), 0, stream, sa);
+    else hipLaunchKernelGGL(GemmQ8SmallKernel<0>, grid, dim3(kSmallThreads), 0, stream, sa);
+    Check(hipGetLastError(), "GemmQ8SmallKernel launch");
+    return true;
   }
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;

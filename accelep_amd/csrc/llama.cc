@@ -226,6 +226,7 @@ struct Model {
         else if (m <= 4) v.tiled = StagedColumnTiles(v.q, w.in, w.out, ctx.stream);
         LaunchGemvQ8(a, v, c, m, w.in, w.out, e, ctx.stream);
       } else {
+        if (GemmWantsSmall(m, w.in, w.out, v)) v.bf16x16 = StagedBf16x16(v.q, w.in, w.out, ctx.stream);
         LaunchGemmF32(a, nullptr, v, c, m, w.in, w.out, e, ctx.stream);
       }
     } else if (ctx.exact_products) {

@@ -5,7 +5,8 @@
 // few columns walks k rows 14 KB apart, which HBM serves at well under half its streaming
 // rate. On its first use by the GEMV, the matrix is copied once into 8-column tiles, each
 // tile's k x 8 bytes contiguous (the m > 1 MFMA GEMV takes a group-interleaved form of the
-// same tiles instead, and the int8-weight GEMM a bf16 copy in its MFMA operand order); later
+// same tiles instead, and the int8-weight GEMM a bf16 copy in its MFMA operand order, or in the
+// small GEMM's for a short k); later
 // calls read the copy. The original bytes stay as
 // they are, so every counted copy and every other kernel still sees the EP's layout.
 //
@@ -36,7 +37,7 @@
 namespace accel_hip {
 namespace {
 
-enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1, kLayoutBf16 = 2, kLayoutF32Parts = 3 };
+enum Layout : int { kLayoutTiles = 0, kLayoutGroups = 1, kLayoutBf16 = 2, kLayoutF32Parts = 3, kLayoutBf16x16 = 4 };
 
 struct Key {
   uint64_t id;
@@ -123,6 +124,7 @@ const int8_t* Staged(const void* src, int64_t k, int64_t n, int layout, hipStrea
   ReleasePending();
   const size_t bytes = layout == kLayoutGroups     ? StagedGroupBytes(k, n)
                        : layout == kLayoutBf16     ? StagedBf16Bytes(k, n)
+                       : layout == kLayoutBf16x16  ? StagedBf16x16Bytes(k, n)
                        : layout == kLayoutF32Parts ? StagedF32PartsBytes(k, n)
                                                    : StagedTileBytes(k, n);
   EvictFor(bytes);
@@ -131,6 +133,7 @@ const int8_t* Staged(const void* src, int64_t k, int64_t n, int layout, hipStrea
   const int8_t* q = static_cast<const int8_t*>(src);
   if (layout == kLayoutGroups) LaunchTileGroups(q, k, n, dst, stream);
   else if (layout == kLayoutBf16) LaunchTileBf16(q, k, n, dst, stream);
+  else if (layout == kLayoutBf16x16) LaunchTileBf16x16(q, k, n, dst, stream);
   else if (layout == kLayoutF32Parts) LaunchStageF32Parts(static_cast<const float*>(src), k, n, dst, stream);
   else LaunchTileColumns(q, k, n, dst, stream);
   const uint64_t serial = g_next_serial++;
@@ -155,6 +158,11 @@ const int8_t* StagedGroupTiles(const int8_t* q, int64_t k, int64_t n, hipStream_
 const void* StagedBf16Image(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
   if (k % 32 != 0) return nullptr;
   return Staged(q, k, n, kLayoutBf16, stream, create);
+}
+
+const void* StagedBf16x16(const int8_t* q, int64_t k, int64_t n, hipStream_t stream, bool create) {
+  if (k % 32 != 0) return nullptr;
+  return Staged(q, k, n, kLayoutBf16x16, stream, create);
 }
 
 const void* StagedF32Parts(const float* b, int64_t k, int64_t n, hipStream_t stream, bool create) {

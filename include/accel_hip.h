@@ -146,10 +146,11 @@ ACCEL_HIP_API int accel_hip_matmul_quantized(const float* a, const AccelHipQuant
  * weight's allocation is freed or written. Refused (ACCEL_HIP_RUNTIME_ERROR) during a graph
  * capture; ACCEL_HIP_INVALID_ARGUMENT for a layout the plane cannot take or a weight outside
  * this library's heap. *staged (if not NULL) receives the layouts built. */
-#define ACCEL_HIP_STAGE_GEMV_TILES 1u  /* 8-column tiles: the int8 GEMV at m <= 2 (m <= 4 otherwise) */
+#define ACCEL_HIP_STAGE_GEMV_TILES 1u  /* 8-column tiles: the int8 GEMV at m <= 4 where groups are not taken */
 #define ACCEL_HIP_STAGE_GEMV_GROUPS 2u /* group-interleaved tiles: the bf16-split GEMV, 3 <= m <= 16 */
 #define ACCEL_HIP_STAGE_GEMM_BF16 4u   /* bf16 in MFMA operand order: the int8-weight GEMM, m > 16 */
-#define ACCEL_HIP_STAGE_ALL 7u
+#define ACCEL_HIP_STAGE_GEMM_SMALL 8u  /* bf16 in the small GEMM's operand order: m > 16, k <= 768 */
+#define ACCEL_HIP_STAGE_ALL 15u
 ACCEL_HIP_API int accel_hip_prepare_quantized(const AccelHipQuantPlane* b_quant, int64_t k, int64_t n,
                                               uint32_t layouts, uint32_t* staged);
 /* Exact products (no reference counterpart as a switch; it selects the reference's own

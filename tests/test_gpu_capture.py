@@ -190,7 +190,7 @@ def test_capture_inside_capture_is_refused():
 
 
 INVALID_ARGUMENT = 1
-STAGE_TILES, STAGE_GROUPS, STAGE_BF16 = 1, 2, 4
+STAGE_TILES, STAGE_GROUPS, STAGE_BF16, STAGE_SMALL = 1, 2, 4, 8
 
 
 def _prepare(plane, k, n, layouts=0):
@@ -211,7 +211,7 @@ def test_prepared_weight_can_be_captured():
     g4["qd"], g4["sd"], g4["plane"] = g1["qd"], g1["sd"], g1["plane"]  # the same weight
     rc, staged = _prepare(g1["plane"], k, n)
     assert rc == 0, L.accel_hip_last_error()
-    assert staged == STAGE_TILES | STAGE_GROUPS | STAGE_BF16
+    assert staged == STAGE_TILES | STAGE_GROUPS | STAGE_BF16 | STAGE_SMALL
     check(_call(g1))
     check(_call(g4))
     eager1, eager4 = g1["out"].numpy().copy(), g4["out"].numpy().copy()
@@ -256,7 +256,11 @@ def test_prepare_reports_and_refuses():
     assert rc == INVALID_ARGUMENT and b"group-interleaved" in L.accel_hip_last_error()
     rc, _ = _prepare(zero, k, n, STAGE_BF16)
     assert rc == INVALID_ARGUMENT and b"bf16 copy" in L.accel_hip_last_error()
-    rc, _ = _prepare(plain, k, n, 8)
+    rc, _ = _prepare(zero, k, n, STAGE_SMALL)
+    assert rc == INVALID_ARGUMENT and b"small GEMM" in L.accel_hip_last_error()
+    rc, _ = _prepare(plain, 800, n, STAGE_SMALL)  # k > 768
+    assert rc == INVALID_ARGUMENT
+    rc, _ = _prepare(plain, k, n, 16)
     assert rc == INVALID_ARGUMENT and b"unknown layout" in L.accel_hip_last_error()
     rc, _ = _prepare(plain, 60, n, STAGE_GROUPS)  # k % 32 != 0
     assert rc == INVALID_ARGUMENT
@@ -268,14 +272,15 @@ def test_prepare_reports_and_refuses():
         graph = _end_capture()
         check(L.accel_hip_graph_destroy(graph))
     assert rc == RUNTIME_ERROR and staged == 0, msg
-    assert _prepare(plain, k, n) == (0, STAGE_TILES | STAGE_GROUPS | STAGE_BF16)
+    assert _prepare(plain, k, n) == (0, STAGE_TILES | STAGE_GROUPS | STAGE_BF16 | STAGE_SMALL)
 
 
 def test_event_records_inside_a_capture_are_timeable():
     """accel_hip_event_record during a capture adds an event node that every replay records:
     the elapsed time between two such events is readable after each replay (a plain record
     inside a graph is refused by hipEventElapsedTime), positive, and no longer than the same
-    replay timed from outside the graph."""
+    replay timed from outside the graph (both spans from one replay: a replay's span varies
+    with the clocks from one replay to the next)."""
     L = lib()
     g = _gemv(1, 1024, 4096, 91)
     check(_call(g))  # stage the weight copy eagerly
@@ -289,15 +294,13 @@ def test_event_records_inside_a_capture_are_timeable():
     handle = _end_capture()
     try:
         for _ in range(3):
-            check(L.accel_hip_graph_launch(handle, 1))
-            check(L.accel_hip_synchronize())
-            inner = L.accel_hip_event_elapsed_ms(0, 1)
-            assert inner > 0, L.accel_hip_last_error().decode()
             check(L.accel_hip_event_record(2))
             check(L.accel_hip_graph_launch(handle, 1))
             check(L.accel_hip_event_record(3))
             outer = L.accel_hip_event_elapsed_ms(2, 3)
             assert outer > 0, L.accel_hip_last_error().decode()
+            inner = L.accel_hip_event_elapsed_ms(0, 1)
+            assert inner > 0, L.accel_hip_last_error().decode()
             assert inner <= outer
         np.testing.assert_allclose(g["out"].numpy(), g["a"].astype(np.float64) @ g["w"].astype(np.float64),
                                    rtol=1e-4, atol=1e-4)

@@ -438,7 +438,8 @@ def test_gemm_q8_bf16_bound(m, k, n, whole):
 def test_gemm_q8_bf16_integer_sums_exact(m, k, n):
     """Integer A with |a| <= 16: every partial sum is an integer below 2^24, so C = fl(S *
     scale) bit for bit; a row, column or k slot paired wrongly changes S. The last two
-    shapes have fewer tiles than CUs and split K (21 and 6 splits)."""
+    shapes have fewer tiles than CUs: 100 x 2048 x 264 splits K (21 splits), 512 x 576 x 3072
+    (k <= 768) runs on the small kernel."""
     r = np.random.default_rng(91 + m)
     a = r.integers(-16, 17, size=(m, k)).astype(np.float32)
     case = _split_case(m, k, n, 92 + m, a=a)
@@ -469,6 +470,70 @@ def test_gemm_q8_bf16_epilogues():
     m, k, n = 512, 128, 8192
     case = _split_case(m, k, n, 95)
     r = np.random.default_rng(96)
+    bias = r.standard_normal(n).astype(np.float32)
+    resid = r.standard_normal((m, n)).astype(np.float32)
+    bias_d, res_d = dev(bias), dev(resid)
+    base = (case["a"].astype(np.float64) @ dequant_host(case["bq"], k, n).astype(np.float64)).astype(np.float32)
+    o = oracle()
+    for act in (1, 2):
+        e = Epilogue(alpha=1.5, beta=0.5, bias=bias_d.ptr, bias_rank=1, activation=act, residual=res_d.ptr)
+        e.bias_shape[0] = n
+        got = matmul_quantized(case, e)
+        want = o.gemm_epilogue(base, 1.5, bias, [n], 0.5, act) + resid
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
+# ---- int8 GEMM for a short k on the small kernel: m > 16, k <= 768, a grid below the 128-tile
+# image path. 16-row blocks over all of k; the activation rows split into three exact bf16 parts
+# in LDS; the weight read from its bf16 copy in the B-operand order of the 16x16x32 MFMA ------
+
+@pytest.mark.parametrize("m,k,n,whole", [(17, 32, 8, False), (37, 96, 1000, True), (100, 768, 136, False),
+                                         (512, 576, 960, False), (333, 160, 3080, False)])
+def test_gemm_q8_small_bound(m, k, n, whole):
+    """A partial 16-row block, column blocks and groups partly past n, one 32-row block, the
+    largest k, a whole-tensor scale: within 2 gamma_K of the float64 product and within the
+    plugin tolerance of it."""
+    case = _split_case(m, k, n, 7 * m + k + n, whole_scale=whole)
+    got = matmul_quantized(case)
+    w = dequant_host(case["bq"], k, n)
+    assert_gamma_bound(got, case["a"], w)
+    assert_plugin_tolerance(got, case["a"], w)
+
+
+@pytest.mark.parametrize("m,k,n", [(48, 768, 264), (530, 576, 576)])
+def test_gemm_q8_small_integer_sums_exact(m, k, n):
+    """Integer A with |a| <= 16 on the small kernel: C = fl(S * scale) bit for bit; a row,
+    column or k slot paired wrongly anywhere changes S."""
+    r = np.random.default_rng(17 + m)
+    a = r.integers(-16, 17, size=(m, k)).astype(np.float32)
+    case = _split_case(m, k, n, 18 + m, a=a)
+    got = matmul_quantized(case)
+    s = a.astype(np.float64) @ case["bq"]["q"].reshape(k, n).astype(np.float64)
+    assert np.abs(s).max() < 2 ** 24
+    same_bits(got, (s.astype(np.float32) * case["bq"]["scale"][None, :]).astype(np.float32))
+
+
+def test_gemm_q8_small_full_precision_a():
+    """One power-of-two weight per column on the small kernel: C = fl(a * w * scale) exactly,
+    which needs all three bf16 parts of every N(0, 1) activation to reach the sum."""
+    m, k, n = 40, 256, 264
+    r = np.random.default_rng(19)
+    rows = r.integers(0, k, size=n)
+    vals = r.choice(np.array([-64, -8, -2, -1, 1, 4, 16, 64], np.int8), size=n)
+    q = np.zeros((k, n), np.int8)
+    q[rows, np.arange(n)] = vals
+    case = _split_case(m, k, n, 20, q=q.ravel())
+    got = matmul_quantized(case)
+    prod = (case["a"][:, rows] * vals.astype(np.float32)[None, :]).astype(np.float32)
+    same_bits(got, (prod * case["bq"]["scale"][None, :]).astype(np.float32))
+
+
+def test_gemm_q8_small_epilogues():
+    """alpha, beta * bias, Relu / exact Gelu and a same-shape residual at the small kernel's
+    store, against the oracle's epilogue of the float64 product."""
+    m, k, n = 200, 384, 1000
+    case = _split_case(m, k, n, 21)
+    r = np.random.default_rng(22)
     bias = r.standard_normal(n).astype(np.float32)
     resid = r.standard_normal((m, n)).astype(np.float32)
     bias_d, res_d = dev(bias), dev(resid)
