@@ -50,6 +50,7 @@ struct GemvArgs {
   int32_t tiles;
   int32_t tiles_per_xcd;
   int32_t splits;
+  int32_t group_pairs;  // split-bf16 kernel: column groups x splits
   int64_t rows_per_split;
   float* partials;  // [splits][m][n] when splits > 1
   // Column-tiled copy of W (narrow kernel): 8-column tile t, row r at tiled + (t*kp + r)*8
@@ -960,86 +961,53 @@ constexpr int kSplitBlockRows = static_cast<int>(kGemvGroupRows);  // K of one M
 constexpr int kSplitBatch = 2;  // blocks a wave loads before using any
 constexpr int kSplitGroupBytes = kSplitTiles * kNarrowTile;  // bytes of one row of a group
 
-// kPlain: the epilogue is the identity and C one [m, n] matrix, so each sum is stored as
-// sum * scale with no epilogue code (which costs about 1 us of the m = 16 kernel's tail).
+// One 32-row block of a lane: its four weight loads w (rows 8g + 2h, 8g + 2h + 1 of its tile
+// in load h) and its 8 activations x (rows 8g .. 8g + 7) into the 8 accumulators, hi, then
+// mid, then lo parts.
+__device__ __forceinline__ void SplitBf16Block(const u32x4 (&w)[4], const f32x2 (&x)[4], v4f (&acc)[kNarrowTile]) {
+  u32x4 ah, am, al;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const float x0 = x[h][0];
+    const float x1 = x[h][1];
+    ah[h] = PackBf16(x0, x1);
+    const float r0 = x0 - Bf16Low(ah[h]);
+    const float r1 = x1 - Bf16High(ah[h]);
+    am[h] = PackBf16(r0, r1);
+    al[h] = PackBf16(r0 - Bf16Low(am[h]), r1 - Bf16High(am[h]));
+  }
+  // Column c of the tile: row 8g + 2h in byte c of words 0..1 of load h, row 8g + 2h + 1 in
+  // words 2..3.
+  u32x4 bw[kNarrowTile];
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c)
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      bw[c][h] = PackBf16(ByteToFloat(w[h][c >> 2], c & 3), ByteToFloat(w[h][2 + (c >> 2)], c & 3));
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c)
+    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), __builtin_bit_cast(bf16x8, bw[c]),
+                                                     acc[c], 0, 0, 0);
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c)
+    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), __builtin_bit_cast(bf16x8, bw[c]),
+                                                     acc[c], 0, 0, 0);
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c)
+    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), __builtin_bit_cast(bf16x8, bw[c]),
+                                                     acc[c], 0, 0, 0);
+}
+
+// The end of a split-bf16 workgroup: the waves' accumulators meet in LDS (`red`, wave order),
+// then either the group's sums are scaled and stored, or, with K splits, this split's partial
+// sums are stored and the last workgroup of the group to arrive adds the splits in split order.
 template <bool kPlain>
-__global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p) {
-  __shared__ float red[kSplitWaves][32][65];  // [wave][4 * column + row of the MFMA tile][lane]
-  __shared__ bool is_last;
+__device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&acc)[kNarrowTile],
+                                                float (*red)[32][65], bool* is_last_flag, int group, int split) {
+  bool& is_last = *is_last_flag;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int slot = lane & 15;  // B column slot (tile) and A row
-  const int g = lane >> 4;     // k group
-  const int group = blockIdx.x;
-  const int split = blockIdx.y;
-  const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
-  const int64_t ke = min(p.k, kb + p.rows_per_split);
-  const int blocks = static_cast<int>((ke - kb) / kSplitBlockRows);
-  const int8_t* tb = p.grouped + (static_cast<int64_t>(group) * p.k + kb) * kSplitGroupBytes + 64 * slot + 16 * g;
-  const bool row_live = slot < p.m;
-  const float* ab = p.a + static_cast<int64_t>(row_live ? slot : p.m - 1) * p.k + kb + 8 * g;
-
-  v4f acc[kNarrowTile];
-#pragma unroll
-  for (int c = 0; c < kNarrowTile; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  for (int b0 = wave; b0 < blocks; b0 += kSplitWaves * kSplitBatch) {
-    u32x4 w[kSplitBatch][4];
-    f32x2 x[kSplitBatch][4];
-#pragma unroll
-    for (int u = 0; u < kSplitBatch; ++u) {
-      const int blk = b0 + u * kSplitWaves;
-      const int bc = blk < blocks ? blk : blocks - 1;  // a valid block; its A is zeroed below
-      const u32x4* wb = reinterpret_cast<const u32x4*>(tb + static_cast<int64_t>(bc) * (kSplitBlockRows * kSplitGroupBytes));
-      const v4f* xb = reinterpret_cast<const v4f*>(ab + static_cast<int64_t>(bc) * kSplitBlockRows);
-#pragma unroll
-      for (int h = 0; h < 4; ++h) w[u][h] = __builtin_nontemporal_load(wb + 64 * h);  // rows 8g + 2h, 8g + 2h + 1
-      // This lane's 8 activations of the block, rows 8g .. 8g + 7: two 16-byte loads.
-      const v4f x0 = xb[0], x1 = xb[1];
-      x[u][0] = f32x2{x0[0], x0[1]};
-      x[u][1] = f32x2{x0[2], x0[3]};
-      x[u][2] = f32x2{x1[0], x1[1]};
-      x[u][3] = f32x2{x1[2], x1[3]};
-    }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any is used
-#pragma unroll
-    for (int u = 0; u < kSplitBatch; ++u) {
-      const bool live = row_live && b0 + u * kSplitWaves < blocks;
-      u32x4 ah, am, al;
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const float x0 = live ? x[u][h][0] : 0.f;
-        const float x1 = live ? x[u][h][1] : 0.f;
-        ah[h] = PackBf16(x0, x1);
-        const float r0 = x0 - Bf16Low(ah[h]);
-        const float r1 = x1 - Bf16High(ah[h]);
-        am[h] = PackBf16(r0, r1);
-        al[h] = PackBf16(r0 - Bf16Low(am[h]), r1 - Bf16High(am[h]));
-      }
-      // Column c of the tile: row 8g + 2h in byte c of words 0..1 of load h, row 8g + 2h + 1
-      // in words 2..3.
-      u32x4 bw[kNarrowTile];
-#pragma unroll
-      for (int c = 0; c < kNarrowTile; ++c)
-#pragma unroll
-        for (int h = 0; h < 4; ++h)
-          bw[c][h] = PackBf16(ByteToFloat(w[u][h][c >> 2], c & 3), ByteToFloat(w[u][h][2 + (c >> 2)], c & 3));
-#pragma unroll
-      for (int c = 0; c < kNarrowTile; ++c)
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), __builtin_bit_cast(bf16x8, bw[c]),
-                                                         acc[c], 0, 0, 0);
-#pragma unroll
-      for (int c = 0; c < kNarrowTile; ++c)
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), __builtin_bit_cast(bf16x8, bw[c]),
-                                                         acc[c], 0, 0, 0);
-#pragma unroll
-      for (int c = 0; c < kNarrowTile; ++c)
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), __builtin_bit_cast(bf16x8, bw[c]),
-                                                         acc[c], 0, 0, 0);
-    }
-  }
-
   // Element r of MFMA c in lane l: row 4 * (l / 16) + r, column 8 * (16 * group + l % 16) + c.
 #pragma unroll
   for (int c = 0; c < kNarrowTile; ++c)
@@ -1113,6 +1081,72 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
     if (kPlain) p.c[mm * static_cast<int>(p.n) + col] = __fmul_rn(sum[i], cs);
     else StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(sum[i], cs), mm, col, p.n, p.epi));
   }
+}
+
+// kPlain: the epilogue is the identity and C one [m, n] matrix, so each sum is stored as
+// sum * scale with no epilogue code (which costs about 1 us of the m = 16 kernel's tail).
+// Grid: one dimension, `slots` workgroups (a multiple of 8); the workgroups of one XCD
+// (blockIdx.x % 8) take consecutive (group, split) pairs, so the splits of a group and
+// neighbouring groups run on one XCD; slots past groups x splits exit at once.
+// Rows m .. 15 of the MFMA tile are lanes that read row m - 1's activations; their sums are
+// never stored, so they need no zeroing.
+template <bool kPlain>
+__global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p) {
+  __shared__ float red[kSplitWaves][32][65];  // [wave][4 * column + row of the MFMA tile][lane]
+  __shared__ bool is_last;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slot = lane & 15;  // B column slot (tile) and A row
+  const int g = lane >> 4;     // k group
+  const int per_xcd = static_cast<int>(gridDim.x / kXcds);
+  const int pair = static_cast<int>(blockIdx.x % kXcds) * per_xcd + static_cast<int>(blockIdx.x / kXcds);
+  if (pair >= p.group_pairs) return;
+  const int group = pair / p.splits;
+  const int split = pair - group * p.splits;
+  const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
+  const int64_t ke = min(p.k, kb + p.rows_per_split);
+  const int blocks = static_cast<int>((ke - kb) / kSplitBlockRows);
+  const int8_t* tb = p.grouped + (static_cast<int64_t>(group) * p.k + kb) * kSplitGroupBytes + 64 * slot + 16 * g;
+  const float* ab = p.a + static_cast<int64_t>(slot < p.m ? slot : p.m - 1) * p.k + kb + 8 * g;
+
+  v4f acc[kNarrowTile];
+#pragma unroll
+  for (int c = 0; c < kNarrowTile; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // The wave's blocks wave, wave + 4, ...: whole batches, then the rest one at a time.
+  const int nb = blocks > wave ? (blocks - wave + kSplitWaves - 1) / kSplitWaves : 0;
+  auto load_block = [&](int j, u32x4 (&w)[4], f32x2 (&x)[4]) {
+    const int blk = wave + kSplitWaves * j;
+    const u32x4* wb = reinterpret_cast<const u32x4*>(tb + static_cast<int64_t>(blk) * (kSplitBlockRows * kSplitGroupBytes));
+    const v4f* xb = reinterpret_cast<const v4f*>(ab + static_cast<int64_t>(blk) * kSplitBlockRows);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) w[h] = __builtin_nontemporal_load(wb + 64 * h);  // rows 8g + 2h, 8g + 2h + 1
+    // This lane's 8 activations of the block, rows 8g .. 8g + 7: two 16-byte loads.
+    const v4f x0 = xb[0], x1 = xb[1];
+    x[0] = f32x2{x0[0], x0[1]};
+    x[1] = f32x2{x0[2], x0[3]};
+    x[2] = f32x2{x1[0], x1[1]};
+    x[3] = f32x2{x1[2], x1[3]};
+  };
+  int j = 0;
+  for (; j + kSplitBatch <= nb; j += kSplitBatch) {
+    u32x4 w[kSplitBatch][4];
+    f32x2 x[kSplitBatch][4];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) load_block(j + u, w[u], x[u]);
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any is used
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) SplitBf16Block(w[u], x[u], acc);
+  }
+  for (; j < nb; ++j) {
+    u32x4 w[4];
+    f32x2 x[4];
+    load_block(j, w, x);
+    SplitBf16Block(w, x, acc);
+  }
+
+  SplitBf16Finish<kPlain>(p, acc, red, &is_last, group, split);
 }
 
 // dst (group-interleaved, see StagedGroupBytes) from q [k, n]: one thread writes the 16 bytes
@@ -1386,7 +1420,10 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
   if (split_bf16) {
     const int64_t groups = (tiles + kSplitTiles - 1) / kSplitTiles;
     if (splits > 1) args.arrivals = static_cast<uint32_t*>(Temp(kTempArrivals, static_cast<size_t>(groups) * 4));
-    const dim3 sgrid(static_cast<uint32_t>(groups), static_cast<uint32_t>(splits));
+    const int64_t pairs = groups * splits;
+    if (pairs > 0x7ffffff0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV too large");
+    args.group_pairs = static_cast<int32_t>(pairs);
+    const dim3 sgrid(static_cast<uint32_t>((pairs + kXcds - 1) / kXcds * kXcds));
     if (epi.Identity() && epi.split[0] == 0)
       hipLaunchKernelGGL(GemvSplitBf16Kernel<true>, sgrid, dim3(kSplitThreads), 0, stream, args);
     else
