@@ -1002,7 +1002,8 @@ __device__ __forceinline__ void SplitBf16Block(const u32x4 (&w)[4], const f32x2 
 // then either the group's sums are scaled and stored, or, with K splits, this split's partial
 // sums are stored and the last workgroup of the group to arrive adds the splits in split order.
 template <bool kPlain>
-__device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&acc)[kNarrowTile],
+__device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, int32_t m, int32_t splits, float* partials,
+                                                uint32_t* arrivals, const v4f (&acc)[kNarrowTile],
                                                 float (*red)[32][65], bool* is_last_flag, int group, int split) {
   bool& is_last = *is_last_flag;
   const int tid = threadIdx.x;
@@ -1020,7 +1021,7 @@ __device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&a
   const int c = cc & 7;
   const int64_t col = static_cast<int64_t>(group * kSplitTiles + jt) * kNarrowTile + c;
   const int m0 = (tid >> 7) * 8;
-  const int mend = min(p.m, static_cast<int64_t>(m0 + 8));
+  const int mend = min(m, m0 + 8);
   float sum[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -1033,13 +1034,13 @@ __device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&a
     sum[i] = s;
   }
   const bool live_col = col < p.n;
-  if (p.splits > 1) {
+  if (splits > 1) {
     // Partial sums out (agent scope: the last workgroup, on any XCD, reads them), then the
     // arrival count of the group. Split sp's [m, n] block starts at the uniform (scalar)
     // offset sp * m * n; rows within it are 32-bit offsets (the launcher checks m * n < 2^31).
     const int n32 = static_cast<int>(p.n);
-    const int64_t split_stride = p.m * p.n;
-    float* part = p.partials + col;
+    const int64_t split_stride = static_cast<int64_t>(m) * p.n;
+    float* part = partials + col;
     float* mine = part + split * split_stride;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -1047,21 +1048,21 @@ __device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&a
         __hip_atomic_store(&mine[(m0 + i) * n32], sum[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) is_last = atomicAdd(&p.arrivals[group], 1u) == static_cast<uint32_t>(p.splits - 1);
+    if (tid == 0) is_last = atomicAdd(&arrivals[group], 1u) == static_cast<uint32_t>(splits - 1);
     __syncthreads();
     if (!is_last) return;
-    if (tid == 0) atomicExch(&p.arrivals[group], 0u);  // ready for the next launch
+    if (tid == 0) atomicExch(&arrivals[group], 0u);  // ready for the next launch
     if (!live_col || m0 >= mend) return;
     // The splits' sums in split order; kChunk splits of all 8 rows are requested at once
     // (clamped to valid rows and splits; the extra values are not used).
     constexpr int kChunk = 4;
-    for (int sp0 = 0; sp0 < p.splits; sp0 += kChunk) {
+    for (int sp0 = 0; sp0 < splits; sp0 += kChunk) {
       float v[kChunk][8];
 #pragma unroll
       for (int t = 0; t < kChunk; ++t)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int sp = min(sp0 + t, p.splits - 1);
+          const int sp = min(sp0 + t, splits - 1);
           const int mm = min(m0 + i, mend - 1);
           v[t][i] = __hip_atomic_load(&part[sp * split_stride + mm * n32], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1069,7 +1070,7 @@ __device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&a
       for (int t = 0; t < kChunk; ++t)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          if (sp0 + t < p.splits) sum[i] = sp0 + t == 0 ? v[t][i] : sum[i] + v[t][i];
+          if (sp0 + t < splits) sum[i] = sp0 + t == 0 ? v[t][i] : sum[i] + v[t][i];
     }
   }
   if (!live_col) return;
@@ -1085,13 +1086,19 @@ __device__ __forceinline__ void SplitBf16Finish(const GemvArgs& p, const v4f (&a
 
 // kPlain: the epilogue is the identity and C one [m, n] matrix, so each sum is stored as
 // sum * scale with no epilogue code (which costs about 1 us of the m = 16 kernel's tail).
+// What the loads and the arrival need leads the arguments (13 dwords, preloaded into SGPRs
+// at wave launch, so the first weight loads issue without a kernarg round trip); the
+// epilogue's fields are read from `p` behind the loads.
 // Grid: one dimension, `slots` workgroups (a multiple of 8); the workgroups of one XCD
 // (blockIdx.x % 8) take consecutive (group, split) pairs, so the splits of a group and
 // neighbouring groups run on one XCD; slots past groups x splits exit at once.
 // Rows m .. 15 of the MFMA tile are lanes that read row m - 1's activations; their sums are
 // never stored, so they need no zeroing.
 template <bool kPlain>
-__global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p) {
+__global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(const int8_t* grouped, const float* a,
+                                                                     float* partials, uint32_t* arrivals, int32_t m,
+                                                                     int32_t k, int32_t rows_per_split, int32_t splits,
+                                                                     int32_t group_pairs, GemvArgs p) {
   __shared__ float red[kSplitWaves][32][65];  // [wave][4 * column + row of the MFMA tile][lane]
   __shared__ bool is_last;
   const int tid = threadIdx.x;
@@ -1101,14 +1108,14 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
   const int g = lane >> 4;     // k group
   const int per_xcd = static_cast<int>(gridDim.x / kXcds);
   const int pair = static_cast<int>(blockIdx.x % kXcds) * per_xcd + static_cast<int>(blockIdx.x / kXcds);
-  if (pair >= p.group_pairs) return;
-  const int group = pair / p.splits;
-  const int split = pair - group * p.splits;
-  const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
-  const int64_t ke = min(p.k, kb + p.rows_per_split);
+  if (pair >= group_pairs) return;
+  const int group = pair / splits;
+  const int split = pair - group * splits;
+  const int64_t kb = static_cast<int64_t>(split) * rows_per_split;
+  const int64_t ke = min(static_cast<int64_t>(k), kb + rows_per_split);
   const int blocks = static_cast<int>((ke - kb) / kSplitBlockRows);
-  const int8_t* tb = p.grouped + (static_cast<int64_t>(group) * p.k + kb) * kSplitGroupBytes + 64 * slot + 16 * g;
-  const float* ab = p.a + static_cast<int64_t>(slot < p.m ? slot : p.m - 1) * p.k + kb + 8 * g;
+  const int8_t* tb = grouped + (static_cast<int64_t>(group) * k + kb) * kSplitGroupBytes + 64 * slot + 16 * g;
+  const float* ab = a + static_cast<int64_t>(slot < m ? slot : m - 1) * k + kb + 8 * g;
 
   v4f acc[kNarrowTile];
 #pragma unroll
@@ -1146,7 +1153,7 @@ __global__ __launch_bounds__(kSplitThreads) void GemvSplitBf16Kernel(GemvArgs p)
     SplitBf16Block(w, x, acc);
   }
 
-  SplitBf16Finish<kPlain>(p, acc, red, &is_last, group, split);
+  SplitBf16Finish<kPlain>(p, m, splits, partials, arrivals, acc, red, &is_last, group, split);
 }
 
 // dst (group-interleaved, see StagedGroupBytes) from q [k, n]: one thread writes the 16 bytes
@@ -1424,10 +1431,14 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     if (pairs > 0x7ffffff0) Fail(ACCEL_HIP_INVALID_ARGUMENT, "GEMV too large");
     args.group_pairs = static_cast<int32_t>(pairs);
     const dim3 sgrid(static_cast<uint32_t>((pairs + kXcds - 1) / kXcds * kXcds));
+    const int32_t m32 = static_cast<int32_t>(m), k32 = static_cast<int32_t>(k), rows32 = static_cast<int32_t>(rows);
+    const int32_t splits32 = static_cast<int32_t>(splits), pairs32 = static_cast<int32_t>(pairs);
     if (epi.Identity() && epi.split[0] == 0)
-      hipLaunchKernelGGL(GemvSplitBf16Kernel<true>, sgrid, dim3(kSplitThreads), 0, stream, args);
+      hipLaunchKernelGGL(GemvSplitBf16Kernel<true>, sgrid, dim3(kSplitThreads), 0, stream, b.grouped, a, args.partials,
+                         args.arrivals, m32, k32, rows32, splits32, pairs32, args);
     else
-      hipLaunchKernelGGL(GemvSplitBf16Kernel<false>, sgrid, dim3(kSplitThreads), 0, stream, args);
+      hipLaunchKernelGGL(GemvSplitBf16Kernel<false>, sgrid, dim3(kSplitThreads), 0, stream, b.grouped, a, args.partials,
+                         args.arrivals, m32, k32, rows32, splits32, pairs32, args);
   } else if (narrow) {
     const bool pair_a = (k % 2 == 0) && (reinterpret_cast<uintptr_t>(a) % 8 == 0);
     // The staged prologue row lives in LDS (16-byte aligned), so only an even k is needed
