@@ -384,7 +384,9 @@ __device__ __forceinline__ void StageInputRow(const GemvArgs& p, float* a_stage,
 // stride 256, wave then fixed-order LDS sums), so the row equals that pass's output.
 template <int M, bool kZero, bool kRowScale, bool kPairA, int kAOp = kAOpNone>
 __global__ __launch_bounds__(NarrowShape<M>::kThreads)
-__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))) void GemvNarrowKernel(GemvArgs p) {
+__attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))) void GemvNarrowKernel(
+    const int8_t* tiled, const float* a, const float* scale, int32_t m, int32_t k, int32_t n, int32_t tiles,
+    int32_t tiles_per_xcd, int32_t rows_per_split, GemvArgs p) {
   using S = NarrowShape<M>;
   static_assert(kAOp == kAOpNone || (M == 1 && S::kThreads == 256), "prologue: m = 1, RmsNormKernel's block");
   __shared__ float red[S::kWaves][M][kNarrowTile];
@@ -394,14 +396,14 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
   const int wave = tid >> 6;
   // A workgroup past the last tile (the grid is a multiple of the XCD count) recomputes the
   // last tile and stores nothing: no branch on the arguments before the loads are issued.
-  const int tile_raw = (blockIdx.x % kXcds) * p.tiles_per_xcd + blockIdx.x / kXcds;
-  const bool tile_live = tile_raw < p.tiles;
-  const int tile = tile_live ? tile_raw : p.tiles - 1;
+  const int tile_raw = (blockIdx.x % kXcds) * tiles_per_xcd + blockIdx.x / kXcds;
+  const bool tile_live = tile_raw < tiles;
+  const int tile = tile_live ? tile_raw : tiles - 1;
   const int split = blockIdx.y;
-  const int64_t kb = static_cast<int64_t>(split) * p.rows_per_split;
-  const int64_t ke = min(p.k, kb + p.rows_per_split);
+  const int64_t kb = static_cast<int64_t>(split) * rows_per_split;
+  const int64_t ke = min(static_cast<int64_t>(k), kb + rows_per_split);
   const int64_t kw = ke + (ke & 1);
-  const int64_t kp = p.k + (p.k & 1);
+  const int64_t kp = k + (k & 1);
   const int64_t col0 = static_cast<int64_t>(tile) * kNarrowTile;
 
   float zc[kNarrowTile];
@@ -410,15 +412,15 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
   if (kZero && !kRowScale) {
 #pragma unroll
     for (int c = 0; c < kNarrowTile; ++c) {
-      const int64_t col = col0 + c < p.n ? col0 + c : p.n - 1;
+      const int64_t col = col0 + c < n ? col0 + c : n - 1;
       zc[c] = static_cast<float>(p.mode == kScalePerCol ? p.zero[col] : p.zero[p.const_index]);
     }
   }
   // The scale of the column this thread may store (c = tid % 8), loaded now so that storing
   // the sums waits for no memory. Every thread loads (from a clamped, valid index); a per-row
   // scale was folded into A and is not used here.
-  const int64_t scol = col0 + (tid & 7) < p.n ? col0 + (tid & 7) : p.n - 1;
-  const float col_scale = p.scale[p.mode == kScalePerCol ? scol : (p.mode == kScaleConst ? p.const_index : 0)];
+  const int64_t scol = col0 + (tid & 7) < n ? col0 + (tid & 7) : n - 1;
+  const float col_scale = scale[p.mode == kScalePerCol ? scol : (p.mode == kScaleConst ? p.const_index : 0)];
   float acc[M][kNarrowTile];
 #pragma unroll
   for (int mm = 0; mm < M; ++mm)
@@ -428,10 +430,10 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
   // One batch in flight per wave: its loads are all issued before any of them is used. A
   // workgroup holds few registers, so several run per CU and cover each other's waits (a
   // second buffer would double the registers and halve the workgroups per CU).
-  const int8_t* tbase = p.tiled + static_cast<int64_t>(tile) * kp * kNarrowTile;
+  const int8_t* tbase = tiled + static_cast<int64_t>(tile) * kp * kNarrowTile;
   const float* arow[M];
 #pragma unroll
-  for (int mm = 0; mm < M; ++mm) arow[mm] = p.a + static_cast<int64_t>(mm < p.m ? mm : p.m - 1) * p.k;
+  for (int mm = 0; mm < M; ++mm) arow[mm] = a + static_cast<int64_t>(mm < m ? mm : m - 1) * k;
   if (kAOp != kAOpNone) {
     // One clamped batch covers k (the launcher checks k <= kBatchRows and sends no split).
     __shared__ double part[S::kWaves];
@@ -486,14 +488,14 @@ __attribute__((amdgpu_waves_per_eu(NarrowMinWaves<M, kZero, kRowScale, kAOp>()))
     const int mm = tid / kNarrowTile;
     const int c = tid % kNarrowTile;
     const int64_t col = col0 + c;
-    if (mm < p.m && col < p.n) {
+    if (mm < m && col < n) {
       float s = red[0][mm][c];
       for (int wv = 1; wv < S::kWaves; ++wv) s = s + red[wv][mm][c];
       if (p.splits > 1) {
-        p.partials[(static_cast<int64_t>(split) * p.m + mm) * p.n + col] = s;
+        p.partials[(static_cast<int64_t>(split) * m + mm) * n + col] = s;
       } else {
         const float cs = p.mode == kScalePerRow ? 1.f : col_scale;
-        StoreC(p.c, mm, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(s, cs), mm, col, p.n, p.epi));
+        StoreC(p.c, mm, col, n, p.epi, ApplyEpilogue(__fmul_rn(s, cs), mm, col, n, p.epi));
       }
     }
   }
@@ -1285,12 +1287,17 @@ void LaunchSplitReduce(const float* partials, int32_t splits, int64_t m, int64_t
 namespace {
 
 template <int M>
+// The leading arguments of GemvNarrowKernel (preloaded into SGPRs at wave launch), from `g`.
+#define ACCEL_NARROW_LEAD(g)                                                                                   \
+  (g).tiled, (g).a, (g).scale, static_cast<int32_t>((g).m), static_cast<int32_t>((g).k),                        \
+      static_cast<int32_t>((g).n), (g).tiles, (g).tiles_per_xcd, static_cast<int32_t>((g).rows_per_split)
+
 void LaunchNarrow(const GemvArgs& args, dim3 grid, bool zero, bool row_scale, bool pair_a, hipStream_t stream) {
   const dim3 block(NarrowShape<M>::kThreads);
   switch ((zero ? 4 : 0) | (row_scale ? 2 : 0) | (pair_a ? 1 : 0)) {
 #define ACCEL_GEMV_CASE(Z, R, P) \
   case (Z ? 4 : 0) | (R ? 2 : 0) | (P ? 1 : 0): \
-    hipLaunchKernelGGL((GemvNarrowKernel<M, Z, R, P>), grid, block, 0, stream, args); \
+    hipLaunchKernelGGL((GemvNarrowKernel<M, Z, R, P>), grid, block, 0, stream, ACCEL_NARROW_LEAD(args), args); \
     break;
     ACCEL_GEMV_CASE(true, true, true) ACCEL_GEMV_CASE(true, true, false) ACCEL_GEMV_CASE(true, false, true)
     ACCEL_GEMV_CASE(true, false, false) ACCEL_GEMV_CASE(false, true, true) ACCEL_GEMV_CASE(false, true, false)
@@ -1578,14 +1585,14 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
     } else if (a_op == kAOpRms) {
       // The staged row in LDS is 16-byte aligned and k is whole, so pairs load as one.
       if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpRms>), grid,
-                                         dim3(NarrowShape<1>::kThreads), 0, stream, args);
+                                         dim3(NarrowShape<1>::kThreads), 0, stream, ACCEL_NARROW_LEAD(args), args);
       else hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, false, kAOpRms>), grid,
-                              dim3(NarrowShape<1>::kThreads), 0, stream, args);
+                              dim3(NarrowShape<1>::kThreads), 0, stream, ACCEL_NARROW_LEAD(args), args);
     } else if (a_op == kAOpSiluUp) {
       if (k % 2 == 0) hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, true, kAOpSiluUp>), grid,
-                                         dim3(NarrowShape<1>::kThreads), 0, stream, args);
+                                         dim3(NarrowShape<1>::kThreads), 0, stream, ACCEL_NARROW_LEAD(args), args);
       else hipLaunchKernelGGL((GemvNarrowKernel<1, false, false, false, kAOpSiluUp>), grid,
-                              dim3(NarrowShape<1>::kThreads), 0, stream, args);
+                              dim3(NarrowShape<1>::kThreads), 0, stream, ACCEL_NARROW_LEAD(args), args);
     } else if (m == 1) {
       LaunchNarrow<1>(args, grid, zero, row_scale, pair_a, stream);
     } else if (m == 2) {
