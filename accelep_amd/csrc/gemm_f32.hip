@@ -571,7 +571,20 @@ __device__ __forceinline__ void StoreRows(const float (&v)[kWsRowsPerThread], co
 // kGroups > 0: the K range of a wave is exactly kGroups groups of 32. kGroups == 0: any even
 // number of groups. kStaged: B's parts are read from p.bparts (the same bits the split gives).
 template <int kGroups, bool kStaged>
-__global__ __launch_bounds__(kThreads) void GemmF32SplitBf16Kernel(WsArgs p) {
+// The pointers and sizes the operand loads need lead the arguments (10 dwords, preloaded into
+// SGPRs at wave launch, so the first loads issue without a kernarg round trip); the output
+// pointers and the epilogue come from `args`, read behind the loads.
+__global__ __launch_bounds__(kThreads) void GemmF32SplitBf16Kernel(const float* a, const float* b,
+                                                                   const u32x4* bparts, int32_t m, int32_t k,
+                                                                   int32_t n, int32_t k_per_wg, WsArgs args) {
+  WsArgs p = args;
+  p.a = a;
+  p.b = b;
+  p.bparts = bparts;
+  p.m = m;
+  p.k = k;
+  p.n = n;
+  p.k_per_wg = k_per_wg;
   __shared__ float red[4][kWsTile][kWsPad];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -731,7 +744,7 @@ bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
     int64_t wsplits = wtiles < cus ? std::max<int64_t>(1, std::min<int64_t>((cus + wtiles - 1) / wtiles, k / (4 * unit)))
                                    : 1;
     while (wsplits > 1 && k % (wsplits * unit) != 0) --wsplits;
-    if (k % (wsplits * unit) == 0 && wtiles <= 0x7fffffff) {
+    if (k % (wsplits * unit) == 0 && wtiles <= 0x7fffffff && m <= 0x7fffffff && n <= 0x7fffffff && k <= 0x7fffffff) {
       WsArgs ws;
       ws.a = a;
       ws.b = b;
@@ -747,12 +760,18 @@ bool LaunchGemmF32(const float* a, const float* b, const Q8View& bq, float* c, i
       ws.bparts = static_cast<const u32x4*>(StagedF32Parts(b, k, n, stream, stage_b));
       const dim3 grid(static_cast<uint32_t>(wtiles), static_cast<uint32_t>(wsplits));
       const bool full = ws.k_per_wg / 4 == 256;
+      const int32_t m32 = static_cast<int32_t>(m), k32 = static_cast<int32_t>(k), n32 = static_cast<int32_t>(n);
+      const int32_t kpw32 = static_cast<int32_t>(ws.k_per_wg);
       if (ws.bparts != nullptr) {
-        if (full) hipLaunchKernelGGL((GemmF32SplitBf16Kernel<8, true>), grid, dim3(kThreads), 0, stream, ws);
-        else hipLaunchKernelGGL((GemmF32SplitBf16Kernel<0, true>), grid, dim3(kThreads), 0, stream, ws);
+        if (full) hipLaunchKernelGGL((GemmF32SplitBf16Kernel<8, true>), grid, dim3(kThreads), 0, stream, ws.a, ws.b,
+                                     ws.bparts, m32, k32, n32, kpw32, ws);
+        else hipLaunchKernelGGL((GemmF32SplitBf16Kernel<0, true>), grid, dim3(kThreads), 0, stream, ws.a, ws.b,
+                                     ws.bparts, m32, k32, n32, kpw32, ws);
       } else {
-        if (full) hipLaunchKernelGGL((GemmF32SplitBf16Kernel<8, false>), grid, dim3(kThreads), 0, stream, ws);
-        else hipLaunchKernelGGL((GemmF32SplitBf16Kernel<0, false>), grid, dim3(kThreads), 0, stream, ws);
+        if (full) hipLaunchKernelGGL((GemmF32SplitBf16Kernel<8, false>), grid, dim3(kThreads), 0, stream, ws.a, ws.b,
+                                     ws.bparts, m32, k32, n32, kpw32, ws);
+        else hipLaunchKernelGGL((GemmF32SplitBf16Kernel<0, false>), grid, dim3(kThreads), 0, stream, ws.a, ws.b,
+                                     ws.bparts, m32, k32, n32, kpw32, ws);
       }
       Check(hipGetLastError(), "GemmF32SplitBf16Kernel launch");
       if (wsplits > 1)
