@@ -329,8 +329,8 @@ constexpr int kMfmaPad = kFlashDim + 4;  // LDS row stride: the 16 key rows fall
 typedef float mv4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashMfmaKernel(
-    const float* q, const float* k, const float* v, float* out, int64_t seq, int64_t position_arg, int64_t heads,
-    int64_t kv_heads, const int32_t* position_dev) {
+    const float* q, const float* k, const float* v, float* out, const int32_t* position_dev, int32_t seq,
+    int32_t position_arg, int32_t heads, int32_t kv_heads) {
   __shared__ __align__(16) float ks[kFlashWaves][kFlashStage][kMfmaPad];
   __shared__ __align__(16) float vs[kFlashWaves][kFlashStage][kMfmaPad];
   __shared__ float part_m[kFlashWaves][kFlashRows];
@@ -938,9 +938,11 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
   if (fast && head_dim == kFlashDim && aligned && (reinterpret_cast<uintptr_t>(q) % 16 == 0) &&
       (reinterpret_cast<uintptr_t>(out) % 16 == 0)) {
     const int64_t qblocks = (seq + kFlashRows - 1) / kFlashRows;
-    if (qblocks > 0x7fffffff || heads > 65535) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
+    if (qblocks > 0x7fffffff || heads > 65535 || seq > 0x7fffffff || position > 0x7fffffff || kv_heads > 65535)
+      Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
     hipLaunchKernelGGL(AttentionFlashMfmaKernel, dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(heads)),
-                       dim3(kFlashWaves * 64), 0, stream, q, k, v, out, seq, position, heads, kv_heads, position_dev);
+                       dim3(kFlashWaves * 64), 0, stream, q, k, v, out, position_dev, static_cast<int32_t>(seq),
+                       static_cast<int32_t>(position), static_cast<int32_t>(heads), static_cast<int32_t>(kv_heads));
     Check(hipGetLastError(), "AttentionFlashMfmaKernel launch");
     return;
   }

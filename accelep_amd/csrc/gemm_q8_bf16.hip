@@ -838,8 +838,21 @@ __global__ void TileBf16x16Kernel(const int8_t* __restrict__ q, int64_t k, int64
 }
 
 // kKbs: k / 32 fixed at compile time (every loop unrolled, constant LDS offsets), or 0 for any k.
+// The pointers and sizes the first loads need lead the arguments (preloaded into SGPRs at wave
+// launch, so the weight and activation loads issue without a kernarg round trip); the output
+// and the epilogue come from `args`, read behind the loads.
 template <int kKbs>
-__global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(SmallArgs p) {
+__global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(const float* a, const u32x4* w16, const float* scale,
+                                                                   int32_t m, int32_t k, int32_t n, int32_t col_groups,
+                                                                   SmallArgs args) {
+  SmallArgs p = args;
+  p.a = a;
+  p.w16 = w16;
+  p.scale = scale;
+  p.m = m;
+  p.k = k;
+  p.n = n;
+  p.col_groups = col_groups;
   static_assert(kKbs >= 0 && kKbs <= kSmallMaxBlocks, "k blocks");
   __shared__ u32x4 parts[(kKbs > 0 ? kKbs : kSmallMaxBlocks) * 3 * 64];
   const int tid = threadIdx.x;
@@ -1045,9 +1058,12 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
     sa.epi = epi;
     const int64_t blocks = (m + 15) / 16 * sa.col_groups;
     const dim3 grid(static_cast<uint32_t>(blocks));
-    if (k == 576) hipLaunchKernelGGL(GemmQ8SmallKernel<18>, grid, dim3(kSmallThreads), 0, stream, sa);
-    else if (k == 768) hipLaunchKernelGGL(GemmQ8SmallKernel<24>, grid, dim3(kSmallThreads), 0, stream, sa);
-    else hipLaunchKernelGGL(GemmQ8SmallKernel<0>, grid, dim3(kSmallThreads), 0, stream, sa);
+    if (k == 576) hipLaunchKernelGGL(GemmQ8SmallKernel<18>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
+                                  sa.m, sa.k, sa.n, sa.col_groups, sa);
+    else if (k == 768) hipLaunchKernelGGL(GemmQ8SmallKernel<24>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
+                                  sa.m, sa.k, sa.n, sa.col_groups, sa);
+    else hipLaunchKernelGGL(GemmQ8SmallKernel<0>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
+                                  sa.m, sa.k, sa.n, sa.col_groups, sa);
     Check(hipGetLastError(), "GemmQ8SmallKernel launch");
     return true;
   }
