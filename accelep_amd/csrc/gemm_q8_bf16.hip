@@ -786,7 +786,8 @@ __global__ void RmsScaleKernel(const float* c, const double* __restrict__ row_ss
 
 // ---- small products: 16-row blocks over all of a short k, no LDS round trip per chunk ------
 // An m > 16 product whose 128-tile grid leaves CUs idle and whose k is short (k <= 768: the
-// Llama prompt's q/k/v, o and gate/up at 512 rows) spends its time in GemmQ8Bf16Kernel's
+// Llama prompt's q/k/v, o and gate/up at 512 rows; k = 1536, its down projection, when the grid
+// fits the CUs in one round) spends its time in GemmQ8Bf16Kernel's
 // per-chunk chain of LDS stores, barrier and LDS reads, and in a split-K reduce launch. Here a
 // workgroup of kSmallWaves waves owns one 16-row block and kSmallWaves 16-column blocks over
 // all of k (no K split):
@@ -803,6 +804,11 @@ constexpr int kSmallThreads = kSmallWaves * 64;
 constexpr int kSmallStages = 6;
 constexpr int64_t kSmallMaxK = 768;
 constexpr int kSmallMaxBlocks = static_cast<int>(kSmallMaxK / kBK);
+// One longer k with an instance of its own (the Llama prompt's down projection): its activation
+// parts take 144 KB of LDS, so one workgroup fills a CU; it is taken only where the grid fits
+// the CUs in one round.
+constexpr int64_t kSmallWideK = 1536;
+constexpr int kSmallWideBlocks = static_cast<int>(kSmallWideK / kBK);
 
 struct SmallArgs {
   const float* a;
@@ -811,7 +817,7 @@ struct SmallArgs {
   int32_t mode;
   int64_t const_index;
   float* c;
-  int32_t m, k, n;     // k % 32 == 0, 32 <= k <= kSmallMaxK
+  int32_t m, k, n;     // k % 32 == 0, 32 <= k <= kSmallMaxK, or k == kSmallWideK
   int32_t col_groups;  // workgroups along n: ceil(ceil(n / 16) / kSmallWaves)
   Epilogue epi;
 };
@@ -853,7 +859,7 @@ __global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(const float* 
   p.k = k;
   p.n = n;
   p.col_groups = col_groups;
-  static_assert(kKbs >= 0 && kKbs <= kSmallMaxBlocks, "k blocks");
+  static_assert(kKbs >= 0 && (kKbs <= kSmallMaxBlocks || kKbs == kSmallWideBlocks), "k blocks");
   __shared__ u32x4 parts[(kKbs > 0 ? kKbs : kSmallMaxBlocks) * 3 * 64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -961,13 +967,19 @@ void LaunchTileBf16x16(const int8_t* q, int64_t k, int64_t n, void* dst, hipStre
 
 bool GemmSmallStageable(int64_t k, int64_t n, const Q8View& v) {
   if (v.q == nullptr || v.zero != nullptr || (v.mode != kScalePerCol && v.mode != kScaleConst)) return false;
-  return k >= kBK && k <= kSmallMaxK && k % kBK == 0 && n >= 8 && n % 8 == 0 && n < (int64_t(1) << 30);
+  return k >= kBK && (k <= kSmallMaxK || k == kSmallWideK) && k % kBK == 0 && n >= 8 && n % 8 == 0 &&
+         n < (int64_t(1) << 30);
 }
 
 bool GemmWantsSmall(int64_t m, int64_t k, int64_t n, const Q8View& v) {
   if (m <= 16 || m >= (int64_t(1) << 30) || !GemmSmallStageable(k, n, v) || GemmWantsBf16Image(m, k, n, v)) return false;
   const int64_t groups = ((n + 15) / 16 + kSmallWaves - 1) / kSmallWaves;
-  return (m + 15) / 16 * groups <= 0x7fffffff;
+  const int64_t blocks = (m + 15) / 16 * groups;
+  if (k == kSmallWideK) {
+    Context& ctx = Ctx();
+    return blocks <= (ctx.cu_count > 0 ? ctx.cu_count : 256);
+  }
+  return blocks <= 0x7fffffff;
 }
 
 bool GemmBf16Stageable(int64_t k, int64_t n, const Q8View& v) {
@@ -1062,6 +1074,9 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
                                   sa.m, sa.k, sa.n, sa.col_groups, sa);
     else if (k == 768) hipLaunchKernelGGL(GemmQ8SmallKernel<24>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
                                   sa.m, sa.k, sa.n, sa.col_groups, sa);
+    else if (k == kSmallWideK)
+      hipLaunchKernelGGL(GemmQ8SmallKernel<kSmallWideBlocks>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16,
+                         sa.scale, sa.m, sa.k, sa.n, sa.col_groups, sa);
     else hipLaunchKernelGGL(GemmQ8SmallKernel<0>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
                                   sa.m, sa.k, sa.n, sa.col_groups, sa);
     Check(hipGetLastError(), "GemmQ8SmallKernel launch");
