@@ -312,6 +312,26 @@ void LaunchGemvQ8(const float* a, const Q8View& b, float* c, int64_t m, int64_t 
 // identity epilogue) runs one wave per tile: an even k <= 1024 over at least 8 tiles per CU. There
 // the norm-after prologue may come with the greedy keys and the advance.
 bool GemvWaveTileApplies(int64_t m, int64_t k, int64_t n);
+// Input transforms of the small int8 GEMM (m > 16, GemmWantsSmall), applied to A as it is split
+// into bf16 parts: the RMSNorm of each row (rms_weight, rms_eps: A = fl(x * w) and each sum times
+// float(1 / rms) at the store, as GemvPrologue::rms_after; fast mode only) or a = fl(x * mul)
+// elementwise (mul: [m, k] like A); and the SiLU of the stored values of columns
+// [0, epi.split[0]) (silu_split0: SiluMulKernel's first half, for a gate/up product whose down
+// projection takes mul = up).
+constexpr int kSmallInNone = 0;
+constexpr int kSmallInRms = 1;
+constexpr int kSmallInMul = 2;
+struct SmallPrologue {
+  const float* rms_weight = nullptr;
+  float rms_eps = 0.f;
+  const float* mul = nullptr;
+  bool silu_split0 = false;
+};
+// The int8-weight GEMM on the small kernel with an input transform (pro may be null): false,
+// with nothing launched, where that kernel does not take the product (b.bf16x16 staged,
+// GemmWantsSmall, A and the transform's operand 16-byte aligned, a column split for the SiLU).
+bool LaunchGemmQ8Small(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
+                       hipStream_t stream, const SmallPrologue* pro);
 // An RMSNormalization of the product's rows (after the epilogue) that a GEMM may take over:
 // out[i, :] = RmsNorm(C[i, :]) with the weight and eps given (SimRmsNorm's arithmetic).
 struct RmsRequest {

@@ -820,6 +820,7 @@ struct SmallArgs {
   int32_t m, k, n;     // k % 32 == 0, 32 <= k <= kSmallMaxK, or k == kSmallWideK
   int32_t col_groups;  // workgroups along n: ceil(ceil(n / 16) / kSmallWaves)
   Epilogue epi;
+  SmallPrologue pro;   // the input transform (the kernel's kIn) and the SiLU store
 };
 
 // One thread per 16-byte lane piece of the staged copy (layout: StagedBf16x16Bytes).
@@ -844,10 +845,15 @@ __global__ void TileBf16x16Kernel(const int8_t* __restrict__ q, int64_t k, int64
 }
 
 // kKbs: k / 32 fixed at compile time (every loop unrolled, constant LDS offsets), or 0 for any k.
+// kIn: the input transform applied to A as it is split (SmallPrologue): kSmallInNone; kSmallInRms,
+// the RMSNorm of each row applied after the product, as the decode GEMV's rms_after does: A =
+// fl(x * w) enters the product and each stored sum is multiplied by float(1 / rms), with rms from
+// the row's double sum of squares formed from the same loads (RmsNormKernel normalizes first and
+// sums in another order, so the fast mode only); kSmallInMul, a = fl(x * mul) elementwise.
 // The pointers and sizes the first loads need lead the arguments (preloaded into SGPRs at wave
 // launch, so the weight and activation loads issue without a kernarg round trip); the output
 // and the epilogue come from `args`, read behind the loads.
-template <int kKbs>
+template <int kKbs, int kIn>
 __global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(const float* a, const u32x4* w16, const float* scale,
                                                                    int32_t m, int32_t k, int32_t n, int32_t col_groups,
                                                                    SmallArgs args) {
@@ -877,16 +883,39 @@ __global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(const float* 
     rw[i] = wp[static_cast<int64_t>(i < kbs ? i : kbs - 1) * 64];
     __builtin_amdgcn_sched_barrier(0);
   }
+  // kSmallInRms: each thread's pieces are all of one row (l % 16 = tid % 16); its share of the
+  // row's double sum of squares, summed over the wave's four lanes of the row, then over the
+  // waves through LDS after the split's barrier.
+  __shared__ double row_ss[kIn == kSmallInRms ? kSmallWaves : 1][16];
+  __shared__ float row_inv[kIn == kSmallInRms ? 16 : 1];
+  double ss = 0.0;
   for (int pc = tid; pc < kbs * 64; pc += kSmallThreads) {
     const int kb = pc >> 6;
     const int l = pc & 63;
     const int row = rb * 16 + (l & 15);
     float x[8];
     if (row < p.m) {
-      const float4* src = reinterpret_cast<const float4*>(p.a + static_cast<int64_t>(row) * p.k + kb * kBK + 8 * (l >> 4));
+      const int64_t at = static_cast<int64_t>(row) * p.k + kb * kBK + 8 * (l >> 4);
+      const float4* src = reinterpret_cast<const float4*>(p.a + at);
       const float4 x0 = src[0], x1 = src[1];
       x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
       x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+      if constexpr (kIn == kSmallInRms) {
+        const float4* wsrc = reinterpret_cast<const float4*>(p.pro.rms_weight + kb * kBK + 8 * (l >> 4));
+        const float4 w0 = wsrc[0], w1 = wsrc[1];
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
+          x[i] = __fmul_rn(x[i], wv[i]);
+        }
+      } else if constexpr (kIn == kSmallInMul) {
+        const float4* usrc = reinterpret_cast<const float4*>(p.pro.mul + at);
+        const float4 u0 = usrc[0], u1 = usrc[1];
+        const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = __fmul_rn(x[i], uv[i]);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) x[i] = 0.f;
@@ -904,10 +933,24 @@ __global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(const float* 
     parts[(kb * 3 + 1) * 64 + l] = mid;
     parts[(kb * 3 + 2) * 64 + l] = lo;
   }
+  if constexpr (kIn == kSmallInRms) {
+    ss += XorLane<16>(ss);
+    ss += XorLane<32>(ss);
+    if (lane < 16) row_ss[wave][lane] = ss;
+  }
   // An LDS-only barrier: the W blocks in flight stay in flight.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if constexpr (kIn == kSmallInRms) {
+    // float(1 / rms) of each row, once: the 16 lanes of the last wave, before its products.
+    if (wave == kSmallWaves - 1 && lane < 16) {
+      double total = row_ss[0][lane];
+#pragma unroll
+      for (int wv = 1; wv < kSmallWaves; ++wv) total += row_ss[wv][lane];
+      row_inv[lane] = static_cast<float>(1.0 / sqrt(total / static_cast<double>(p.k) + static_cast<double>(p.pro.rms_eps)));
+    }
+  }
   v4f acc_hi = v4f{0.f, 0.f, 0.f, 0.f};
   v4f acc_ml = v4f{0.f, 0.f, 0.f, 0.f};
   for (int kb0 = 0; kb0 < kbs; kb0 += kSmallStages) {
@@ -928,16 +971,26 @@ __global__ __launch_bounds__(kSmallThreads) void GemmQ8SmallKernel(const float* 
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if constexpr (kIn == kSmallInRms) LdsBarrier();  // row_inv is written
   if (cb >= cbs) return;
   // Element r of the 16 x 16 tile: row 16 rb + 4 (lane / 16) + r, column 16 cb + lane % 16.
   const int col = cb * 16 + (lane & 15);
   if (col >= p.n) return;
   const float cs = p.scale[p.mode == kScalePerCol ? col : p.const_index];
+  // SmallPrologue::silu_split0: the stored values of columns [0, epi.split[0]) are SiLU(v),
+  // SiluMulKernel's first half.
+  const bool silu = p.pro.silu_split0 && col < p.epi.split[0];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = rb * 16 + 4 * (lane >> 4) + r;
-    if (row < p.m)
-      StoreC(p.c, row, col, p.n, p.epi, ApplyEpilogue(__fmul_rn(acc_hi[r] + acc_ml[r], cs), row, col, p.n, p.epi));
+    if (row < p.m) {
+      float sum = acc_hi[r] + acc_ml[r];
+      // The norm after the product: the sum of fl(x * w) * q times float(1 / rms) of the row.
+      if constexpr (kIn == kSmallInRms) sum = __fmul_rn(sum, row_inv[4 * (lane >> 4) + r]);
+      float v = ApplyEpilogue(__fmul_rn(sum, cs), row, col, p.n, p.epi);
+      if (silu) v = __fdiv_rn(v, __fadd_rn(1.f, expf(-v)));
+      StoreC(p.c, row, col, p.n, p.epi, v);
+    }
   }
 }
 
@@ -992,6 +1045,50 @@ bool GemmWantsBf16Image(int64_t m, int64_t k, int64_t n, const Q8View& v) {
   Context& ctx = Ctx();
   const int64_t cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
   return ((m + 127) / 128) * ((n + 127) / 128) >= cus;  // the 128-tile grid, no K split
+}
+
+bool LaunchGemmQ8Small(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
+                       hipStream_t stream, const SmallPrologue* pro) {
+  if (b.bf16x16 == nullptr || !GemmWantsSmall(m, k, n, b) || reinterpret_cast<uintptr_t>(a) % 16 != 0) return false;
+  const SmallPrologue none{};
+  const SmallPrologue& pr = pro != nullptr ? *pro : none;
+  const int in = pr.rms_weight != nullptr ? kSmallInRms : pr.mul != nullptr ? kSmallInMul : kSmallInNone;
+  const auto aligned = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  if ((in == kSmallInRms && !aligned(pr.rms_weight)) || (in == kSmallInMul && !aligned(pr.mul)) ||
+      (pr.silu_split0 && epi.split[0] <= 0))
+    return false;
+  SmallArgs sa;
+  sa.a = a;
+  sa.w16 = static_cast<const u32x4*>(b.bf16x16);
+  sa.scale = b.scale;
+  sa.mode = b.mode;
+  sa.const_index = b.const_index;
+  sa.c = c;
+  sa.m = static_cast<int32_t>(m);
+  sa.k = static_cast<int32_t>(k);
+  sa.n = static_cast<int32_t>(n);
+  sa.col_groups = static_cast<int32_t>(((n + 15) / 16 + kSmallWaves - 1) / kSmallWaves);
+  sa.epi = epi;
+  sa.pro = pr;
+  const int64_t blocks = (m + 15) / 16 * sa.col_groups;
+  const dim3 grid(static_cast<uint32_t>(blocks));
+#define ACCEL_SMALL_LAUNCH(KB, IN)                                                                              \
+  hipLaunchKernelGGL((GemmQ8SmallKernel<KB, IN>), grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale, \
+                     sa.m, sa.k, sa.n, sa.col_groups, sa)
+#define ACCEL_SMALL_K(IN)                                          \
+  do {                                                             \
+    if (k == 576) ACCEL_SMALL_LAUNCH(18, IN);                      \
+    else if (k == 768) ACCEL_SMALL_LAUNCH(24, IN);                 \
+    else if (k == kSmallWideK) ACCEL_SMALL_LAUNCH(kSmallWideBlocks, IN); \
+    else ACCEL_SMALL_LAUNCH(0, IN);                                \
+  } while (0)
+  if (in == kSmallInRms) ACCEL_SMALL_K(kSmallInRms);
+  else if (in == kSmallInMul) ACCEL_SMALL_K(kSmallInMul);
+  else ACCEL_SMALL_K(kSmallInNone);
+#undef ACCEL_SMALL_K
+#undef ACCEL_SMALL_LAUNCH
+  Check(hipGetLastError(), "GemmQ8SmallKernel launch");
+  return true;
 }
 
 bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int64_t k, int64_t n, const Epilogue& epi,
@@ -1055,33 +1152,7 @@ bool LaunchGemmQ8Bf16(const float* a, const Q8View& b, float* c, int64_t m, int6
       return true;
     }
   }
-  if (b.bf16x16 != nullptr && GemmWantsSmall(m, k, n, b)) {
-    SmallArgs sa;
-    sa.a = a;
-    sa.w16 = static_cast<const u32x4*>(b.bf16x16);
-    sa.scale = b.scale;
-    sa.mode = b.mode;
-    sa.const_index = b.const_index;
-    sa.c = c;
-    sa.m = static_cast<int32_t>(m);
-    sa.k = static_cast<int32_t>(k);
-    sa.n = static_cast<int32_t>(n);
-    sa.col_groups = static_cast<int32_t>(((n + 15) / 16 + kSmallWaves - 1) / kSmallWaves);
-    sa.epi = epi;
-    const int64_t blocks = (m + 15) / 16 * sa.col_groups;
-    const dim3 grid(static_cast<uint32_t>(blocks));
-    if (k == 576) hipLaunchKernelGGL(GemmQ8SmallKernel<18>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
-                                  sa.m, sa.k, sa.n, sa.col_groups, sa);
-    else if (k == 768) hipLaunchKernelGGL(GemmQ8SmallKernel<24>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
-                                  sa.m, sa.k, sa.n, sa.col_groups, sa);
-    else if (k == kSmallWideK)
-      hipLaunchKernelGGL(GemmQ8SmallKernel<kSmallWideBlocks>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16,
-                         sa.scale, sa.m, sa.k, sa.n, sa.col_groups, sa);
-    else hipLaunchKernelGGL(GemmQ8SmallKernel<0>, grid, dim3(kSmallThreads), 0, stream, sa.a, sa.w16, sa.scale,
-                                  sa.m, sa.k, sa.n, sa.col_groups, sa);
-    Check(hipGetLastError(), "GemmQ8SmallKernel launch");
-    return true;
-  }
+  if (LaunchGemmQ8Small(a, b, c, m, k, n, epi, stream, nullptr)) return true;
   Context& ctx0 = Ctx();
   const int64_t cus = ctx0.cu_count > 0 ? ctx0.cu_count : 256;
   // 128 x 128 tiles when they give one per CU, else 64 x 64.

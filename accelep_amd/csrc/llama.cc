@@ -273,9 +273,31 @@ struct Model {
       ApplyPrologue(w, x, c, e, pro);
       return;
     }
+    Q8View sv;
+    if (SmallFusable(w, m, sv)) {
+      SmallPrologue pro;
+      pro.rms_weight = norm.as<float>();
+      pro.rms_eps = cfg.eps;
+      pro.silu_split0 = silu_split0;
+      if (LaunchGemmQ8Small(x, sv, c, m, w.in, w.out, e, stream(), &pro)) return;
+    }
+    if (silu_split0) Fail(ACCEL_HIP_RUNTIME_ERROR, "SiLU store planned for a product that cannot take it");
     LaunchRmsNormRows(x, norm.as<float>(), normed.as<float>(), m, cfg.hidden, cfg.eps, stream());
     if (norm_mark >= 0) Mark(norm_mark);
     Apply(w, normed.as<float>(), c, m, e);
+  }
+  // A prompt's product (m > 16) on the small int8 GEMM, which can take the row's RMSNorm, the
+  // multiply by up and the SiLU store as it splits A (fuse bit 1, fast mode; the staged copy is
+  // built here on first use).
+  bool SmallFusable(const Linear& w, int64_t m, Q8View& v) const {
+    if ((fuse & 1) == 0 || m <= 16 || w.q.empty() || Ctx().exact_products) return false;
+    v.q = w.q.as<int8_t>();
+    v.scale = w.scale.as<float>();
+    v.mode = kScalePerCol;
+    v.cached = cached_loads;
+    if (!GemmWantsSmall(m, w.in, w.out, v)) return false;
+    v.bf16x16 = StagedBf16x16(v.q, w.in, w.out, Ctx().stream);
+    return v.bf16x16 != nullptr;
   }
   // c = (SiLU(gate) * up) @ W: one kernel for a decode row, else SiLU*up in place first. With
   // silu_done the gate already holds SiLU(gate) (SiluFold) and the GEMV multiplies by up.
@@ -288,13 +310,28 @@ struct Model {
       ApplyPrologue(w, g, c, e, pro);
       return;
     }
+    if (silu_done) {
+      Q8View sv;
+      SmallPrologue pro;
+      pro.mul = u;
+      if (!SmallFusable(w, m, sv) || !LaunchGemmQ8Small(g, sv, c, m, w.in, w.out, e, stream(), &pro))
+        Fail(ACCEL_HIP_RUNTIME_ERROR, "SiLU store planned for a down projection that cannot multiply by up");
+      return;
+    }
     LaunchSiluMul(g, u, m * cfg.intermediate, stream());
     Apply(w, g, c, m, e);
   }
   // A decode row's SiLU(gate) * up in two halves: the gate/up GEMV stores SiLU(gate) for its
   // gate columns (one expf per gate value) and the down GEMV multiplies by up, the same
   // operations as SiluMulKernel's, instead of every down workgroup forming SiLU per lane.
+  // A prompt (m > 16) folds the same way when both products run on the small GEMM.
   bool SiluFold(const LayerWeights& l, int64_t m) const {
+    if (m > 16) {
+      Q8View gv, dv;
+      const auto aligned = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+      return SmallFusable(l.gu, m, gv) && SmallFusable(l.down, m, dv) && aligned(hidden.as<float>()) &&
+             aligned(l.post_norm.as<float>()) && aligned(gate.as<float>()) && aligned(up.as<float>());
+    }
     return Fusable(l.gu, m) && l.gu.out <= kFusedNormMaxOut && l.gu.in % 2 == 0 && Fusable(l.down, m) &&
            l.down.in % 2 == 0;
   }
