@@ -144,6 +144,29 @@ def test_llama_full_size_matches_reference():
         eng.close()
 
 
+def test_llama_full_size_prompt_in_parts_matches_reference():
+    """The 512-id prompt fed in three parts (200, 137 and 175 ids, the later ones at positions
+    200 and 337 against the cache): the prompt attention's key spans then start at a nonzero
+    position and cross the parts' boundary. The last row's logits within the gate of the
+    reference's prefill row."""
+    gold = _full_golden()
+    case = llama_full_case()
+    eng = Engine(case["config"], case["weights"], case["quant"])
+    try:
+        prompt = np.ascontiguousarray(case["prompt"], np.int32)
+        for lo, hi in ((0, 200), (200, 337), (337, prompt.size)):
+            part = np.ascontiguousarray(prompt[lo:hi])
+            assert eng.L.accel_llama_forward_ids(eng.h, part.ctypes.data_as(I32P), part.size, int(lo == 0)) == 0, \
+                eng.L.accel_llama_last_error()
+        row = np.zeros(case["config"]["vocab"], np.float32)
+        assert eng.L.accel_llama_logits(eng.h, row.ctypes.data_as(F32P), row.size) == 0
+        worst = float(np.abs(row.astype(np.float64) - gold["prefill_logits"]).max())
+        print(f"prompt in three parts: logits max|diff| = {worst:.3g}", flush=True)
+        assert worst <= LOGIT_TOL
+    finally:
+        eng.close()
+
+
 def test_llama_full_size_sampled_matches_reference():
     """The same model with top-k sampling (temperature 0.8, top 40, seed 11): 128 ids that do
     not settle on a fixed point, so every decode position and KV row takes part. The ids must
