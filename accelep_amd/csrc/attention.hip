@@ -290,14 +290,14 @@ __global__ __launch_bounds__(64) void AttentionCombineKernel(const float* partia
 
 
 // ---- prompt rows, head_dim 64, fast mode: online softmax over key stages ------------------
-// One workgroup per (16 query rows, head); its four waves take a quarter of the keys each and
-// the quarters are combined at the end. Each wave stages 16 keys of K and V in its own LDS
-// slice (coalesced loads; the next stage's loads are issued while the current one is
-// multiplied), so K and V are read once per 16 query rows instead of once per row. The
+// One workgroup per (16 query rows, head), in a 1D grid; its eight waves take an eighth of
+// the keys each and the eighths are combined at the end. Each wave stages 16 keys of K and V
+// in its own LDS slice (coalesced loads; the next stage's loads are issued while the current
+// one is multiplied), so K and V are read once per 16 query rows instead of once per row. The
 // summation order differs from the reference's sequential loops (rounding only), so this
 // path serves the fast mode; the per-row kernel above keeps the reference's score bits.
 constexpr int kFlashRows = 16;
-constexpr int kFlashWaves = 4;
+constexpr int kFlashWaves = 8;
 constexpr int kFlashStage = 16;  // keys per LDS stage
 constexpr int kFlashDim = 64;
 
@@ -341,8 +341,13 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashMfmaKernel(
   const int wave = tid >> 6;
   const int j = lane & 15;  // query row of the block
   const int g = lane >> 4;  // key group / dim group
-  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * kFlashRows;
-  const int64_t h = blockIdx.y;
+  // Heaviest row blocks first, over all heads: the workgroups beyond one per CU are then the
+  // blocks with the fewest keys, and no two long blocks share a CU.
+  const int32_t unit = static_cast<int32_t>(blockIdx.x);
+  const int32_t qblocks = static_cast<int32_t>(gridDim.x) / heads;
+  const int32_t rank = unit / heads;
+  const int64_t s0 = static_cast<int64_t>(qblocks - 1 - rank) * kFlashRows;
+  const int64_t h = unit - rank * heads;
   const int64_t kv = h / (heads / kv_heads);
   const int64_t row = s0 + j;
   const bool live = row < seq;
@@ -435,7 +440,7 @@ __global__ __launch_bounds__(kFlashWaves * 64) void AttentionFlashMfmaKernel(
     __builtin_amdgcn_wave_barrier();  // the stage is read before the next one overwrites it
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  // Row j's sum over the four key groups; then the quarters meet in LDS. acc_o[t][r] is
+  // Row j's sum over the four key groups; then the waves' eighths meet in LDS. acc_o[t][r] is
   // O^T[dim 16 t + 4 g + r][row j]; the wave's stage rows hold its 16 x 64 block.
   l = l + XorLane<16>(l);
   l = l + XorLane<32>(l);
@@ -940,7 +945,8 @@ void LaunchAttention(const float* q, const float* k, const float* v, float* out,
     const int64_t qblocks = (seq + kFlashRows - 1) / kFlashRows;
     if (qblocks > 0x7fffffff || heads > 65535 || seq > 0x7fffffff || position > 0x7fffffff || kv_heads > 65535)
       Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
-    hipLaunchKernelGGL(AttentionFlashMfmaKernel, dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(heads)),
+    if (qblocks * heads > 0x7fffffff) Fail(ACCEL_HIP_INVALID_ARGUMENT, "Attention is too large");
+    hipLaunchKernelGGL(AttentionFlashMfmaKernel, dim3(static_cast<uint32_t>(qblocks * heads)),
                        dim3(kFlashWaves * 64), 0, stream, q, k, v, out, position_dev, static_cast<int32_t>(seq),
                        static_cast<int32_t>(position), static_cast<int32_t>(heads), static_cast<int32_t>(kv_heads));
     Check(hipGetLastError(), "AttentionFlashMfmaKernel launch");
